@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark: Piper Attention forward on one MI355X (gfx950).
+
+Workload (the headline shape): B1 H24 S16384 D128 fp16,
+non-causal, synthetic seeded inputs already resident in HBM.  One *step* is one complete
+operator call: the HIP prep pipeline (K/V means, INT8 Q/K/V quantisation) followed by the
+fused INT8-MFMA attention kernel -- exactly what ``piper_attention`` runs.
+
+Prints ONE JSON line.  ``value`` = whole-call TOPS (reference op count 4*B*H*Sq*Skv*D per
+call, benchmarks/benchmark_attention.py:184-193).  ``roofline`` prices the dominant
+kernel (the fused attention kernel) against MI355X's dense INT8 MFMA peak, with its
+average duration measured by HIP events recorded on the launch stream inside the timed
+region.  ``cpu_baseline`` times the CPU oracle (a numpy restatement of the reference's
+portable path) on a bounded slice of the same workload, on one host thread.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path[:0] = [str(REPO), str(REPO / "piper-kernels_amd")]
+
+INT8_PEAK_TOPS = 5033.2  # MI355X dense INT8 MFMA: 256 CU x 2.4 GHz x 8192 ops/clk/CU
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    return parser.parse_args()
+
+
+def traffic_from_profile(workload: str):
+    """HBM bytes per attention launch measured by rocprofv3 --pmc (committed summary), if any."""
+    path = REPO / "profiles" / f"attention_{workload}_hbm_traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text())["bytes_per_launch"]
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(workload, seconds: float) -> dict:
+    """Time the CPU oracle (prep of one head + the streaming loop over a row slice)."""
+    import platform
+
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import piper_oracle as oracle
+    from piper_kernels.measure import attention_operations
+    from piper_kernels.workloads import make_inputs
+
+    q, k, v = make_inputs(workload, heads=[0], batches=[0])
+    scale = workload.head_dim**-0.5
+    with threadpool_limits(limits=1):
+        # calibrate on a small slice, then size the timed slice to ~`seconds`
+        prep = oracle.prepare(q, k, v, workload.is_causal, "per_thread")
+        rows = 64
+
+        def run(rows: int) -> float:
+            sub = dict(prep)
+            for key in ("query_code", "query_scale"):
+                sub[key] = prep[key][:, :, :rows]
+            start = time.perf_counter()
+            oracle.attention_from_prepared(sub, scale, workload.is_causal)
+            return time.perf_counter() - start
+
+        per_row = run(rows) / rows
+        rows = int(max(64, min(workload.query_length, seconds / max(per_row, 1e-9))))
+        start = time.perf_counter()
+        prep = oracle.prepare(q, k, v, workload.is_causal, "per_thread")
+        prep_s = time.perf_counter() - start
+        loop_s = run(rows)
+    total = prep_s + loop_s
+    ops = attention_operations(1, 1, rows, workload.key_length, workload.head_dim, workload.is_causal)
+    return {
+        "value": ops / total / 1e12,
+        "unit": "TOPS",
+        "cores": 1,
+        "kind": "port",
+        "sample": (
+            f"{workload.name} batch 0 head 0: prep of the full head (S={workload.key_length}) + "
+            f"the 64-key streaming loop for {rows} of {workload.query_length} query rows; "
+            f"{total:.1f} s wall; numpy {np.__version__}, 1 BLAS thread; "
+            f"cpu={platform.processor() or platform.machine()} os.cpu_count={os.cpu_count()}"
+        ),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on exactly one GPU (asked for --gpus {args.gpus}); this build has no "
+            "multi-GPU path -- see DESIGN.md for how the operator would shard.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from piper_kernels.attention.piper_attention.hip import _launch_piper_attention, _prepare_piper_attention
+    from piper_kernels.measure import attention_operations, prep_algorithmic_bytes
+    from piper_kernels.workloads import WORKLOADS, make_inputs
+
+    workload = WORKLOADS[args.workload]
+    device = torch.device("cuda", 0)
+    log(f"[bench] generating {workload.description}")
+    q, k, v = make_inputs(workload, device)
+    scale = workload.head_dim**-0.5
+    b, h, sq, sk, d = workload.shape
+    ops = attention_operations(b, h, sq, sk, d, workload.is_causal)
+
+    def step(events=None):
+        if events is not None:
+            events[0].record()
+        prepared = _prepare_piper_attention(q, k, v, scale, workload.is_causal)
+        if events is not None:
+            events[1].record()
+        out = _launch_piper_attention(prepared)
+        if events is not None:
+            events[2].record()
+        return out
+
+    with torch.no_grad():
+        log(f"[bench] warmup {args.warmup}")
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        log(f"[bench] timing {args.steps} steps")
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for i in range(args.steps):
+            step(events[i])
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    prep_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
+    attn_ms = sorted(e[1].elapsed_time(e[2]) for e in events)
+    attn_mean = sum(attn_ms) / len(attn_ms)
+    prep_mean = sum(prep_ms) / len(prep_ms)
+    attn_tops = ops / (attn_mean * 1e-3) / 1e12
+    prep_bytes = prep_algorithmic_bytes(b, h, sq, sk, d, workload.is_causal)
+    value = ops / (ms_per_step * 1e-3) / 1e12
+    log(f"[bench] step {ms_per_step:.4f} ms ({value:.1f} TOPS); attention {attn_mean:.4f} ms "
+        f"({attn_tops:.1f} TOPS, {100 * attn_tops / INT8_PEAK_TOPS:.1f}% of INT8 peak); prep {prep_mean:.4f} ms")
+
+    result = {
+        "metric": "attention TOPS + % INT8 MFMA peak, B1 H24 S16k D128 fp16, 1 MI355X",
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded numpy PCG64 per head, fp16 inputs resident in HBM)",
+        "config": {
+            **workload.as_dict(),
+            "step": "complete operator call: HIP prep + fused attention kernel",
+            "plan": None,
+        },
+        "percent_of_int8_peak": round(100 * value / INT8_PEAK_TOPS, 2),
+        "attention_kernel": {
+            "ms_mean": round(attn_mean, 5),
+            "ms_p20_p50_p80": [round(attn_ms[int(f * (len(attn_ms) - 1))], 5) for f in (0.2, 0.5, 0.8)],
+            "tops": round(attn_tops, 2),
+            "percent_of_int8_peak": round(100 * attn_tops / INT8_PEAK_TOPS, 2),
+        },
+        "prep": {
+            "ms_mean": round(prep_mean, 5),
+            "algorithmic_bytes": prep_bytes,
+            "gbps": round(prep_bytes / (prep_mean * 1e-3) / 1e9, 1),
+            "percent_of_hbm_peak": round(100 * prep_bytes / (prep_mean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(attn_tops, 2),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TOPS",
+            "frac": round(attn_tops / INT8_PEAK_TOPS, 4),
+            "traffic": traffic_from_profile(workload.name),
+        },
+        "cpu_baseline": None,
+    }
+    from piper_kernels.attention.piper_attention._plan import select_plan
+
+    result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(workload, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,168 @@
+/*
+ * piper_mi355x.h -- C ABI of the MI355X (gfx950) Piper Attention forward backend.
+ *
+ * The library exports plain extern "C" functions over POD structs: raw device pointers,
+ * element strides and sizes, a HIP stream handle passed as void*, and an int status.
+ * It never allocates or frees device memory and never synchronises the stream: the caller
+ * (the Python host layer on PyTorch-ROCm) owns every buffer for the stream-ordered
+ * lifetime of the launches.
+ *
+ * Reference interfaces these entry points replace (jumbledpoophj/piper-kernels 0.2.1):
+ *   piper_prepare            <- _prepare_piper_attention
+ *                               src/piper_kernels/attention/piper_attention/triton.py:772-890
+ *                               (K/V means triton.py:638-699, Q/K quantisation
+ *                               attention/kernels/qk_quantization/int8/sage/triton.py:238-356,
+ *                               per-key V quantisation triton.py:176-246 / :839-860)
+ *   piper_attention_forward  <- _launch_piper_attention
+ *                               src/piper_kernels/attention/piper_attention/triton.py:893-951
+ *                               (fused kernel _piper_attention_kernel triton.py:303-635)
+ *   piper_prepared_layout    <- the buffer allocations of _prepare_piper_attention
+ *                               (triton.py:797-874); the sizes the caller must provide
+ *   piper_abi_version,
+ *   piper_last_error         <- no reference counterpart: version handshake and the error
+ *                               text the Python layer raises as RuntimeError
+ *
+ * Status codes: 0 on success; otherwise one of piper_status and piper_last_error()
+ * returns a thread-local, NUL-terminated description.
+ */
+#ifndef PIPER_MI355X_H
+#define PIPER_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PIPER_ABI_VERSION 1
+
+/* Rows per quantisation group (sage/reference.py:6-7) and keys per P block (reference.py:16). */
+#define PIPER_QUERY_BLOCK 32
+#define PIPER_KEY_BLOCK 64
+/* Rows per FP64 partial sum of the order-defined K/V sequence mean. */
+#define PIPER_MEAN_CHUNK 64
+
+typedef enum piper_dtype {
+  PIPER_FLOAT16 = 0,
+  PIPER_BFLOAT16 = 1,
+  PIPER_FLOAT32 = 2 /* attention output only: the FP32 result before the cast */
+} piper_dtype;
+
+typedef enum piper_status {
+  PIPER_OK = 0,
+  PIPER_ERROR_INVALID_ARGUMENT = 1,
+  PIPER_ERROR_UNSUPPORTED = 2,
+  PIPER_ERROR_HIP = 3
+} piper_status;
+
+typedef struct piper_shape {
+  int64_t batch;
+  int64_t heads;
+  int64_t query_length;
+  int64_t key_length;
+  int64_t head_dim; /* 64 or 128 */
+} piper_shape;
+
+/* A [batch, heads, sequence, head_dim] input: element strides of the first three axes;
+ * the head_dim axis must be contiguous (stride 1), as _validation.py:34-35 requires. */
+typedef struct piper_tensor {
+  const void* data;
+  int64_t stride_batch;
+  int64_t stride_head;
+  int64_t stride_seq;
+} piper_tensor;
+
+/*
+ * The prepared (quantised) operands, produced by piper_prepare and consumed by
+ * piper_attention_forward.  With Sq32 = ceil(Sq/32)*32, Sk64 = ceil(Sk/64)*64,
+ * nqb = Sq32/32 and nkb = Sk64/64, all arrays are dense and row-major:
+ *
+ *   query_code         int8    [B, H, Sq32, D]       Q codes, padded rows zero
+ *   query_scale        float   [B, H, nqb]           amax/127 + 1e-7 per 32-row block
+ *   key_code           int8    [B, H, Sk64, D]       codes of K - mean(K), padded rows zero
+ *   key_scale          float   [B, H, nkb]           per 64-row block
+ *   value_code         int8    [B, H, nkb, D, 64]    per-key codes of V - mean(V), stored
+ *                                                    transposed per 64-key tile (V^T tiles);
+ *                                                    padded keys zero
+ *   value_scale        float   [B, H, Sk64]          amax_D/127 + 1e-7 per key (padding 0)
+ *   value_log2_scale   float   [B, H, Sk64]          log2(value_scale) (padding -inf)
+ *   value_inv_multiplier float [B, H, Sk64]          1/(255*value_scale) (padding 0)
+ *   value_correction   int32   [B, H, nkb, D]        128 * sum over the tile's 64 keys of
+ *                                                    value_code (affine PV correction)
+ *   key_mean           float   [B, H, D]             order-defined sequence mean of K
+ *   value_mean         float   [B, H, D]             same for V; zeros when causal
+ */
+typedef struct piper_prepared {
+  int8_t* query_code;
+  float* query_scale;
+  int8_t* key_code;
+  float* key_scale;
+  int8_t* value_code;
+  float* value_scale;
+  float* value_log2_scale;
+  float* value_inv_multiplier;
+  int32_t* value_correction;
+  float* key_mean;
+  float* value_mean;
+} piper_prepared;
+
+/* Byte sizes of every caller-allocated buffer for a shape. */
+typedef struct piper_layout {
+  int64_t query_code_bytes;
+  int64_t query_scale_bytes;
+  int64_t key_code_bytes;
+  int64_t key_scale_bytes;
+  int64_t value_code_bytes;
+  int64_t value_key_array_bytes; /* each of value_scale, value_log2_scale, value_inv_multiplier */
+  int64_t value_correction_bytes;
+  int64_t mean_bytes; /* each of key_mean, value_mean */
+  int64_t workspace_bytes; /* scratch for piper_prepare (FP64 mean partials) */
+} piper_layout;
+
+typedef struct piper_prepare_args {
+  int32_t abi_version; /* PIPER_ABI_VERSION */
+  int32_t dtype;       /* PIPER_FLOAT16 or PIPER_BFLOAT16: dtype of query, key and value */
+  int32_t is_causal;   /* causal calls leave V uncentred (value_mean = 0) */
+  int32_t reserved;
+  piper_shape shape;
+  piper_tensor query;
+  piper_tensor key;
+  piper_tensor value;
+  piper_prepared prepared; /* outputs */
+  void* workspace;
+  int64_t workspace_bytes;
+} piper_prepare_args;
+
+typedef struct piper_attention_args {
+  int32_t abi_version;  /* PIPER_ABI_VERSION */
+  int32_t output_dtype; /* PIPER_FLOAT16, PIPER_BFLOAT16 or PIPER_FLOAT32 */
+  int32_t is_causal;
+  int32_t plan;         /* 0 = default MI355X launch plan */
+  piper_shape shape;
+  float scale;          /* softmax scale, finite and > 0 */
+  int32_t reserved;
+  piper_prepared prepared; /* inputs, as written by piper_prepare */
+  void* output;            /* [B, H, Sq, D] dense row-major, output_dtype */
+} piper_attention_args;
+
+int piper_abi_version(void);
+
+/* Fill *layout with the buffer sizes piper_prepare / piper_attention_forward expect. */
+int piper_prepared_layout(const piper_shape* shape, piper_layout* layout);
+
+/* Quantise Q, K, V into args->prepared on `stream` (a hipStream_t; NULL = default stream).
+ * Launches: FP64 mean partials, mean finalisation, one quantisation kernel. */
+int piper_prepare(const piper_prepare_args* args, void* stream);
+
+/* Fused INT8-QK / UINT8-P x INT8-V online-softmax attention on `stream`. */
+int piper_attention_forward(const piper_attention_args* args, void* stream);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* piper_last_error(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* PIPER_MI355X_H */

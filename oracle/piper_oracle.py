@@ -1,0 +1,352 @@
+"""CPU oracle for Piper Attention's forward pass (numpy restatement).
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker: it may be imported by
+``tests/``, by ``__graft_entry__.smoke()`` and by the ``cpu_baseline`` leg of
+``bench.py``, and by nothing else.  The product path (the ``piper_kernels``
+package and its HIP library) never imports, calls or links it.
+
+It restates, in numpy, the portable PyTorch reference of
+``jumbledpoophj/piper-kernels`` 0.2.1:
+
+* ``src/piper_kernels/attention/piper_attention/reference.py:22-118``
+  (per-key V quantisation and the streaming UINT8-P / INT8-V recurrence);
+* ``src/piper_kernels/attention/kernels/qk_quantization/int8/sage/reference.py:13-108``
+  (K smoothing and INT8 Q/K quantisation, ``per_thread`` and ``per_warp``).
+
+One deliberate, documented deviation: the sequence means of K and V.  The
+reference uses ``torch.mean`` in FP32 (``reference.py:50``,
+``sage/reference.py:89``) whose summation order is internal to torch and not
+reproducible on a GPU.  This oracle pins an order-defined mean instead
+(:func:`sequence_mean`), which the HIP prep kernel reproduces bit for bit.
+For FP16 inputs this definition equals the correctly rounded exact mean
+whenever ``S * max|x| < 2**29`` (every FP16 value is a multiple of 2**-24, so
+every FP64 partial sum is exact).
+
+Parity status of each function (how it is pinned; see tests/test_oracle.py):
+
+* ``sequence_mean`` -- pinned against exact rational arithmetic
+  (``fractions.Fraction``) on FP16 inputs.
+* ``quantize_per_group`` / ``quantize_*_per_thread`` / ``quantize_value_per_key``
+  -- pinned by a pure-Python IEEE re-derivation on small inputs, the
+  reference's own dequantisation bound (``tests/attention/test_qk_quantization.py:26-33``)
+  and hand-written interleave tables for ``per_thread``.
+* ``piper_attention_reference`` -- pinned by an independent FP64
+  non-streaming restatement (``oracle/fp64_check.py``), closed forms for
+  single-key and zero-query inputs, constant-V exactness, causal future
+  independence and the reference's SDPA envelope.  Bit-level parity of the
+  FP32 output with torch is *unpinned* (torch's exp/log/sum order), as it is
+  for every non-torch implementation; outputs are compared by tolerance.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+QUERY_BLOCK = 32  # sage/reference.py:6
+KEY_BLOCK = 64  # sage/reference.py:7
+PV_BLOCK = 64  # reference.py:16
+MEAN_CHUNK = 64  # rows per FP64 partial sum in the pinned mean definition
+INT8_RANGE = np.float32(127.0)  # sage/reference.py quantization_range / reference.py:18
+P_UINT8_RANGE = np.float32(255.0)  # reference.py:17
+SCALE_EPSILON = np.float32(1e-7)  # reference.py:19, sage/reference.py:8
+DENOMINATOR_FLOOR = np.float32(1e-30)  # reference.py:116
+
+GRANULARITIES = ("per_thread", "per_warp")
+
+
+# --------------------------------------------------------------------------------------
+# dtype plumbing
+# --------------------------------------------------------------------------------------
+def as_float32(x) -> np.ndarray:
+    """Widen an fp16/bf16/fp32 array (numpy or torch) to a numpy float32 array, exactly."""
+    if hasattr(x, "detach"):  # torch tensor: bf16 has no numpy dtype, widen in torch
+        return x.detach().float().cpu().numpy()
+    return np.asarray(x).astype(np.float32)
+
+
+def round_to_bfloat16_bits(x32: np.ndarray) -> np.ndarray:
+    """Round float32 to bfloat16 (round to nearest even), returned as uint16 bit patterns."""
+    bits = np.ascontiguousarray(x32, dtype=np.float32).view(np.uint32)
+    nan = np.isnan(x32)
+    rounding_bias = ((bits >> 16) & 1) + np.uint32(0x7FFF)
+    rounded = ((bits + rounding_bias) >> 16).astype(np.uint16)
+    rounded[nan] = np.uint16(0x7FC0)
+    return rounded
+
+
+def bfloat16_bits_to_float32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def cast_output(out32: np.ndarray, dtype: str) -> np.ndarray:
+    """Cast the FP32 result to the input dtype (reference.py:118), returned as float32 values.
+
+    ``dtype`` is ``"float16"`` or ``"bfloat16"``.  Both casts round to nearest even.
+    """
+    if dtype == "float16":
+        return out32.astype(np.float16).astype(np.float32)
+    if dtype == "bfloat16":
+        return bfloat16_bits_to_float32(round_to_bfloat16_bits(out32))
+    raise ValueError(f"unsupported dtype {dtype}")
+
+
+# --------------------------------------------------------------------------------------
+# sequence mean (pinned definition)
+# --------------------------------------------------------------------------------------
+def sequence_mean(x32: np.ndarray, chunk: int = MEAN_CHUNK) -> np.ndarray:
+    """Mean over the sequence axis of ``[B, H, S, D]`` float32 data, order-defined.
+
+    Definition (the HIP prep kernel computes exactly this):
+
+    1. the S rows are cut into chunks of ``chunk`` consecutive rows (the last may be short);
+    2. each chunk's FP64 partial starts at +0.0 and adds its rows in increasing order;
+    3. the total starts at +0.0 and adds the chunk partials in increasing chunk order;
+    4. ``mean = float32(total / S)`` with the division in FP64 (both roundings are to
+       nearest even).
+
+    Replaces the FP32 ``mean(dim=2)`` of ``reference.py:50`` and ``sage/reference.py:89``.
+    """
+    batch, heads, length, width = x32.shape
+    total = np.zeros((batch, heads, width), dtype=np.float64)
+    for start in range(0, length, chunk):
+        partial = np.zeros((batch, heads, width), dtype=np.float64)
+        for row in range(start, min(start + chunk, length)):
+            partial += x32[:, :, row, :].astype(np.float64)
+        total += partial
+    return (total / np.float64(length)).astype(np.float32)
+
+
+# --------------------------------------------------------------------------------------
+# INT8 quantisers
+# --------------------------------------------------------------------------------------
+def _scale_from_amax(amax: np.ndarray, quantization_range: np.float32 = INT8_RANGE) -> np.ndarray:
+    """``amax / range + 1e-7`` in FP32: IEEE division, then an FP32 add (sage/reference.py:68)."""
+    amax = np.asarray(amax, dtype=np.float32)
+    return (amax / np.float32(quantization_range)) + SCALE_EPSILON
+
+
+def _codes(x32: np.ndarray, scale: np.ndarray, quantization_range=INT8_RANGE) -> np.ndarray:
+    """``clamp(round_half_even(x / scale), -range, range)`` as int8 (sage/reference.py:70-75)."""
+    quotient = x32 / scale
+    r = np.float32(quantization_range)
+    return np.clip(np.rint(quotient), -r, r).astype(np.int8)
+
+
+def _pad_rows(x32: np.ndarray, multiple: int) -> tuple[np.ndarray, int]:
+    """Zero-pad the sequence axis to a multiple (sage/reference.py:13-20)."""
+    length = x32.shape[2]
+    padded_length = -(-length // multiple) * multiple
+    if padded_length == length:
+        return x32, length
+    padded = np.zeros(x32.shape[:2] + (padded_length, x32.shape[3]), dtype=np.float32)
+    padded[:, :, :length] = x32
+    return padded, length
+
+
+def quantize_per_group(x32: np.ndarray, group: int, quantization_range=INT8_RANGE):
+    """One scale per ``group`` consecutive rows (sage/reference.py:61-77).
+
+    Returns ``(codes int8 [B,H,S,D], block_scale float32 [B,H,ceil(S/group)])``.
+    """
+    padded, length = _pad_rows(np.asarray(x32, dtype=np.float32), group)
+    batch, heads, padded_length, width = padded.shape
+    grouped = padded.reshape(batch, heads, padded_length // group, group * width)
+    scale = _scale_from_amax(np.abs(grouped).max(axis=-1), quantization_range)
+    codes = _codes(grouped, scale[..., None], quantization_range)
+    return codes.reshape(batch, heads, padded_length, width)[:, :, :length], scale
+
+
+def quantize_query_per_thread(q32: np.ndarray, quantization_range=INT8_RANGE):
+    """Four interleaved query rows {t, t+8, t+16, t+24} share a scale (sage/reference.py:23-39).
+
+    Returns ``(codes [B,H,S,D], per-row scale [B,H,S])``.
+    """
+    padded, length = _pad_rows(np.asarray(q32, dtype=np.float32), QUERY_BLOCK)
+    batch, heads, padded_length, width = padded.shape
+    # row = 32*block + 8*i + t  ->  axes (block, i, t, d); the scale group is (block, t)
+    grouped = padded.reshape(batch, heads, padded_length // QUERY_BLOCK, 4, 8, width)
+    group_scale = _scale_from_amax(np.abs(grouped).max(axis=(3, 5)), quantization_range)
+    row_scale = np.broadcast_to(group_scale[:, :, :, None, :, None], grouped.shape)
+    codes = _codes(grouped, row_scale, quantization_range).reshape(padded.shape)
+    per_row = np.broadcast_to(group_scale[:, :, :, None, :], group_scale.shape[:3] + (4, 8))
+    per_row = per_row.reshape(batch, heads, padded_length)
+    return codes[:, :, :length], np.ascontiguousarray(per_row[:, :, :length])
+
+
+def quantize_key_per_thread(k32: np.ndarray, quantization_range=INT8_RANGE):
+    """Sixteen interleaved key rows {8a + 2t + c} share a scale (sage/reference.py:42-58).
+
+    Returns ``(codes [B,H,S,D], per-row scale [B,H,S])``.
+    """
+    padded, length = _pad_rows(np.asarray(k32, dtype=np.float32), KEY_BLOCK)
+    batch, heads, padded_length, width = padded.shape
+    # row = 64*block + 8*a + 2*t + c -> axes (block, a, t, c, d); the scale group is (block, t)
+    grouped = padded.reshape(batch, heads, padded_length // KEY_BLOCK, 8, 4, 2, width)
+    group_scale = _scale_from_amax(np.abs(grouped).max(axis=(3, 5, 6)), quantization_range)
+    row_scale = np.broadcast_to(group_scale[:, :, :, None, :, None, None], grouped.shape)
+    codes = _codes(grouped, row_scale, quantization_range).reshape(padded.shape)
+    per_row = np.broadcast_to(
+        group_scale[:, :, :, None, :, None], group_scale.shape[:3] + (8, 4, 2)
+    ).reshape(batch, heads, padded_length)
+    return codes[:, :, :length], np.ascontiguousarray(per_row[:, :, :length])
+
+
+def center_key(k32: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """``K - mean_S(K)`` in FP32 with the pinned mean (sage/reference.py:88-89)."""
+    mean = sequence_mean(k32)
+    return k32 - mean[:, :, None, :], mean
+
+
+def quantize_query_key(q32: np.ndarray, k32: np.ndarray, granularity: str):
+    """Centre K and quantise Q/K (sage/reference.py:80-108).
+
+    Returns a dict with codes, per-row scales (as the reference returns them) and, for
+    ``per_warp``, the per-block scales the HIP prep kernel stores.
+    """
+    if granularity not in GRANULARITIES:
+        raise ValueError(f"unknown Q/K quantization granularity: {granularity}")
+    key_centered, key_mean = center_key(k32)
+    result = {"key_mean": key_mean}
+    if granularity == "per_warp":
+        q_codes, q_block_scale = quantize_per_group(q32, QUERY_BLOCK)
+        k_codes, k_block_scale = quantize_per_group(key_centered, KEY_BLOCK)
+        result.update(
+            query_code=q_codes,
+            key_code=k_codes,
+            query_block_scale=q_block_scale,
+            key_block_scale=k_block_scale,
+            query_scale=np.repeat(q_block_scale, QUERY_BLOCK, axis=2)[:, :, : q32.shape[2]],
+            key_scale=np.repeat(k_block_scale, KEY_BLOCK, axis=2)[:, :, : k32.shape[2]],
+        )
+    else:
+        q_codes, q_scale = quantize_query_per_thread(q32)
+        k_codes, k_scale = quantize_key_per_thread(key_centered)
+        result.update(query_code=q_codes, key_code=k_codes, query_scale=q_scale, key_scale=k_scale)
+    return result
+
+
+def quantize_value_per_key(v_centered32: np.ndarray):
+    """One signed-INT8 scale per V row (reference.py:22-32).
+
+    Returns ``(codes int8 [B,H,S,D], scale float32 [B,H,S])``.
+    """
+    scale = _scale_from_amax(np.abs(v_centered32).max(axis=-1))
+    return _codes(v_centered32, scale[..., None]), scale
+
+
+def prepare(q, k, v, is_causal: bool, granularity: str = "per_warp") -> dict:
+    """Everything the reference derives before its key loop (reference.py:45-59)."""
+    q32, k32, v32 = as_float32(q), as_float32(k), as_float32(v)
+    if is_causal:
+        value_mean = np.zeros((v32.shape[0], v32.shape[1], v32.shape[3]), dtype=np.float32)
+    else:
+        value_mean = sequence_mean(v32)
+    value_centered = v32 - value_mean[:, :, None, :]
+    prepared = quantize_query_key(q32, k32, granularity)
+    v_codes, v_scale = quantize_value_per_key(value_centered)
+    prepared.update(value_code=v_codes, value_scale=v_scale, value_mean=value_mean)
+    return prepared
+
+
+# --------------------------------------------------------------------------------------
+# streaming recurrence
+# --------------------------------------------------------------------------------------
+def attention_from_prepared(
+    prepared: dict, scale: float, is_causal: bool, query_offset: int = 0
+) -> np.ndarray:
+    """The 64-key streaming loop and epilogue of reference.py:61-117, in FP32.
+
+    Rows are independent, so ``prepared`` may hold a contiguous subset of the query rows
+    (codes and per-row scales sliced alike); ``query_offset`` is the absolute position of
+    its first row, used by the causal mask.
+
+    Integer products are computed with FP32 matmuls, which are exact here: every partial
+    sum is an integer of magnitude below 2**24 (|QK| <= 128*127**2, |PV| <= 64*255*127).
+    Returns the FP32 output before the cast to the input dtype.
+    """
+    q_code = prepared["query_code"]
+    k_code = prepared["key_code"]
+    v_code = prepared["value_code"]
+    q_scale = prepared["query_scale"].astype(np.float32)
+    k_scale = prepared["key_scale"].astype(np.float32)
+    v_scale = prepared["value_scale"].astype(np.float32)
+    v_mean = prepared["value_mean"]
+    batch, heads, query_length, width = q_code.shape
+    key_length = k_code.shape[2]
+    scale32 = np.float32(scale)
+    out = np.empty((batch, heads, query_length, width), dtype=np.float32)
+    query_positions = np.arange(query_length) + query_offset
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        for b in range(batch):
+            for h in range(heads):
+                qf = q_code[b, h].astype(np.float32)
+                numerator = np.zeros((query_length, width), dtype=np.float32)
+                denominator = np.zeros(query_length, dtype=np.float32)
+                running_max = np.full(query_length, -np.inf, dtype=np.float32)
+                for start in range(0, key_length, PV_BLOCK):
+                    stop = min(start + PV_BLOCK, key_length)
+                    integer_scores = qf @ k_code[b, h, start:stop].astype(np.float32).T
+                    scores = (
+                        integer_scores
+                        * q_scale[b, h, :, None]
+                        * k_scale[b, h, None, start:stop]
+                        * scale32
+                    )
+                    if is_causal:
+                        future = np.arange(start, stop)[None, :] > query_positions[:, None]
+                        scores = np.where(future, np.float32(-np.inf), scores)
+                    block_v_scale = v_scale[b, h, start:stop]
+                    shifted = scores + np.log(block_v_scale)[None, :]
+                    block_max = shifted.max(axis=-1)
+                    next_max = np.maximum(running_max, block_max)
+                    old_weight = np.exp(running_max - next_max)
+                    current_weight = np.exp(block_max - next_max)
+                    probabilities = np.nan_to_num(np.exp(scores - block_max[:, None]))
+                    numerator *= old_weight[:, None]
+                    denominator = denominator * old_weight + probabilities.sum(axis=-1) * current_weight
+                    p_codes = np.clip(
+                        np.rint(probabilities * block_v_scale[None, :] * P_UINT8_RANGE),
+                        np.float32(0.0),
+                        P_UINT8_RANGE,
+                    )
+                    partial = p_codes @ v_code[b, h, start:stop].astype(np.float32)
+                    numerator += partial * (current_weight / P_UINT8_RANGE)[:, None]
+                    running_max = next_max
+                result = numerator / np.maximum(denominator, DENOMINATOR_FLOOR)[:, None]
+                result += v_mean[b, h][None, :]
+                out[b, h] = result
+    return out
+
+
+def piper_attention_reference(
+    q, k, v, scale: float | None = None, is_causal: bool = False, granularity: str = "per_thread"
+) -> np.ndarray:
+    """Full quantised reference (reference.py:35-118). Returns the FP32 pre-cast output.
+
+    ``granularity`` defaults to ``per_thread`` like ``reference.py:42``; the HIP backend
+    quantises per block, which is ``per_warp`` here.
+    """
+    width = q.shape[-1]
+    scale = width**-0.5 if scale is None else float(scale)
+    prepared = prepare(q, k, v, is_causal, granularity)
+    return attention_from_prepared(prepared, scale, is_causal)
+
+
+# --------------------------------------------------------------------------------------
+# full-precision quality reference
+# --------------------------------------------------------------------------------------
+def sdpa_float64(q, k, v, scale: float | None = None, is_causal: bool = False) -> np.ndarray:
+    """Exact softmax attention in FP64 (the full-precision quality reference)."""
+    q64 = as_float32(q).astype(np.float64)
+    k64 = as_float32(k).astype(np.float64)
+    v64 = as_float32(v).astype(np.float64)
+    scale = q64.shape[-1] ** -0.5 if scale is None else float(scale)
+    logits = np.einsum("bhqd,bhkd->bhqk", q64, k64) * scale
+    if is_causal:
+        sq, sk = logits.shape[-2:]
+        logits = np.where(np.arange(sk)[None, :] > np.arange(sq)[:, None], -np.inf, logits)
+    logits -= logits.max(axis=-1, keepdims=True)
+    weights = np.exp(logits)
+    weights /= weights.sum(axis=-1, keepdims=True)
+    return np.einsum("bhqk,bhkd->bhqd", weights, v64)
+

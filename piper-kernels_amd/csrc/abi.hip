@@ -1,0 +1,220 @@
+// extern "C" entry points of libpiper_mi355x.so (declared in include/piper_mi355x.h).
+//
+// Validation, launch geometry and error reporting only: the library never allocates,
+// frees or synchronises; every buffer belongs to the caller.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kernels.h"
+#include "piper_mi355x.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, args);
+  va_end(args);
+  return status;
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+int check_shape(const piper_shape* s) {
+  if (s == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "shape is NULL");
+  if (s->batch <= 0 || s->heads <= 0 || s->query_length <= 0 || s->key_length <= 0)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "dimensions must be positive, got B=%lld H=%lld Sq=%lld Sk=%lld",
+                (long long)s->batch, (long long)s->heads, (long long)s->query_length, (long long)s->key_length);
+  if (s->head_dim != 64 && s->head_dim != 128)
+    return fail(PIPER_ERROR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld", (long long)s->head_dim);
+  // 32-bit index arithmetic inside the kernels: keep every per-call count well inside int.
+  const int64_t bh = s->batch * s->heads;
+  const int64_t longest = s->query_length > s->key_length ? s->query_length : s->key_length;
+  if (bh > (1 << 24) || longest > (1 << 26) || bh * ceil_div(longest, 32) > (int64_t(1) << 30))
+    return fail(PIPER_ERROR_UNSUPPORTED, "shape too large for this build");
+  return PIPER_OK;
+}
+
+int check_input(const char* name, const piper_tensor& t) {
+  if (t.data == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "%s pointer is NULL", name);
+  if (!aligned16(t.data) || (t.stride_batch % 8) != 0 || (t.stride_head % 8) != 0 || (t.stride_seq % 8) != 0)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT,
+                "%s must be 16-byte aligned with batch/head/sequence strides that are multiples of 8 elements",
+                name);
+  return PIPER_OK;
+}
+
+piper::InputTensor to_input(const piper_tensor& t) {
+  return piper::InputTensor{t.data, static_cast<long>(t.stride_batch), static_cast<long>(t.stride_head),
+                            static_cast<long>(t.stride_seq)};
+}
+
+}  // namespace
+
+extern "C" {
+
+int piper_abi_version(void) { return PIPER_ABI_VERSION; }
+
+const char* piper_last_error(void) { return g_last_error; }
+
+int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
+  if (int st = check_shape(shape)) return st;
+  if (layout == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "layout is NULL");
+  const int64_t bh = shape->batch * shape->heads;
+  const int64_t d = shape->head_dim;
+  const int64_t sq32 = ceil_div(shape->query_length, PIPER_QUERY_BLOCK) * PIPER_QUERY_BLOCK;
+  const int64_t sk64 = ceil_div(shape->key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK;
+  const int64_t chunks = ceil_div(shape->key_length, PIPER_MEAN_CHUNK);
+  layout->query_code_bytes = bh * sq32 * d;
+  layout->query_scale_bytes = bh * (sq32 / PIPER_QUERY_BLOCK) * 4;
+  layout->key_code_bytes = bh * sk64 * d;
+  layout->key_scale_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * 4;
+  layout->value_code_bytes = bh * sk64 * d;
+  layout->value_key_array_bytes = bh * sk64 * 4;
+  layout->value_correction_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * d * 4;
+  layout->mean_bytes = bh * d * 4;
+  layout->workspace_bytes = 2 * bh * chunks * d * 8;
+  g_last_error[0] = '\0';
+  return PIPER_OK;
+}
+
+int piper_prepare(const piper_prepare_args* a, void* stream) {
+  if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != PIPER_ABI_VERSION)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", a->abi_version,
+                PIPER_ABI_VERSION);
+  if (a->dtype != PIPER_FLOAT16 && a->dtype != PIPER_BFLOAT16)
+    return fail(PIPER_ERROR_UNSUPPORTED, "input dtype must be float16 or bfloat16");
+  if (int st = check_shape(&a->shape)) return st;
+  if (a->is_causal && a->shape.query_length != a->shape.key_length)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
+  if (int st = check_input("query", a->query)) return st;
+  if (int st = check_input("key", a->key)) return st;
+  if (int st = check_input("value", a->value)) return st;
+  const piper_prepared& o = a->prepared;
+  if (!o.query_code || !o.query_scale || !o.key_code || !o.key_scale || !o.value_code || !o.value_scale ||
+      !o.value_log2_scale || !o.value_inv_multiplier || !o.value_correction || !o.key_mean || !o.value_mean)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared output pointer is NULL");
+  if (!aligned16(o.query_code) || !aligned16(o.key_code) || !aligned16(o.value_code) ||
+      !aligned16(o.value_log2_scale) || !aligned16(o.value_inv_multiplier) || !aligned16(o.value_correction) ||
+      !aligned16(o.value_mean))
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte aligned");
+  piper_layout layout;
+  if (int st = piper_prepared_layout(&a->shape, &layout)) return st;
+  if (a->workspace == nullptr || a->workspace_bytes < layout.workspace_bytes)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "workspace needs %lld bytes, got %lld",
+                (long long)layout.workspace_bytes, (long long)a->workspace_bytes);
+
+  const piper_shape& s = a->shape;
+  const int bh = static_cast<int>(s.batch * s.heads);
+  const int d = static_cast<int>(s.head_dim);
+  const int sq32 = static_cast<int>(ceil_div(s.query_length, PIPER_QUERY_BLOCK) * PIPER_QUERY_BLOCK);
+  const int sk64 = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK);
+
+  piper::MeanParams mp{};
+  mp.key = to_input(a->key);
+  mp.value = to_input(a->value);
+  mp.partials = static_cast<double*>(a->workspace);
+  mp.key_mean = o.key_mean;
+  mp.value_mean = o.value_mean;
+  mp.batch_heads = bh;
+  mp.heads = static_cast<int>(s.heads);
+  mp.length = static_cast<int>(s.key_length);
+  mp.chunks = static_cast<int>(ceil_div(s.key_length, PIPER_MEAN_CHUNK));
+  mp.tensors = a->is_causal ? 1 : 2;
+
+  piper::QuantParams qp{};
+  qp.query = to_input(a->query);
+  qp.key = to_input(a->key);
+  qp.value = to_input(a->value);
+  qp.batch_heads = bh;
+  qp.heads = static_cast<int>(s.heads);
+  qp.query_length = static_cast<int>(s.query_length);
+  qp.key_length = static_cast<int>(s.key_length);
+  qp.sq32 = sq32;
+  qp.sk64 = sk64;
+  qp.nqb = sq32 / PIPER_QUERY_BLOCK;
+  qp.nkb = sk64 / PIPER_KEY_BLOCK;
+  qp.q_blocks_wg = static_cast<int>(ceil_div(static_cast<int64_t>(bh) * qp.nqb, 4));
+  qp.k_blocks_wg = static_cast<int>(ceil_div(static_cast<int64_t>(bh) * qp.nkb, 4));
+  qp.v_blocks_wg = qp.k_blocks_wg;
+  qp.center_value = a->is_causal ? 0 : 1;
+  qp.key_mean = o.key_mean;
+  qp.value_mean = o.value_mean;
+  qp.query_code = o.query_code;
+  qp.query_scale = o.query_scale;
+  qp.key_code = o.key_code;
+  qp.key_scale = o.key_scale;
+  qp.value_code = o.value_code;
+  qp.value_scale = o.value_scale;
+  qp.value_log2_scale = o.value_log2_scale;
+  qp.value_inv_multiplier = o.value_inv_multiplier;
+  qp.value_correction = o.value_correction;
+
+  const hipError_t err = piper::launch_prep(a->dtype == PIPER_BFLOAT16, d, mp, qp, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "prep launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return PIPER_OK;
+}
+
+int piper_attention_forward(const piper_attention_args* a, void* stream) {
+  if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != PIPER_ABI_VERSION)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", a->abi_version,
+                PIPER_ABI_VERSION);
+  if (a->output_dtype != PIPER_FLOAT16 && a->output_dtype != PIPER_BFLOAT16 && a->output_dtype != PIPER_FLOAT32)
+    return fail(PIPER_ERROR_UNSUPPORTED, "output dtype must be float16, bfloat16 or float32");
+  if (int st = check_shape(&a->shape)) return st;
+  if (a->is_causal && a->shape.query_length != a->shape.key_length)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
+  if (!(std::isfinite(a->scale) && a->scale > 0.0f))
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
+  if (a->plan < 0 || a->plan > 1) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
+  const piper_prepared& o = a->prepared;
+  if (!o.query_code || !o.query_scale || !o.key_code || !o.key_scale || !o.value_code || !o.value_log2_scale ||
+      !o.value_inv_multiplier || !o.value_correction || !o.value_mean || !a->output)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared input or the output pointer is NULL");
+  if (!aligned16(o.query_code) || !aligned16(o.key_code) || !aligned16(o.value_code) ||
+      !aligned16(o.value_log2_scale) || !aligned16(o.value_inv_multiplier) || !aligned16(o.value_correction) ||
+      !aligned16(o.value_mean) || (reinterpret_cast<uintptr_t>(a->output) & 7u) != 0)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
+
+  const piper_shape& s = a->shape;
+  const int waves = a->plan == 1 ? 4 : 8;
+  piper::AttnParams ap{};
+  ap.query_code = o.query_code;
+  ap.query_scale = o.query_scale;
+  ap.key_code = o.key_code;
+  ap.key_scale = o.key_scale;
+  ap.value_code = o.value_code;
+  ap.value_log2_scale = o.value_log2_scale;
+  ap.value_inv_multiplier = o.value_inv_multiplier;
+  ap.value_correction = o.value_correction;
+  ap.value_mean = o.value_mean;
+  ap.output = a->output;
+  ap.batch_heads = static_cast<int>(s.batch * s.heads);
+  ap.query_length = static_cast<int>(s.query_length);
+  ap.key_length = static_cast<int>(s.key_length);
+  ap.sq32 = static_cast<int>(ceil_div(s.query_length, PIPER_QUERY_BLOCK) * PIPER_QUERY_BLOCK);
+  ap.sk64 = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK);
+  ap.nqb = ap.sq32 / PIPER_QUERY_BLOCK;
+  ap.nkb = ap.sk64 / PIPER_KEY_BLOCK;
+  ap.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * waves));
+  ap.scale_log2e = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
+  if (static_cast<int64_t>(ap.query_tiles) * ap.batch_heads > 0x7fffffff)
+    return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
+
+  const hipError_t err = piper::launch_attention(static_cast<int>(s.head_dim), a->is_causal != 0, a->output_dtype,
+                                                 waves, ap, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "attention launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return PIPER_OK;
+}
+
+}  // extern "C"

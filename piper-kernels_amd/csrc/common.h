@@ -1,0 +1,73 @@
+// Shared device helpers for the gfx950 Piper Attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace piper {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+constexpr int kQueryBlock = 32;  // rows per Q scale (sage/reference.py:6)
+constexpr int kKeyBlock = 64;    // rows per K scale and keys per P block (reference.py:16)
+constexpr int kMeanChunk = 64;   // rows per FP64 partial of the order-defined mean
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+// Exact widening of 8 packed 16-bit floats (one 16-byte load) to float.
+template <bool kBf16>
+__device__ __forceinline__ void widen8(const uint4 raw, float (&out)[8]) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (kBf16) {
+      out[2 * i] = __uint_as_float(w[i] << 16);
+      out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    } else {
+      out[2 * i] = half_bits_to_float(w[i] & 0xffffu);
+      out[2 * i + 1] = half_bits_to_float(w[i] >> 16);
+    }
+  }
+}
+
+// Round-to-nearest-even narrowing of float to the 16-bit output formats.
+__device__ __forceinline__ uint32_t float_to_half_bits(float x) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x)));
+}
+
+__device__ __forceinline__ uint32_t float_to_bf16_bits(float x) {
+  const uint32_t bits = __float_as_uint(x);
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN
+  return (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+}
+
+// Max / sum of a value over the two 32-lane halves of a wave (lane l and l ^ 32).
+__device__ __forceinline__ float cross_half_max(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float cross_half_sum(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Remap the
+// hardware block id so that consecutive logical ids -- the query blocks of one head, which
+// stream the same K/V tiles -- run on the same XCD.
+__device__ __forceinline__ int xcd_remap(int block, int blocks) {
+  const int xcd = block & 7;
+  const int local = block >> 3;
+  const int base = blocks >> 3;
+  const int rem = blocks & 7;
+  return xcd * base + (xcd < rem ? xcd : rem) + local;
+}
+
+}  // namespace piper

@@ -1,0 +1,308 @@
+// Prep kernels: order-defined K/V sequence means, per-block INT8 Q/K and per-key INT8 V.
+//
+// Behaviour follows the reference's portable algorithm (jumbledpoophj/piper-kernels 0.2.1):
+//   K smoothing and per-block ("per_warp") Q/K codes  sage/reference.py:61-108
+//   V centring (non-causal only) and per-key V codes   piper_attention/reference.py:22-59
+// Every code and scale is bit-exact with that arithmetic: scale = amax/127 + 1e-7 in FP32
+// (IEEE division, FP32 add), code = clamp(round_half_even(x / scale), -127, 127) with an IEEE
+// division per element.  The means use the order-defined FP64 definition documented in the
+// C header (chunks of 64 rows summed in order, chunk partials summed in order, FP64 divide,
+// round to FP32).
+#include "common.h"
+#include "kernels.h"
+
+namespace piper {
+
+// ---------------------------------------------------------------------------------------
+// Means, pass 1: one thread owns 8 columns of one 64-row chunk of K (tensor 0) or V
+// (tensor 1) and adds the chunk's rows in order into FP64 accumulators that start at +0.0.
+// ---------------------------------------------------------------------------------------
+template <bool kBf16, int D>
+__global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
+  constexpr int kGroups = D / 8;  // 16-byte column groups per row
+  const long gid = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long per_tensor = static_cast<long>(p.batch_heads) * p.chunks * kGroups;
+  if (gid >= per_tensor * p.tensors) return;
+  const int tensor = static_cast<int>(gid / per_tensor);
+  const long rem = gid - tensor * per_tensor;
+  const int group = static_cast<int>(rem % kGroups);
+  const int chunk = static_cast<int>((rem / kGroups) % p.chunks);
+  const int bh = static_cast<int>(rem / (static_cast<long>(kGroups) * p.chunks));
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+
+  const InputTensor& t = tensor == 0 ? p.key : p.value;
+  const uint16_t* base = static_cast<const uint16_t*>(t.data) + b * t.stride_batch +
+                         h * t.stride_head + group * 8;
+  const int row0 = chunk * kMeanChunk;
+  const int row1 = min(row0 + kMeanChunk, p.length);
+
+  double acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0;
+  int row = row0;
+  for (; row + 8 <= row1; row += 8) {  // 8 loads in flight, adds still in row order
+    uint4 raw[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      raw[u] = *reinterpret_cast<const uint4*>(base + static_cast<long>(row + u) * t.stride_seq);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      float f[8];
+      widen8<kBf16>(raw[u], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += static_cast<double>(f[i]);
+    }
+  }
+  for (; row < row1; ++row) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * t.stride_seq);
+    float f[8];
+    widen8<kBf16>(raw, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += static_cast<double>(f[i]);
+  }
+  double* out = p.partials + ((static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks + chunk) * D +
+                group * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = acc[i];
+}
+
+// Means, pass 2: sum the chunk partials of one (tensor, batch-head, column) in chunk order,
+// divide by the length in FP64 and round to FP32.  Causal calls write a zero V mean.
+__global__ void __launch_bounds__(256) mean_finalize_kernel(const MeanParams p, int head_dim) {
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int per_tensor = p.batch_heads * head_dim;
+  if (gid >= 2 * per_tensor) return;
+  const int tensor = gid / per_tensor;
+  const int rem = gid - tensor * per_tensor;
+  float* dst = tensor == 0 ? p.key_mean : p.value_mean;
+  if (tensor >= p.tensors) {
+    dst[rem] = 0.0f;
+    return;
+  }
+  const int bh = rem / head_dim;
+  const int d = rem - bh * head_dim;
+  const double* src = p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks * head_dim + d;
+  double total = 0.0;
+  for (int c = 0; c < p.chunks; ++c) total += src[static_cast<long>(c) * head_dim];
+  dst[rem] = static_cast<float>(total / static_cast<double>(p.length));
+}
+
+// ---------------------------------------------------------------------------------------
+// Quantisation.  Each wave owns one unit: a 32-row Q block, a 64-row K block or a 64-key V
+// tile.  A workgroup (4 waves) holds units of one kind only, so V workgroups can use
+// workgroup barriers around their LDS transpose.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+template <int kLanes>
+__device__ __forceinline__ float group_max(float v) {  // max over aligned groups of kLanes lanes
+#pragma unroll
+  for (int m = kLanes / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+__device__ __forceinline__ float scale_from_amax(float amax) {
+  // amax / 127 + 1e-7: correctly rounded FP32 division, then an FP32 add (no contraction).
+  const float q = amax / 127.0f;
+  return __fadd_rn(q, 1e-7f);
+}
+
+__device__ __forceinline__ int code_of(float x, float scale) {
+  const float r = __builtin_rintf(x / scale);  // IEEE division, round half to even
+  return static_cast<int>(fminf(fmaxf(r, -127.0f), 127.0f));
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+         ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
+// Q or K block of kRows rows: one scale over kRows x D values.
+template <bool kBf16, int D, int kRows, bool kCenter>
+__device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int h, int row0, int length,
+                                               const float* __restrict__ mean, int8_t* __restrict__ codes,
+                                               float* __restrict__ scale_out) {
+  constexpr int kGroups = D / 8;
+  constexpr int kRowsPerIter = kWave / kGroups;
+  constexpr int kIters = kRows / kRowsPerIter;
+  const int lane = threadIdx.x & 63;
+  const int group = lane % kGroups;
+  const int sub = lane / kGroups;
+  const uint16_t* base = static_cast<const uint16_t*>(in.data) + b * in.stride_batch + h * in.stride_head +
+                         group * 8;
+  float mu[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mu[i] = kCenter ? mean[group * 8 + i] : 0.0f;
+
+  uint4 raw[kIters];
+  float amax = 0.0f;
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int row = row0 + it * kRowsPerIter + sub;
+    raw[it] = row < length ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * in.stride_seq)
+                           : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int row = row0 + it * kRowsPerIter + sub;
+    float f[8];
+    widen8<kBf16>(raw[it], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // padded rows are zero after centring (sage/reference.py:13-20 pads the centred K)
+      const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
+      amax = fmaxf(amax, fabsf(x));
+    }
+  }
+  amax = wave_max(amax);
+  const float scale = scale_from_amax(amax);
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int row = row0 + it * kRowsPerIter + sub;
+    float f[8];
+    widen8<kBf16>(raw[it], f);
+    int c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
+      c[i] = code_of(x, scale);
+    }
+    uint2 packed = make_uint2(pack4(c[0], c[1], c[2], c[3]), pack4(c[4], c[5], c[6], c[7]));
+    *reinterpret_cast<uint2*>(codes + static_cast<long>(it * kRowsPerIter + sub) * D + group * 8) = packed;
+  }
+  if (lane == 0) *scale_out = scale;
+}
+
+template <bool kBf16, int D>
+__global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
+  constexpr int kVStride = kKeyBlock + 16;  // LDS row stride of a V^T tile (bytes)
+  __shared__ __attribute__((aligned(16))) int8_t vt_lds[4][D * kVStride];
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int block = blockIdx.x;
+
+  if (block < p.q_blocks_wg) {
+    const int unit = block * 4 + wave;
+    if (unit >= p.batch_heads * p.nqb) return;
+    const int bh = unit / p.nqb;
+    const int qb = unit - bh * p.nqb;
+    const int b = bh / p.heads;
+    const int h = bh - b * p.heads;
+    quantize_block<kBf16, D, kQueryBlock, false>(
+        p.query, b, h, qb * kQueryBlock, p.query_length, nullptr,
+        p.query_code + (static_cast<long>(bh) * p.sq32 + qb * kQueryBlock) * D, p.query_scale + unit);
+    return;
+  }
+  if (block < p.q_blocks_wg + p.k_blocks_wg) {
+    const int unit = (block - p.q_blocks_wg) * 4 + wave;
+    if (unit >= p.batch_heads * p.nkb) return;
+    const int bh = unit / p.nkb;
+    const int kb = unit - bh * p.nkb;
+    const int b = bh / p.heads;
+    const int h = bh - b * p.heads;
+    quantize_block<kBf16, D, kKeyBlock, true>(
+        p.key, b, h, kb * kKeyBlock, p.key_length, p.key_mean + static_cast<long>(bh) * D,
+        p.key_code + (static_cast<long>(bh) * p.sk64 + kb * kKeyBlock) * D, p.key_scale + unit);
+    return;
+  }
+
+  // ---- V tile: per-key scales, codes transposed through LDS, tile column sums ----
+  const int unit = (block - p.q_blocks_wg - p.k_blocks_wg) * 4 + wave;
+  const bool active = unit < p.batch_heads * p.nkb;
+  int8_t* lds = vt_lds[wave];
+  int bh = 0, kb = 0;
+  if (active) {
+    bh = unit / p.nkb;
+    kb = unit - bh * p.nkb;
+    const int b = bh / p.heads;
+    const int h = bh - b * p.heads;
+    constexpr int kGroups = D / 8;
+    constexpr int kRowsPerIter = kWave / kGroups;
+    constexpr int kIters = kKeyBlock / kRowsPerIter;
+    const int group = lane % kGroups;
+    const int sub = lane / kGroups;
+    const uint16_t* base = static_cast<const uint16_t*>(p.value.data) + b * p.value.stride_batch +
+                           h * p.value.stride_head + group * 8;
+    float mu[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mu[i] = p.center_value ? p.value_mean[static_cast<long>(bh) * D + group * 8 + i] : 0.0f;
+#pragma unroll 4
+    for (int it = 0; it < kIters; ++it) {
+      const int key_in_tile = it * kRowsPerIter + sub;
+      const int row = kb * kKeyBlock + key_in_tile;
+      const bool valid = row < p.key_length;
+      const uint4 raw = valid ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
+                              : make_uint4(0, 0, 0, 0);
+      float f[8];
+      widen8<kBf16>(raw, f);
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        f[i] = valid ? f[i] - mu[i] : 0.0f;
+        amax = fmaxf(amax, fabsf(f[i]));
+      }
+      amax = group_max<kGroups>(amax);
+      const float scale = scale_from_amax(amax);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<int8_t>(code_of(f[i], scale));
+      if (group == 0) {
+        const long k = static_cast<long>(bh) * p.sk64 + row;
+        p.value_scale[k] = valid ? scale : 0.0f;
+        p.value_log2_scale[k] = valid ? log2f(scale) : -__builtin_inff();
+        p.value_inv_multiplier[k] = valid ? 1.0f / (255.0f * scale) : 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  // transposed rows: lane owns features d = lane, lane + 64, ...
+  for (int d = lane; d < D; d += kWave) {
+    const uint4* src = reinterpret_cast<const uint4*>(lds + d * kVStride);
+    uint4* dst = reinterpret_cast<uint4*>(p.value_code + ((static_cast<long>(bh) * p.nkb + kb) * D + d) * kKeyBlock);
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 w = src[j];
+      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.x), 0x01010101, sum, false);
+      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.y), 0x01010101, sum, false);
+      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.z), 0x01010101, sum, false);
+      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.w), 0x01010101, sum, false);
+      dst[j] = w;
+    }
+    p.value_correction[(static_cast<long>(bh) * p.nkb + kb) * D + d] = 128 * sum;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------------------
+template <bool kBf16, int D>
+static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {
+  const long mean_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 8) * mp.tensors;
+  hipLaunchKernelGGL((mean_partial_kernel<kBf16, D>), dim3(static_cast<unsigned>((mean_threads + 255) / 256)),
+                     dim3(256), 0, stream, mp);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int fin_threads = 2 * mp.batch_heads * D;
+  hipLaunchKernelGGL(mean_finalize_kernel, dim3((fin_threads + 255) / 256), dim3(256), 0, stream, mp, D);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int blocks = qp.q_blocks_wg + qp.k_blocks_wg + qp.v_blocks_wg;
+  hipLaunchKernelGGL((quantize_kernel<kBf16, D>), dim3(blocks), dim3(256), 0, stream, qp);
+  return hipGetLastError();
+}
+
+hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {
+  if (bf16) {
+    return head_dim == 128 ? launch_prep_typed<true, 128>(mp, qp, stream) : launch_prep_typed<true, 64>(mp, qp, stream);
+  }
+  return head_dim == 128 ? launch_prep_typed<false, 128>(mp, qp, stream) : launch_prep_typed<false, 64>(mp, qp, stream);
+}
+
+}  // namespace piper

@@ -1,0 +1,196 @@
+"""ctypes binding of ``libpiper_mi355x.so`` (C ABI in ``include/piper_mi355x.h``).
+
+The structures below mirror the header field for field.  torch is imported before the
+library is opened: torch ships its own HIP runtime with the same SONAME
+(``libamdhip64.so.7``), and the library must bind to that instance so that torch's
+stream handles and allocations are valid inside it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime first; see module docstring)
+
+from .build import LIBRARY_PATH
+
+ABI_VERSION = 1
+QUERY_BLOCK = 32
+KEY_BLOCK = 64
+MEAN_CHUNK = 64
+
+FLOAT16 = 0
+BFLOAT16 = 1
+FLOAT32 = 2
+
+EXPORTED_SYMBOLS = (
+    "piper_abi_version",
+    "piper_prepared_layout",
+    "piper_prepare",
+    "piper_attention_forward",
+    "piper_last_error",
+)
+
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_ptr = ctypes.c_void_p
+
+
+class PiperShape(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64),
+        ("heads", _i64),
+        ("query_length", _i64),
+        ("key_length", _i64),
+        ("head_dim", _i64),
+    ]
+
+
+class PiperTensor(ctypes.Structure):
+    _fields_ = [("data", _ptr), ("stride_batch", _i64), ("stride_head", _i64), ("stride_seq", _i64)]
+
+
+class PiperPrepared(ctypes.Structure):
+    _fields_ = [
+        ("query_code", _ptr),
+        ("query_scale", _ptr),
+        ("key_code", _ptr),
+        ("key_scale", _ptr),
+        ("value_code", _ptr),
+        ("value_scale", _ptr),
+        ("value_log2_scale", _ptr),
+        ("value_inv_multiplier", _ptr),
+        ("value_correction", _ptr),
+        ("key_mean", _ptr),
+        ("value_mean", _ptr),
+    ]
+
+
+class PiperLayout(ctypes.Structure):
+    _fields_ = [
+        ("query_code_bytes", _i64),
+        ("query_scale_bytes", _i64),
+        ("key_code_bytes", _i64),
+        ("key_scale_bytes", _i64),
+        ("value_code_bytes", _i64),
+        ("value_key_array_bytes", _i64),
+        ("value_correction_bytes", _i64),
+        ("mean_bytes", _i64),
+        ("workspace_bytes", _i64),
+    ]
+
+
+class PiperPrepareArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("dtype", _i32),
+        ("is_causal", _i32),
+        ("reserved", _i32),
+        ("shape", PiperShape),
+        ("query", PiperTensor),
+        ("key", PiperTensor),
+        ("value", PiperTensor),
+        ("prepared", PiperPrepared),
+        ("workspace", _ptr),
+        ("workspace_bytes", _i64),
+    ]
+
+
+class PiperAttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("output_dtype", _i32),
+        ("is_causal", _i32),
+        ("plan", _i32),
+        ("shape", PiperShape),
+        ("scale", ctypes.c_float),
+        ("reserved", _i32),
+        ("prepared", PiperPrepared),
+        ("output", _ptr),
+    ]
+
+
+class LibraryUnavailableError(RuntimeError):
+    """The gfx950 HIP library is not built or cannot be opened."""
+
+
+class NativeLibrary:
+    """Typed wrapper over the exported C functions; non-zero status raises RuntimeError."""
+
+    def __init__(self, path: Path) -> None:
+        self.path = Path(path)
+        self._lib = ctypes.CDLL(str(self.path))
+        lib = self._lib
+        lib.piper_abi_version.argtypes = []
+        lib.piper_abi_version.restype = ctypes.c_int
+        lib.piper_last_error.argtypes = []
+        lib.piper_last_error.restype = ctypes.c_char_p
+        lib.piper_prepared_layout.argtypes = [ctypes.POINTER(PiperShape), ctypes.POINTER(PiperLayout)]
+        lib.piper_prepared_layout.restype = ctypes.c_int
+        lib.piper_prepare.argtypes = [ctypes.POINTER(PiperPrepareArgs), _ptr]
+        lib.piper_prepare.restype = ctypes.c_int
+        lib.piper_attention_forward.argtypes = [ctypes.POINTER(PiperAttentionArgs), _ptr]
+        lib.piper_attention_forward.restype = ctypes.c_int
+        version = lib.piper_abi_version()
+        if version != ABI_VERSION:
+            raise LibraryUnavailableError(
+                f"{self.path} has ABI version {version}, this package expects {ABI_VERSION}"
+            )
+
+    def has_symbol(self, name: str) -> bool:
+        return hasattr(self._lib, name)
+
+    def last_error(self) -> str:
+        return (self._lib.piper_last_error() or b"").decode("utf-8", "replace")
+
+    def _check(self, status: int, what: str) -> None:
+        if status != 0:
+            raise RuntimeError(f"{what} failed (status {status}): {self.last_error()}")
+
+    def abi_version(self) -> int:
+        return int(self._lib.piper_abi_version())
+
+    def prepared_layout(self, shape: PiperShape) -> PiperLayout:
+        layout = PiperLayout()
+        self._check(self._lib.piper_prepared_layout(ctypes.byref(shape), ctypes.byref(layout)), "piper_prepared_layout")
+        return layout
+
+    def prepare(self, args: PiperPrepareArgs, stream: int) -> None:
+        self._check(self._lib.piper_prepare(ctypes.byref(args), _ptr(stream)), "piper_prepare")
+
+    def attention_forward(self, args: PiperAttentionArgs, stream: int) -> None:
+        self._check(self._lib.piper_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_attention_forward")
+
+
+_lock = threading.Lock()
+_library: NativeLibrary | None = None
+
+
+def load_library(path: Path | None = None) -> NativeLibrary:
+    """Open the in-tree library (once); raise :class:`LibraryUnavailableError` if absent."""
+    global _library
+    with _lock:
+        if path is None and _library is not None:
+            return _library
+        target = Path(path) if path is not None else LIBRARY_PATH
+        if not target.exists():
+            raise LibraryUnavailableError(
+                f"{target} is not built; run __graft_entry__.build() or python -m piper_kernels._hip.build"
+            )
+        try:
+            library = NativeLibrary(target)
+        except OSError as error:
+            raise LibraryUnavailableError(f"cannot open {target}: {error}") from error
+        if path is None:
+            _library = library
+        return library
+
+
+def library_available() -> bool:
+    try:
+        load_library()
+    except LibraryUnavailableError:
+        return False
+    return True

@@ -1,0 +1,201 @@
+"""MI355X (gfx950) backend: prepare / launch over the C ABI, and the torch custom op.
+
+Mirrors the reference's Triton backend interface
+(``src/piper_kernels/attention/piper_attention/triton.py``): ``_prepare_piper_attention``
+(``:772-890``) quantises Q/K/V into a :class:`PreparedPiperAttention` bundle
+(``:754-769``), ``_launch_piper_attention`` (``:893-951``) runs only the fused kernel, and
+``piper_kernels::piper_attention`` is registered with the same schema and fake
+(``:984-1010``).  torch allocates every buffer; the C side only launches kernels on the
+current stream and never synchronises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from ..._hip import library as native
+from ._plan import MI355XPlan, select_plan
+
+_DTYPE_CODES = {torch.float16: native.FLOAT16, torch.bfloat16: native.BFLOAT16, torch.float32: native.FLOAT32}
+
+
+@dataclass(frozen=True)
+class PreparedPiperAttention:
+    """Quantised operands (layouts documented in ``include/piper_mi355x.h``)."""
+
+    query_code: torch.Tensor  # int8 [B, H, Sq32, D]
+    query_scale: torch.Tensor  # fp32 [B, H, Sq32/32]
+    key_code: torch.Tensor  # int8 [B, H, Sk64, D]
+    key_scale: torch.Tensor  # fp32 [B, H, Sk64/64]
+    value_code: torch.Tensor  # int8 [B, H, Sk64/64, D, 64] (V^T per 64-key tile)
+    value_scale: torch.Tensor  # fp32 [B, H, Sk64]
+    value_log2_scale: torch.Tensor  # fp32 [B, H, Sk64]
+    value_inv_multiplier: torch.Tensor  # fp32 [B, H, Sk64]
+    value_correction: torch.Tensor  # int32 [B, H, Sk64/64, D]
+    key_mean: torch.Tensor  # fp32 [B, H, D]
+    value_mean: torch.Tensor  # fp32 [B, H, D]
+    output: torch.Tensor  # [B, H, Sq, D] in the input dtype
+    shape: tuple[int, int, int, int, int]  # B, H, Sq, Sk, D
+    scale: float
+    is_causal: bool
+    plan: MI355XPlan
+
+    def native_prepared(self) -> native.PiperPrepared:
+        return native.PiperPrepared(
+            self.query_code.data_ptr(),
+            self.query_scale.data_ptr(),
+            self.key_code.data_ptr(),
+            self.key_scale.data_ptr(),
+            self.value_code.data_ptr(),
+            self.value_scale.data_ptr(),
+            self.value_log2_scale.data_ptr(),
+            self.value_inv_multiplier.data_ptr(),
+            self.value_correction.data_ptr(),
+            self.key_mean.data_ptr(),
+            self.value_mean.data_ptr(),
+        )
+
+
+def _native_input(tensor: torch.Tensor) -> tuple[torch.Tensor, native.PiperTensor]:
+    """Keep any [B,H,S,D] view whose rows are 16-byte aligned; copy anything else."""
+    strides = tensor.stride()[:3]
+    if tensor.data_ptr() % 16 != 0 or any(s % 8 != 0 for s in strides):
+        tensor = tensor.contiguous()
+        strides = tensor.stride()[:3]
+    return tensor, native.PiperTensor(tensor.data_ptr(), *strides)
+
+
+def _native_shape(batch: int, heads: int, sq: int, sk: int, d: int) -> native.PiperShape:
+    return native.PiperShape(batch, heads, sq, sk, d)
+
+
+def _prepare_piper_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    scale: float,
+    is_causal: bool,
+    *,
+    plan: MI355XPlan | None = None,
+    workspace: torch.Tensor | None = None,
+) -> PreparedPiperAttention:
+    """Quantise Q/K/V on the GPU (one HIP prep pipeline) and allocate the output."""
+    lib = native.load_library()
+    batch, heads, sq, d = query.shape
+    sk = key.shape[2]
+    if plan is None:
+        plan = select_plan(batch, heads, sq, sk, d, is_causal)
+    shape = _native_shape(batch, heads, sq, sk, d)
+    layout = lib.prepared_layout(shape)
+    device = query.device
+    sq32 = -(-sq // native.QUERY_BLOCK) * native.QUERY_BLOCK
+    sk64 = -(-sk // native.KEY_BLOCK) * native.KEY_BLOCK
+    nkb = sk64 // native.KEY_BLOCK
+
+    def empty(shape_, dtype):
+        return torch.empty(shape_, device=device, dtype=dtype)
+
+    prepared = PreparedPiperAttention(
+        query_code=empty((batch, heads, sq32, d), torch.int8),
+        query_scale=empty((batch, heads, sq32 // native.QUERY_BLOCK), torch.float32),
+        key_code=empty((batch, heads, sk64, d), torch.int8),
+        key_scale=empty((batch, heads, nkb), torch.float32),
+        value_code=empty((batch, heads, nkb, d, native.KEY_BLOCK), torch.int8),
+        value_scale=empty((batch, heads, sk64), torch.float32),
+        value_log2_scale=empty((batch, heads, sk64), torch.float32),
+        value_inv_multiplier=empty((batch, heads, sk64), torch.float32),
+        value_correction=empty((batch, heads, nkb, d), torch.int32),
+        key_mean=empty((batch, heads, d), torch.float32),
+        value_mean=empty((batch, heads, d), torch.float32),
+        output=empty((batch, heads, sq, d), query.dtype),
+        shape=(batch, heads, sq, sk, d),
+        scale=float(scale),
+        is_causal=bool(is_causal),
+        plan=plan,
+    )
+    if workspace is None or workspace.numel() < layout.workspace_bytes:
+        workspace = empty((max(layout.workspace_bytes, 1),), torch.uint8)
+    query, q_arg = _native_input(query)
+    key, k_arg = _native_input(key)
+    value, v_arg = _native_input(value)
+    args = native.PiperPrepareArgs(
+        abi_version=native.ABI_VERSION,
+        dtype=_DTYPE_CODES[query.dtype],
+        is_causal=int(bool(is_causal)),
+        reserved=0,
+        shape=shape,
+        query=q_arg,
+        key=k_arg,
+        value=v_arg,
+        prepared=prepared.native_prepared(),
+        workspace=workspace.data_ptr(),
+        workspace_bytes=workspace.numel(),
+    )
+    with torch.cuda.device(device):
+        lib.prepare(args, torch.cuda.current_stream(device).cuda_stream)
+    # the caching allocator must not recycle inputs or workspace before the stream reaches them
+    stream = torch.cuda.current_stream(device)
+    for tensor in (query, key, value, workspace):
+        tensor.record_stream(stream)
+    return prepared
+
+
+def _launch_piper_attention(
+    prepared: PreparedPiperAttention, *, output: torch.Tensor | None = None
+) -> torch.Tensor:
+    """Run only the fused kernel on prepared operands; ``output`` may be FP32 for tests."""
+    lib = native.load_library()
+    batch, heads, sq, sk, d = prepared.shape
+    out = prepared.output if output is None else output
+    if out.shape != (batch, heads, sq, d) or not out.is_contiguous() or out.dtype not in _DTYPE_CODES:
+        raise ValueError("output must be a contiguous [B, H, Sq, D] float16/bfloat16/float32 tensor")
+    args = native.PiperAttentionArgs(
+        abi_version=native.ABI_VERSION,
+        output_dtype=_DTYPE_CODES[out.dtype],
+        is_causal=int(prepared.is_causal),
+        plan=prepared.plan.plan_id,
+        shape=_native_shape(batch, heads, sq, sk, d),
+        scale=ctypes.c_float(prepared.scale).value,
+        reserved=0,
+        prepared=prepared.native_prepared(),
+        output=out.data_ptr(),
+    )
+    device = out.device
+    with torch.cuda.device(device):
+        lib.attention_forward(args, torch.cuda.current_stream(device).cuda_stream)
+    return out
+
+
+def _run_piper_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    scale: float,
+    is_causal: bool,
+    *,
+    plan: MI355XPlan | None = None,
+) -> torch.Tensor:
+    prepared = _prepare_piper_attention(query, key, value, scale, is_causal, plan=plan)
+    return _launch_piper_attention(prepared)
+
+
+@torch.library.custom_op("piper_kernels::piper_attention", mutates_args=())
+def hip_piper_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    scale: float,
+    is_causal: bool,
+) -> torch.Tensor:
+    """Piper Attention prep + fused INT8 kernel on MI355X (schema of triton.py:984-999)."""
+    return _run_piper_attention(query, key, value, scale, is_causal)
+
+
+@hip_piper_attention.register_fake
+def _hip_piper_attention_fake(
+    query: torch.Tensor, _key: torch.Tensor, _value: torch.Tensor, _scale: float, _is_causal: bool
+) -> torch.Tensor:
+    return torch.empty_like(query, memory_format=torch.contiguous_format)

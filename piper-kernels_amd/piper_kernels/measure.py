@@ -1,0 +1,121 @@
+"""Measurement semantics restated from the reference's benchmark harness.
+
+* ``attention_operations`` -- the operation count of
+  ``benchmarks/benchmark_attention.py:184-193``: 4*B*H*pairs*D, pairs = Sq*Skv, or the
+  causal triangle Sq*(Sq+1)/2.
+* ``measure_quality`` -- the metric definitions of ``benchmarks/lib/quality.py:88-252``:
+  mean/max absolute error, relative L1/L2 error, SQNR in dB and cosine similarity over the
+  finite pairs, with non-finite values counted separately.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import asdict, dataclass
+
+import torch
+
+INT8_DENSE_PEAK_TOPS = 5033.2  # MI355X: 256 CU x 2.4 GHz x 8192 int8 ops/clk/CU (dense)
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+
+
+def attention_operations(
+    batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool
+) -> int:
+    pairs = query_length * key_length
+    if is_causal:
+        pairs = query_length * (query_length + 1) // 2
+    return 4 * batch * heads * pairs * head_dim
+
+
+def effective_tops(operations: int, milliseconds: float) -> float:
+    return operations / (milliseconds * 1e-3) / 1e12
+
+
+@dataclass(frozen=True)
+class QualityMetrics:
+    mean_absolute_error: float
+    max_absolute_error: float
+    relative_l1_error: float
+    relative_l2_error: float
+    sqnr_db: float
+    cosine_similarity: float
+    actual_nonfinite_count: int
+    reference_nonfinite_count: int
+    nonfinite_mismatch_count: int
+
+    def as_dict(self) -> dict:
+        return asdict(self)
+
+
+def _comparison_dtype(actual: torch.Tensor, reference: torch.Tensor) -> torch.dtype:
+    if (
+        torch.float64 in (actual.dtype, reference.dtype)
+        or not actual.is_floating_point()
+        or not reference.is_floating_point()
+    ):
+        return torch.float64
+    return torch.float32
+
+
+def measure_quality(actual: torch.Tensor, reference: torch.Tensor) -> QualityMetrics:
+    """Compare ``actual`` with ``reference`` over finite pairs (quality.py:170-252)."""
+    if actual.shape != reference.shape:
+        raise ValueError(f"shape mismatch: actual {actual.shape}, reference {reference.shape}")
+    if actual.dtype in (torch.int64, torch.uint64) or reference.dtype in (torch.int64, torch.uint64):
+        raise ValueError(
+            "int64 and uint64 quality inputs are unsupported because float64 cannot "
+            "preserve every full-width integer value"
+        )
+    dtype = _comparison_dtype(actual, reference)
+    a = actual.detach().to(dtype).flatten()
+    r = reference.detach().to(dtype).flatten()
+    a_finite = torch.isfinite(a)
+    r_finite = torch.isfinite(r)
+    finite = a_finite & r_finite
+    nonfinite_positions = ~a_finite | ~r_finite
+    matching = (torch.isnan(a) & torch.isnan(r)) | (a == r)
+    mismatch = int(torch.count_nonzero(nonfinite_positions & ~matching))
+    a_nonfinite = int(torch.count_nonzero(~a_finite))
+    r_nonfinite = int(torch.count_nonzero(~r_finite))
+    if not bool(torch.any(finite)):
+        nan = math.nan
+        return QualityMetrics(nan, nan, nan, nan, nan, nan, a_nonfinite, r_nonfinite, mismatch)
+    a = a[finite]
+    r = r[finite]
+    error = a - r
+    abs_error = error.abs()
+    tiny = torch.finfo(dtype).tiny
+    ref_l1 = r.abs().sum()
+    ref_l2_sq = r.square().sum()
+    err_l2_sq = error.square().sum()
+    sqnr = 10 * torch.log10(ref_l2_sq / err_l2_sq)
+    a_norm = torch.linalg.vector_norm(a)
+    r_norm = torch.linalg.vector_norm(r)
+    if a_norm == 0 or r_norm == 0:
+        cosine = 1.0 if a_norm == 0 and r_norm == 0 else 0.0
+    else:
+        cosine = float((torch.dot(a, r) / (a_norm * r_norm)).clamp(-1, 1))
+    return QualityMetrics(
+        mean_absolute_error=float(abs_error.mean()),
+        max_absolute_error=float(abs_error.max()),
+        relative_l1_error=float(abs_error.sum() / ref_l1.clamp_min(tiny)),
+        relative_l2_error=float(torch.sqrt(err_l2_sq) / torch.sqrt(ref_l2_sq).clamp_min(tiny)),
+        sqnr_db=float(sqnr),
+        cosine_similarity=cosine,
+        actual_nonfinite_count=a_nonfinite,
+        reference_nonfinite_count=r_nonfinite,
+        nonfinite_mismatch_count=mismatch,
+    )
+
+
+def prep_algorithmic_bytes(
+    batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool
+) -> int:
+    """Minimum HBM bytes of the prep stage: fp16/bf16 reads of Q, K, V, int8 code writes,
+    FP32 scales (Q per 32 rows, K per 64 rows, V per key) and the K/V means."""
+    eq = batch * heads * query_length * head_dim
+    ekv = batch * heads * key_length * head_dim
+    scales = 4 * batch * heads * (-(-query_length // 32) + -(-key_length // 64) + key_length)
+    means = (4 if is_causal else 8) * batch * heads * head_dim
+    return 2 * (eq + 2 * ekv) + (eq + 2 * ekv) + scales + means

@@ -1,0 +1,229 @@
+"""Host-side contract (CPU): validation, target detection, dispatch, plan, custom op, metrics.
+
+Validation cases and messages follow the reference's
+tests/attention/piper_attention/test_dispatch.py:98-165; target detection follows
+tests/triton/test_targets.py:90-112; metric known answers follow
+tests/benchmark_support/test_quality.py:8-22 and test_benchmark_attention.py:349-359.
+"""
+
+from __future__ import annotations
+
+import math
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+import piper_kernels
+from piper_kernels import piper_attention
+from piper_kernels._hip import library as native
+from piper_kernels._hip.targets import AcceleratorTarget
+from piper_kernels.attention.piper_attention import dispatch
+from piper_kernels.attention.piper_attention._plan import MI355XPlan, select_plan
+from piper_kernels.measure import attention_operations, measure_quality, prep_algorithmic_bytes
+from piper_kernels.workloads import WORKLOADS, make_inputs
+
+
+def _inputs():
+    q = torch.randn(1, 2, 16, 64, dtype=torch.float16)
+    return q, torch.randn_like(q), torch.randn_like(q)
+
+
+def test_package_root_exports_piper_attention() -> None:
+    assert piper_kernels.piper_attention is piper_attention
+    assert "piper_attention" in piper_kernels.__all__
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.int8])
+def test_rejects_unsupported_dtype(dtype) -> None:
+    q = torch.zeros((1, 1, 8, 64), dtype=dtype)
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        piper_attention(q, q, q)
+
+
+def test_rejects_non_4d() -> None:
+    q = torch.zeros((1, 8, 64), dtype=torch.float16)
+    with pytest.raises(ValueError, match=r"shape \[batch, heads, sequence, head_dim\]"):
+        piper_attention(q, q, q)
+
+
+def test_rejects_mismatched_dtypes() -> None:
+    q, k, v = _inputs()
+    with pytest.raises(ValueError, match="share a dtype"):
+        piper_attention(q, k.to(torch.bfloat16), v)
+
+
+def test_rejects_unequal_heads() -> None:
+    q, k, v = _inputs()
+    with pytest.raises(ValueError, match="equal batch and head dimensions"):
+        piper_attention(q, k[:, :1], v[:, :1])
+
+
+def test_rejects_unsupported_head_dimension() -> None:
+    q = torch.randn(1, 1, 8, 32, dtype=torch.float16)
+    with pytest.raises(ValueError, match="head dimensions 64 and 128"):
+        piper_attention(q, q, q)
+
+
+def test_rejects_mismatched_key_value_lengths() -> None:
+    q, k, v = _inputs()
+    with pytest.raises(ValueError, match="key/value lengths"):
+        piper_attention(q, k, v[:, :, :-1])
+
+
+def test_rejects_rectangular_causal_inputs() -> None:
+    q, k, v = _inputs()
+    with pytest.raises(ValueError, match="equal query and key lengths"):
+        piper_attention(q[:, :, :-1], k, v, is_causal=True)
+
+
+@pytest.mark.parametrize(("query_length", "key_length"), [(0, 8), (8, 0)])
+def test_rejects_empty_sequences(query_length, key_length) -> None:
+    q = torch.empty((1, 1, query_length, 64), dtype=torch.float16)
+    k = torch.empty((1, 1, key_length, 64), dtype=torch.float16)
+    with pytest.raises(ValueError, match="does not accept empty"):
+        piper_attention(q, k, k)
+
+
+def test_rejects_noncontiguous_head_dimension() -> None:
+    storage = torch.randn(1, 1, 8, 128, dtype=torch.float16)
+    q = storage[..., ::2]
+    with pytest.raises(ValueError, match="head dimension must be contiguous"):
+        piper_attention(q, q, q)
+
+
+def test_rejects_autograd() -> None:
+    q, k, v = _inputs()
+    q.requires_grad_(True)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        piper_attention(q, k, v)
+
+
+@pytest.mark.parametrize("scale", [0.0, -1.0, float("inf"), float("nan")])
+def test_rejects_invalid_scale(scale) -> None:
+    q, k, v = _inputs()
+    with pytest.raises(ValueError, match="finite and positive"):
+        piper_attention(q, k, v, scale=scale)
+
+
+def test_cpu_tensors_fail_loudly_instead_of_falling_back() -> None:
+    q, k, v = _inputs()
+    with pytest.raises(NotImplementedError, match="gfx950"):
+        piper_attention(q, k, v)
+
+
+# ---- target detection ----------------------------------------------------------------
+def test_rocm_target_normalises_gcn_arch_name(monkeypatch) -> None:
+    monkeypatch.setattr(torch.version, "hip", "7.0.0", raising=False)
+    monkeypatch.setattr(
+        torch.cuda, "get_device_properties", lambda _d: SimpleNamespace(gcnArchName="gfx950:sramecc+:xnack-")
+    )
+    target = AcceleratorTarget.from_device(torch.device("cuda", 0))
+    assert target == AcceleratorTarget("hip", "gfx950")
+    assert target.is_amd_hip and target.supports_piper_mi355x
+
+
+@pytest.mark.parametrize("arch", ["gfx942", "gfx1201:sramecc+:xnack-", None])
+def test_other_amd_architectures_are_not_supported(monkeypatch, arch) -> None:
+    monkeypatch.setattr(torch.version, "hip", "7.0.0", raising=False)
+    monkeypatch.setattr(torch.cuda, "get_device_properties", lambda _d: SimpleNamespace(gcnArchName=arch))
+    assert not AcceleratorTarget.from_device(torch.device("cuda", 0)).supports_piper_mi355x
+
+
+def test_cpu_and_cuda_targets_are_not_supported(monkeypatch) -> None:
+    assert not AcceleratorTarget.from_device(torch.device("cpu")).supports_piper_mi355x
+    monkeypatch.setattr(torch.version, "hip", None, raising=False)
+    monkeypatch.setattr(torch.cuda, "get_device_capability", lambda _d: (12, 0))
+    target = AcceleratorTarget.from_device(torch.device("cuda", 0))
+    assert target == AcceleratorTarget("cuda", "sm120") and not target.supports_piper_mi355x
+
+
+# ---- dispatch ------------------------------------------------------------------------
+def test_gfx950_dispatch_routes_to_custom_op_with_default_scale(monkeypatch) -> None:
+    calls = []
+    monkeypatch.setattr(dispatch.AcceleratorTarget, "from_device", classmethod(lambda cls, d: cls("hip", "gfx950")))
+    monkeypatch.setattr(dispatch, "load_library", lambda: None)
+    monkeypatch.setattr(dispatch, "hip_piper_attention", lambda q, k, v, s, c: calls.append((s, c)) or q)
+    q, k, v = _inputs()
+    piper_attention(q, k, v)
+    piper_attention(q, k, v, scale=0.2, is_causal=True)
+    assert calls == [(64**-0.5, False), (0.2, True)]
+
+
+def test_gfx950_without_library_raises(monkeypatch, tmp_path) -> None:
+    monkeypatch.setattr(dispatch.AcceleratorTarget, "from_device", classmethod(lambda cls, d: cls("hip", "gfx950")))
+
+    def missing():
+        return native.load_library(tmp_path / "absent.so")
+
+    monkeypatch.setattr(dispatch, "load_library", missing)
+    monkeypatch.setattr(dispatch, "hip_piper_attention", lambda *a: pytest.fail("must not run without library"))
+    q, k, v = _inputs()
+    with pytest.raises(RuntimeError, match="not built"):
+        piper_attention(q, k, v)
+
+
+# ---- plan ----------------------------------------------------------------------------
+def test_plan_selection() -> None:
+    assert select_plan(1, 24, 16384, 16384, 128, False) == MI355XPlan(waves=8)
+    assert select_plan(1, 2, 193, 193, 128, False) == MI355XPlan(waves=4)
+    assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
+    assert MI355XPlan(8).as_dict() == {"waves": 8, "block_m": 256, "block_n": 64}
+    with pytest.raises(ValueError):
+        MI355XPlan(waves=2)
+
+
+# ---- custom op -----------------------------------------------------------------------
+def test_custom_op_is_registered_with_reference_schema_and_fake() -> None:
+    op = torch.ops.piper_kernels.piper_attention.default
+    schema = str(op._schema)
+    assert "Tensor query, Tensor key, Tensor value, float scale, bool is_causal" in schema
+    q = torch.empty((2, 3, 5, 64), dtype=torch.float16, device="meta").transpose(0, 1)
+    out = torch.ops.piper_kernels.piper_attention(q, q, q, 0.125, False)
+    assert out.device.type == "meta" and out.shape == q.shape and out.is_contiguous()
+
+
+# ---- measurement ---------------------------------------------------------------------
+def test_quality_metrics_have_expected_definitions() -> None:
+    reference = torch.tensor([1.0, 2.0, 0.0])
+    actual = torch.tensor([1.0, 1.0, 0.0])
+    m = measure_quality(actual, reference)
+    assert m.mean_absolute_error == pytest.approx(1 / 3)
+    assert m.max_absolute_error == 1.0
+    assert m.relative_l1_error == pytest.approx(1 / 3)
+    assert m.relative_l2_error == pytest.approx(1 / math.sqrt(5))
+    assert m.sqnr_db == pytest.approx(10 * math.log10(5))
+    assert m.cosine_similarity == pytest.approx(3 / math.sqrt(10))
+    assert m.actual_nonfinite_count == m.reference_nonfinite_count == m.nonfinite_mismatch_count == 0
+
+
+def test_quality_counts_nonfinite_values() -> None:
+    m = measure_quality(torch.tensor([math.nan, math.inf, 1.0]), torch.tensor([math.nan, 2.0, 1.0]))
+    assert m.mean_absolute_error == 0 and math.isinf(m.sqnr_db)
+    assert (m.actual_nonfinite_count, m.reference_nonfinite_count, m.nonfinite_mismatch_count) == (2, 1, 1)
+
+
+def test_effective_operations_account_for_causal_triangle() -> None:
+    assert attention_operations(1, 2, 4, 4, 8, False) == 4 * 1 * 2 * 4 * 4 * 8
+    assert attention_operations(1, 2, 4, 4, 8, True) == 4 * 1 * 2 * (4 * 5 // 2) * 8
+    assert attention_operations(1, 24, 16384, 16384, 128, False) == 3_298_534_883_328
+
+
+def test_prep_algorithmic_bytes_for_headline_shape() -> None:
+    assert prep_algorithmic_bytes(1, 24, 16384, 16384, 128, False) == 454_656_000
+
+
+def test_workload_inputs_are_reproducible_per_head() -> None:
+    w = WORKLOADS["c1"]
+    q1, k1, v1 = make_inputs(w)
+    q2, k2, v2 = make_inputs(w, heads=[3, 5])
+    assert q1.shape == (1, 8, 1024, 64) and q1.dtype is torch.float16
+    assert torch.equal(q1[:, [3, 5]], q2) and torch.equal(k1[:, [3, 5]], k2) and torch.equal(v1[:, [3, 5]], v2)
+
+
+def test_student_t_workload_has_constant_value_heads() -> None:
+    w = WORKLOADS["c5"]
+    small = type(w)(**{**w.__dict__, "query_length": 256, "key_length": 256})
+    q, k, v = make_inputs(small, heads=[0, 39], batches=[1])
+    assert torch.equal(v[0, 0], v[0, 0, :1].expand_as(v[0, 0]))
+    assert not torch.equal(v[0, 1], v[0, 1, :1].expand_as(v[0, 1]))

@@ -1,0 +1,133 @@
+"""The C-ABI library on the CPU: it loads, exports what the header declares, and its host-side
+validation reports errors.  No call here reaches a kernel launch."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from piper_kernels._hip import library as native
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "piper_mi355x.h"
+
+
+@pytest.fixture(scope="module")
+def lib() -> native.NativeLibrary:
+    if not native.library_available():
+        pytest.fail("libpiper_mi355x.so is not built; run __graft_entry__.build()")
+    return native.load_library()
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:int|const char\*)\s+(piper_\w+)\s*\(", text, re.MULTILINE))
+
+
+def test_header_declares_exactly_the_bound_symbols() -> None:
+    assert declared_functions() == set(native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib) -> None:
+    missing = [name for name in declared_functions() if not lib.has_symbol(name)]
+    assert not missing
+    assert lib.abi_version() == native.ABI_VERSION
+
+
+def test_ctypes_structures_match_the_c_header(tmp_path) -> None:
+    structs = {
+        "piper_shape": native.PiperShape,
+        "piper_tensor": native.PiperTensor,
+        "piper_prepared": native.PiperPrepared,
+        "piper_layout": native.PiperLayout,
+        "piper_prepare_args": native.PiperPrepareArgs,
+        "piper_attention_args": native.PiperAttentionArgs,
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "piper_mi355x.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{cname}.{field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("  return 0; }")
+    source = tmp_path / "abi.c"
+    source.write_text("\n".join(lines))
+    exe = tmp_path / "abi"
+    subprocess.run(["gcc", f"-I{REPO / 'include'}", str(source), "-o", str(exe)], check=True)
+    expected = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True).stdout.splitlines())
+    for cname, cls in structs.items():
+        assert int(expected[cname]) == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert int(expected[f"{cname}.{field}"]) == getattr(cls, field).offset, f"{cname}.{field}"
+
+
+@pytest.mark.parametrize(
+    "shape", [(1, 24, 16384, 16384, 128), (2, 3, 35, 67, 64), (1, 1, 1, 1, 64), (4, 32, 8192, 8192, 128)]
+)
+def test_prepared_layout_sizes(lib, shape) -> None:
+    b, h, sq, sk, d = shape
+    layout = lib.prepared_layout(native.PiperShape(*shape))
+    sq32, sk64 = -(-sq // 32) * 32, -(-sk // 64) * 64
+    assert layout.query_code_bytes == b * h * sq32 * d
+    assert layout.query_scale_bytes == b * h * (sq32 // 32) * 4
+    assert layout.key_code_bytes == layout.value_code_bytes == b * h * sk64 * d
+    assert layout.key_scale_bytes == b * h * (sk64 // 64) * 4
+    assert layout.value_key_array_bytes == b * h * sk64 * 4
+    assert layout.value_correction_bytes == b * h * (sk64 // 64) * d * 4
+    assert layout.mean_bytes == b * h * d * 4
+    assert layout.workspace_bytes == 2 * b * h * (-(-sk // 64)) * d * 8
+
+
+@pytest.mark.parametrize("bad", [(1, 1, 8, 8, 32), (0, 1, 8, 8, 64), (1, 1, 0, 8, 64)])
+def test_layout_rejects_bad_shapes(lib, bad) -> None:
+    with pytest.raises(RuntimeError, match="piper_prepared_layout failed"):
+        lib.prepared_layout(native.PiperShape(*bad))
+
+
+def test_prepare_validates_before_launching(lib) -> None:
+    args = native.PiperPrepareArgs(abi_version=native.ABI_VERSION, dtype=native.FLOAT16, shape=native.PiperShape(1, 1, 8, 8, 64))
+    with pytest.raises(RuntimeError, match="query pointer is NULL"):
+        lib.prepare(args, 0)
+    args.abi_version = 99
+    with pytest.raises(RuntimeError, match="ABI version mismatch"):
+        lib.prepare(args, 0)
+    args.abi_version = native.ABI_VERSION
+    args.dtype = native.FLOAT32
+    with pytest.raises(RuntimeError, match="float16 or bfloat16"):
+        lib.prepare(args, 0)
+
+
+def test_prepare_rejects_misaligned_inputs(lib) -> None:
+    fake = 0x1000
+    args = native.PiperPrepareArgs(
+        abi_version=native.ABI_VERSION,
+        dtype=native.FLOAT16,
+        shape=native.PiperShape(1, 1, 8, 8, 64),
+        query=native.PiperTensor(fake + 2, 512, 512, 64),
+        key=native.PiperTensor(fake, 512, 512, 64),
+        value=native.PiperTensor(fake, 512, 512, 64),
+    )
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        lib.prepare(args, 0)
+
+
+def test_attention_validates_before_launching(lib) -> None:
+    args = native.PiperAttentionArgs(
+        abi_version=native.ABI_VERSION, output_dtype=native.FLOAT16, shape=native.PiperShape(1, 1, 8, 8, 64), scale=0.0
+    )
+    with pytest.raises(RuntimeError, match="scale must be finite and positive"):
+        lib.attention_forward(args, 0)
+    args.scale = 0.125
+    args.plan = 7
+    with pytest.raises(RuntimeError, match="unknown plan"):
+        lib.attention_forward(args, 0)
+    args.plan = 0
+    with pytest.raises(RuntimeError, match="NULL"):
+        lib.attention_forward(args, 0)
+    args.is_causal = 1
+    args.shape = native.PiperShape(1, 1, 8, 9, 64)
+    with pytest.raises(RuntimeError, match="equal query and key lengths"):
+        lib.attention_forward(args, 0)
