@@ -45,53 +45,71 @@ struct TileLayout {
   static constexpr int kRounds = (kChunks + kThreads - 1) / kThreads;
 };
 
+// Global -> register -> LDS staging of one 64-key block: kRounds 16-byte chunks per thread.
+// Branch-free on purpose: a per-lane branch around a load makes the compiler wait for it at
+// the reconvergence point, which would serialise the prefetch.  Threads past the last chunk
+// load and store the last chunk again (identical data, benign).
 template <int D, int NW>
-__device__ __forceinline__ void fetch_tile(const AttnParams& p, int bh, int t,
-                                           uint4 (&reg)[TileLayout<D, NW>::kRounds]) {
+struct Staging {
   using L = TileLayout<D, NW>;
-  const int8_t* ktile = p.key_code + (static_cast<long>(bh) * p.sk64 + static_cast<long>(t) * kKeyBlock) * D;
-  const int8_t* vtile = p.value_code + (static_cast<long>(bh) * p.nkb + t) * static_cast<long>(D * kKeyBlock);
-  const float* lk = p.value_log2_scale + static_cast<long>(bh) * p.sk64 + t * kKeyBlock;
-  const float* iv = p.value_inv_multiplier + static_cast<long>(bh) * p.sk64 + t * kKeyBlock;
-  const int32_t* cr = p.value_correction + (static_cast<long>(bh) * p.nkb + t) * D;
+  static constexpr int kRounds = (L::kChunks + L::kThreads - 1) / L::kThreads;
+};
+
+template <int D, int NW>
+__device__ __forceinline__ int staging_chunk(int r) {
+  using L = TileLayout<D, NW>;
+  const int c = threadIdx.x + r * L::kThreads;
+  return c < L::kChunks ? c : L::kChunks - 1;
+}
+
+// Loads block t (t must be a valid block index).
+template <int D, int NW>
+__device__ __forceinline__ void fetch_block(const AttnParams& p, int bh, int t,
+                                            v4i (&reg)[Staging<D, NW>::kRounds]) {
+  using L = TileLayout<D, NW>;
+  const v4i* kb = reinterpret_cast<const v4i*>(p.key_code + (static_cast<long>(bh) * p.sk64 + static_cast<long>(t) * kKeyBlock) * D);
+  const v4i* vb = reinterpret_cast<const v4i*>(p.value_code + (static_cast<long>(bh) * p.nkb + t) * static_cast<long>(D * kKeyBlock));
+  const v4i* lb = reinterpret_cast<const v4i*>(p.value_log2_scale + static_cast<long>(bh) * p.sk64 + t * kKeyBlock);
+  const v4i* ib = reinterpret_cast<const v4i*>(p.value_inv_multiplier + static_cast<long>(bh) * p.sk64 + t * kKeyBlock);
+  const v4i* cb = reinterpret_cast<const v4i*>(p.value_correction + (static_cast<long>(bh) * p.nkb + t) * D);
+  constexpr int kV = L::kChunksK;
+  constexpr int kL = kV + L::kChunksV;
+  constexpr int kI = kL + 16;
+  constexpr int kC = kI + 16;
 #pragma unroll
-  for (int r = 0; r < L::kRounds; ++r) {
-    const int i = threadIdx.x + r * L::kThreads;
-    if (i >= L::kChunks) break;
-    const uint4* src;
-    if (i < L::kChunksK) {
-      src = reinterpret_cast<const uint4*>(ktile) + i;
-    } else if (i < L::kChunksK + L::kChunksV) {
-      src = reinterpret_cast<const uint4*>(vtile) + (i - L::kChunksK);
-    } else if (i < L::kChunksK + L::kChunksV + 16) {
-      src = reinterpret_cast<const uint4*>(lk) + (i - L::kChunksK - L::kChunksV);
-    } else if (i < L::kChunksK + L::kChunksV + 32) {
-      src = reinterpret_cast<const uint4*>(iv) + (i - L::kChunksK - L::kChunksV - 16);
-    } else {
-      src = reinterpret_cast<const uint4*>(cr) + (i - L::kChunksK - L::kChunksV - 32);
-    }
+  for (int r = 0; r < Staging<D, NW>::kRounds; ++r) {
+    const int i = staging_chunk<D, NW>(r);
+    const v4i* src = i < kV ? kb + i : i < kL ? vb + (i - kV) : i < kI ? lb + (i - kL) : i < kC ? ib + (i - kI) : cb + (i - kC);
     reg[r] = *src;
   }
 }
 
 template <int D, int NW>
-__device__ __forceinline__ void store_tile(char* stage, const uint4 (&reg)[TileLayout<D, NW>::kRounds]) {
+__device__ __forceinline__ void store_block(char* stage, const v4i (&reg)[Staging<D, NW>::kRounds]) {
   using L = TileLayout<D, NW>;
 #pragma unroll
-  for (int r = 0; r < L::kRounds; ++r) {
-    const int i = threadIdx.x + r * L::kThreads;
-    if (i >= L::kChunks) break;
-    int dst;
-    if (i < L::kChunksK) {
-      dst = (i / (D / 16)) * L::kKStride + (i % (D / 16)) * 16;
-    } else if (i < L::kChunksK + L::kChunksV) {
-      const int j = i - L::kChunksK;
-      dst = L::kKBytes + (j >> 2) * L::kVStride + (j & 3) * 16;
-    } else {
-      dst = L::kLogOffset + (i - L::kChunksK - L::kChunksV) * 16;  // log2, inv and corr are contiguous
-    }
-    *reinterpret_cast<uint4*>(stage + dst) = reg[r];
+  for (int r = 0; r < Staging<D, NW>::kRounds; ++r) {
+    const int i = staging_chunk<D, NW>(r);
+    const int j = i - L::kChunksK;
+    const int k_dst = (i / (D / 16)) * L::kKStride + (i % (D / 16)) * 16;
+    const int v_dst = L::kKBytes + (j >> 2) * L::kVStride + (j & 3) * 16;
+    const int x_dst = L::kLogOffset + (j - L::kChunksV) * 16;  // log2, inv and corr are contiguous
+    const int dst = i < L::kChunksK ? k_dst : j < L::kChunksV ? v_dst : x_dst;
+    *reinterpret_cast<v4i*>(stage + dst) = reg[r];
   }
+}
+
+// Balanced max over 32 values (depth 4 instead of a 16-long v_max3 chain).
+__device__ __forceinline__ float max32(const float (&x)[32]) {
+  float t[11];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) t[i] = fmaxf(fmaxf(x[3 * i], x[3 * i + 1]), x[3 * i + 2]);
+  t[10] = fmaxf(x[30], x[31]);
+  const float u0 = fmaxf(fmaxf(t[0], t[1]), t[2]);
+  const float u1 = fmaxf(fmaxf(t[3], t[4]), t[5]);
+  const float u2 = fmaxf(fmaxf(t[6], t[7]), t[8]);
+  const float u3 = fmaxf(t[9], t[10]);
+  return fmaxf(fmaxf(u0, u1), fmaxf(u2, u3));
 }
 
 __device__ __forceinline__ uint32_t pack_codes(float e0, float e1, float e2, float e3) {
@@ -102,8 +120,21 @@ __device__ __forceinline__ uint32_t pack_codes(float e0, float e1, float e2, flo
   return w ^ 0x80808080u;  // u - 128 as signed INT8
 }
 
+// Keep x as a materialised FP32 value: narrowing must round the FP32 result (as the
+// reference casts its FP32 output), not a fused multiply-add to f16 (v_fma_mix).
+__device__ __forceinline__ float materialize(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 template <int kOut>
 __device__ __forceinline__ void store4(void* out, long index, float a, float b, float c, float d) {
+  if constexpr (kOut != 2) {
+    a = materialize(a);
+    b = materialize(b);
+    c = materialize(c);
+    d = materialize(d);
+  }
   if constexpr (kOut == 2) {
     *reinterpret_cast<float4*>(static_cast<float*>(out) + index) = make_float4(a, b, c, d);
   } else if constexpr (kOut == 1) {
@@ -117,11 +148,165 @@ __device__ __forceinline__ void store4(void* out, long index, float a, float b, 
   }
 }
 
+// Integer scores S^T = K Q^T of one 64-key block: s[0] keys 0..31, s[1] keys 32..63 (each
+// lane: its query column, keys 16h + r after the K-row permutation).
+template <int D, int NW>
+__device__ __forceinline__ void block_scores(const char* stage, const v4i (&qf)[D / 32], int h, int krow,
+                                             v16i (&s)[2]) {
+  using L = TileLayout<D, NW>;
+  s[0] = s[1] = v16i{};
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+    const char* kb = stage + 32 * c + 16 * h;
+    const v4i a0 = *reinterpret_cast<const v4i*>(kb + krow * L::kKStride);
+    const v4i a1 = *reinterpret_cast<const v4i*>(kb + (32 + krow) * L::kKStride);
+    s[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qf[c], s[0], 0, 0, 0);
+    s[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qf[c], s[1], 0, 0, 0);
+  }
+}
+
+// Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave.
+template <int D, int NW, bool kCausal>
+__device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[2], float ct, int t, int q0, int n,
+                                             int h, float (&num)[D / 32][16], float& den, float& mref) {
+  using L = TileLayout<D, NW>;
+  constexpr int kChunksD = D / 32;
+
+  // ---- shifted scores x = s * c + log2(vs), in-lane over 32 keys, and the block max ----
+  const float4* lk4 = reinterpret_cast<const float4*>(stage + L::kLogOffset);
+  float x[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 la = lk4[4 * h + q];
+    const float4 lb = lk4[8 + 4 * h + q];
+    x[4 * q + 0] = fmaf(static_cast<float>(s[0][4 * q + 0]), ct, la.x);
+    x[4 * q + 1] = fmaf(static_cast<float>(s[0][4 * q + 1]), ct, la.y);
+    x[4 * q + 2] = fmaf(static_cast<float>(s[0][4 * q + 2]), ct, la.z);
+    x[4 * q + 3] = fmaf(static_cast<float>(s[0][4 * q + 3]), ct, la.w);
+    x[16 + 4 * q + 0] = fmaf(static_cast<float>(s[1][4 * q + 0]), ct, lb.x);
+    x[16 + 4 * q + 1] = fmaf(static_cast<float>(s[1][4 * q + 1]), ct, lb.y);
+    x[16 + 4 * q + 2] = fmaf(static_cast<float>(s[1][4 * q + 2]), ct, lb.z);
+    x[16 + 4 * q + 3] = fmaf(static_cast<float>(s[1][4 * q + 3]), ct, lb.w);
+  }
+  if constexpr (kCausal) {
+    if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // block crosses this wave's diagonal
+      const int query = q0 + n;
+      const int key_base = t * kKeyBlock + 16 * h;
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        const int key = key_base + (r < 16 ? r : 16 + r);
+        if (key > query) x[r] = -__builtin_inff();
+      }
+    }
+  }
+  const float mx = cross_half_max(max32(x));
+
+  // ---- lazy rescale of num/den when the block maximum outgrows the reference by 2^8 ----
+  const bool grow = mx > mref + kLazyRescale;
+  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    const float alpha = grow ? __builtin_amdgcn_exp2f(mref - mx) : 1.0f;
+    if (grow) mref = mx;
+#pragma unroll
+    for (int j = 0; j < kChunksD; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) num[j][r] *= alpha;
+    den *= alpha;
+  }
+
+  // ---- e = 255 * vs * p = exp2(x - bm + log2 255), den += sum(p) * beta, UINT8 codes ----
+  const bool empty = mx == -__builtin_inff();
+  const float beta = empty ? 0.0f : __builtin_amdgcn_exp2f(mx - mref);
+  const float shift = empty ? 0.0f : mx - kLog2Of255;
+  const float4* iv4 = reinterpret_cast<const float4*>(stage + L::kInvOffset);
+  float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  uint32_t pw[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 ia = iv4[4 * h + q];
+    const float4 ib = iv4[8 + 4 * h + q];
+    const float e0 = __builtin_amdgcn_exp2f(x[4 * q + 0] - shift);
+    const float e1 = __builtin_amdgcn_exp2f(x[4 * q + 1] - shift);
+    const float e2 = __builtin_amdgcn_exp2f(x[4 * q + 2] - shift);
+    const float e3 = __builtin_amdgcn_exp2f(x[4 * q + 3] - shift);
+    const float f0 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 0] - shift);
+    const float f1 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 1] - shift);
+    const float f2 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 2] - shift);
+    const float f3 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 3] - shift);
+    ps[0] = fmaf(e0, ia.x, ps[0]);
+    ps[1] = fmaf(e1, ia.y, ps[1]);
+    ps[2] = fmaf(e2, ia.z, ps[2]);
+    ps[3] = fmaf(e3, ia.w, ps[3]);
+    ps[0] = fmaf(f0, ib.x, ps[0]);
+    ps[1] = fmaf(f1, ib.y, ps[1]);
+    ps[2] = fmaf(f2, ib.z, ps[2]);
+    ps[3] = fmaf(f3, ib.w, ps[3]);
+    pw[q] = pack_codes(e0, e1, e2, e3);
+    pw[4 + q] = pack_codes(f0, f1, f2, f3);
+  }
+  const float psum = cross_half_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
+  den = fmaf(psum, beta, den);
+  const float weight = beta * (1.0f / 255.0f);
+  const v4i p0 = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]), static_cast<int>(pw[3])};
+  const v4i p1 = {static_cast<int>(pw[4]), static_cast<int>(pw[5]), static_cast<int>(pw[6]), static_cast<int>(pw[7])};
+
+  // ---- numerator: O^T += (V^T (u - 128) + 128 colsum) * beta / 255 ----
+  const v4i* corr4 = reinterpret_cast<const v4i*>(stage + L::kCorrOffset);
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j) {
+    v16i acc;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const v4i c4 = corr4[8 * j + 2 * g + h];
+      acc[4 * g + 0] = c4[0];
+      acc[4 * g + 1] = c4[1];
+      acc[4 * g + 2] = c4[2];
+      acc[4 * g + 3] = c4[3];
+    }
+    const char* vrow = stage + L::kKBytes + (32 * j + n) * L::kVStride + 16 * h;
+    const v4i a0 = *reinterpret_cast<const v4i*>(vrow);
+    const v4i a1 = *reinterpret_cast<const v4i*>(vrow + 32);
+    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, p0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, p1, acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) num[j][r] = fmaf(static_cast<float>(acc[r]), weight, num[j][r]);
+  }
+}
+
+// One loop iteration for one wave: consume block t (LDS stage t % 4), issue the QK MFMAs of
+// block t + 1 first so they run under the softmax VALU work, then write block t + 2 (loaded
+// into `ready` during the previous iteration) to stage (t + 2) % 4 and start loading block
+// t + 3 into `loading`.  Global loads therefore have two iterations to arrive.
+template <int D, int NW, bool kCausal>
+__device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
+                                              const v4i (&qf)[D / 32], float cq, const float* key_scale, int q0,
+                                              int n, int h, int krow, v16i (&s_cur)[2], float (&num)[D / 32][16],
+                                              float& den, float& mref,
+                                              v4i (&ready)[Staging<D, NW>::kRounds],
+                                              v4i (&loading)[Staging<D, NW>::kRounds]) {
+  using L = TileLayout<D, NW>;
+  constexpr int kStages = 4;
+  // unconditional (clamped) so every iteration issues the same loads: static vmcnt waits
+  fetch_block<D, NW>(p, bh, min(t + 3, tiles - 1), loading);
+  if (t < wave_tiles) {
+    v16i s_next[2];
+    block_scores<D, NW>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, s_next);  // unused past the end
+    block_update<D, NW, kCausal>(smem + (t % kStages) * L::kStageBytes, s_cur, cq * key_scale[t], t, q0, n, h, num,
+                                 den, mref);
+    s_cur[0] = s_next[0];
+    s_cur[1] = s_next[1];
+  }
+  if (t + 2 < tiles) store_block<D, NW>(smem + ((t + 2) % kStages) * L::kStageBytes, ready);
+  __syncthreads();
+}
+
+// K/V blocks stream through a 4-stage LDS ring, staged through two alternating register sets.
 template <int D, int NW, bool kCausal, int kOut>
 __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams p) {
   using L = TileLayout<D, NW>;
+  using S = Staging<D, NW>;
   constexpr int kChunksD = D / 32;
-  __shared__ __attribute__((aligned(16))) char smem[2 * L::kStageBytes];
+  constexpr int kStages = 4;
+  __shared__ __attribute__((aligned(16))) char smem[kStages * L::kStageBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -167,136 +352,31 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
   const float* key_scale = p.key_scale + static_cast<long>(bh) * p.nkb;
 
-  uint4 reg[L::kRounds];
-  fetch_tile<D, NW>(p, bh, 0, reg);
-  store_tile<D, NW>(smem, reg);
+  // prologue: blocks 0 and 1 into LDS, block 2 into registers
+  v4i reg_a[S::kRounds];
+  v4i reg_b[S::kRounds];
+  fetch_block<D, NW>(p, bh, 0, reg_a);
+  fetch_block<D, NW>(p, bh, min(1, tiles - 1), reg_b);
+  store_block<D, NW>(smem, reg_a);
+  store_block<D, NW>(smem + L::kStageBytes, reg_b);  // a copy of block 0 when there is one block
+  fetch_block<D, NW>(p, bh, min(2, tiles - 1), reg_a);
   __syncthreads();
 
-  for (int t = 0; t < tiles; ++t) {
-    const char* sb = smem + (t & 1) * L::kStageBytes;
-    if (t + 1 < tiles) fetch_tile<D, NW>(p, bh, t + 1, reg);
+  v16i s_cur[2];
+  if (wave_tiles > 0) block_scores<D, NW>(smem, qf, h, krow, s_cur);
 
-    if (t < wave_tiles) {
-      // ---- integer scores for 64 keys: s0 keys 0..31, s1 keys 32..63 ----
-      v16i s0 = {}, s1 = {};
-#pragma unroll
-      for (int c = 0; c < kChunksD; ++c) {
-        const v4i a0 = *reinterpret_cast<const v4i*>(sb + krow * L::kKStride + 32 * c + 16 * h);
-        const v4i a1 = *reinterpret_cast<const v4i*>(sb + (32 + krow) * L::kKStride + 32 * c + 16 * h);
-        s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qf[c], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qf[c], s1, 0, 0, 0);
-      }
-      const float ct = cq * key_scale[t];
-
-      // ---- shifted scores x = s * c + log2(vs), in-lane over 32 keys ----
-      const float4* lk4 = reinterpret_cast<const float4*>(sb + L::kLogOffset);
-      float x[32];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 la = lk4[4 * h + q];
-        const float4 lb = lk4[8 + 4 * h + q];
-        x[4 * q + 0] = fmaf(static_cast<float>(s0[4 * q + 0]), ct, la.x);
-        x[4 * q + 1] = fmaf(static_cast<float>(s0[4 * q + 1]), ct, la.y);
-        x[4 * q + 2] = fmaf(static_cast<float>(s0[4 * q + 2]), ct, la.z);
-        x[4 * q + 3] = fmaf(static_cast<float>(s0[4 * q + 3]), ct, la.w);
-        x[16 + 4 * q + 0] = fmaf(static_cast<float>(s1[4 * q + 0]), ct, lb.x);
-        x[16 + 4 * q + 1] = fmaf(static_cast<float>(s1[4 * q + 1]), ct, lb.y);
-        x[16 + 4 * q + 2] = fmaf(static_cast<float>(s1[4 * q + 2]), ct, lb.z);
-        x[16 + 4 * q + 3] = fmaf(static_cast<float>(s1[4 * q + 3]), ct, lb.w);
-      }
-      if constexpr (kCausal) {
-        if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // tile crosses this wave's diagonal
-          const int query = q0 + n;
-          const int key_base = t * kKeyBlock + 16 * h;
-#pragma unroll
-          for (int r = 0; r < 32; ++r) {
-            const int key = key_base + (r < 16 ? r : 16 + r);
-            if (key > query) x[r] = -__builtin_inff();
-          }
-        }
-      }
-
-      float mx = x[0];
-#pragma unroll
-      for (int r = 1; r < 32; ++r) mx = fmaxf(mx, x[r]);
-      mx = cross_half_max(mx);  // block max of the shifted scores for this query
-
-      const bool grow = mx > mref + kLazyRescale;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float alpha = grow ? __builtin_amdgcn_exp2f(mref - mx) : 1.0f;
-        if (grow) mref = mx;
-#pragma unroll
-        for (int j = 0; j < kChunksD; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) num[j][r] *= alpha;
-        den *= alpha;
-      }
-      const bool empty = mx == -__builtin_inff();
-      const float beta = empty ? 0.0f : __builtin_amdgcn_exp2f(mx - mref);
-      const float shift = empty ? 0.0f : mx - kLog2Of255;
-
-      // ---- e = 255 * vs * p, den += sum(p), UINT8 codes ----
-      const float4* iv4 = reinterpret_cast<const float4*>(sb + L::kInvOffset);
-      float psum = 0.0f;
-      uint32_t pw[8];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 ia = iv4[4 * h + q];
-        const float4 ib = iv4[8 + 4 * h + q];
-        const float e0 = __builtin_amdgcn_exp2f(x[4 * q + 0] - shift);
-        const float e1 = __builtin_amdgcn_exp2f(x[4 * q + 1] - shift);
-        const float e2 = __builtin_amdgcn_exp2f(x[4 * q + 2] - shift);
-        const float e3 = __builtin_amdgcn_exp2f(x[4 * q + 3] - shift);
-        const float f0 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 0] - shift);
-        const float f1 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 1] - shift);
-        const float f2 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 2] - shift);
-        const float f3 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 3] - shift);
-        psum = fmaf(e0, ia.x, psum);
-        psum = fmaf(e1, ia.y, psum);
-        psum = fmaf(e2, ia.z, psum);
-        psum = fmaf(e3, ia.w, psum);
-        psum = fmaf(f0, ib.x, psum);
-        psum = fmaf(f1, ib.y, psum);
-        psum = fmaf(f2, ib.z, psum);
-        psum = fmaf(f3, ib.w, psum);
-        pw[q] = pack_codes(e0, e1, e2, e3);
-        pw[4 + q] = pack_codes(f0, f1, f2, f3);
-      }
-      psum = cross_half_sum(psum);
-      den = fmaf(psum, beta, den);
-
-      // ---- numerator: O^T += (V^T (u - 128) + 128 colsum) * beta / 255 ----
-      const v4i p0 = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]),
-                      static_cast<int>(pw[3])};
-      const v4i p1 = {static_cast<int>(pw[4]), static_cast<int>(pw[5]), static_cast<int>(pw[6]),
-                      static_cast<int>(pw[7])};
-      const float weight = beta * (1.0f / 255.0f);
-      const char* vsb = sb + L::kKBytes;
-      const v4i* corr4 = reinterpret_cast<const v4i*>(sb + L::kCorrOffset);
-#pragma unroll
-      for (int j = 0; j < kChunksD; ++j) {
-        v16i acc;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const v4i c4 = corr4[8 * j + 2 * g + h];
-          acc[4 * g + 0] = c4[0];
-          acc[4 * g + 1] = c4[1];
-          acc[4 * g + 2] = c4[2];
-          acc[4 * g + 3] = c4[3];
-        }
-        const char* vrow = vsb + (32 * j + n) * L::kVStride + 16 * h;
-        const v4i a0 = *reinterpret_cast<const v4i*>(vrow);
-        const v4i a1 = *reinterpret_cast<const v4i*>(vrow + 32);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, p0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, p1, acc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) num[j][r] = fmaf(static_cast<float>(acc[r]), weight, num[j][r]);
-      }
-    }
-
-    if (t + 1 < tiles) store_tile<D, NW>(smem + ((t + 1) & 1) * L::kStageBytes, reg);
-    __syncthreads();
+  // Iteration t stores the set loaded at t - 1 and loads into the other one: unrolled by two
+  // so both register sets keep static names.
+  int t = 0;
+  for (; t + 1 < tiles; t += 2) {
+    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_cur, num,
+                                  den, mref, reg_a, reg_b);
+    pipeline_step<D, NW, kCausal>(p, smem, t + 1, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_cur,
+                                  num, den, mref, reg_b, reg_a);
   }
+  if (t < tiles)
+    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_cur, num,
+                                  den, mref, reg_a, reg_b);
 
   // ---- epilogue: num / max(den, 1e-30) + mean(V), one query per lane ----
   const int query = q0 + n;
