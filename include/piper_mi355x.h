@@ -78,45 +78,43 @@ typedef struct piper_tensor {
  * piper_attention_forward.  With Sq32 = ceil(Sq/32)*32, Sk64 = ceil(Sk/64)*64,
  * nqb = Sq32/32 and nkb = Sk64/64, all arrays are dense and row-major:
  *
- *   query_code         int8    [B, H, Sq32, D]       Q codes, padded rows zero
- *   query_scale        float   [B, H, nqb]           amax/127 + 1e-7 per 32-row block
- *   key_code           int8    [B, H, Sk64, D]       codes of K - mean(K), padded rows zero
- *   key_scale          float   [B, H, nkb]           per 64-row block
- *   value_code         int8    [B, H, nkb, D, 64]    per-key codes of V - mean(V), stored
- *                                                    transposed per 64-key tile (V^T tiles);
- *                                                    padded keys zero
- *   value_scale        float   [B, H, Sk64]          amax_D/127 + 1e-7 per key (padding 0)
- *   value_log2_scale   float   [B, H, Sk64]          log2(value_scale) (padding -inf)
- *   value_inv_multiplier float [B, H, Sk64]          1/(255*value_scale) (padding 0)
- *   value_correction   int32   [B, H, nkb, D]        128 * sum over the tile's 64 keys of
- *                                                    value_code (affine PV correction)
- *   key_mean           float   [B, H, D]             order-defined sequence mean of K
- *   value_mean         float   [B, H, D]             same for V; zeros when causal
+ *   query_code     int8    [B, H, Sq32, D]   Q codes, padded rows zero
+ *   query_scale    float   [B, H, nqb]       amax/127 + 1e-7 per 32-row block
+ *   key_scale      float   [B, H, nkb]       same for K - mean(K), per 64-row block
+ *   value_scale    float   [B, H, Sk64]      amax_D/127 + 1e-7 per V row (padding 0)
+ *   key_mean       float   [B, H, D]         order-defined sequence mean of K
+ *   value_mean     float   [B, H, D]         same for V; zeros when causal
+ *   kv_tiles       bytes   [B, H, nkb, PIPER_KV_TILE_BYTES(D)]: one self-contained record
+ *                  per 64-key tile, in the order the attention kernel stages it into LDS:
+ *       [0, 64*D)                int8  K codes of K - mean(K), [64 keys][D]; padding zero
+ *       [64*D, 128*D)            int8  V codes of V - mean(V), transposed: [D][64 keys];
+ *                                      padding zero
+ *       [128*D, 128*D + 256)     float log2(value_scale) of the 64 keys (padding -inf)
+ *       [128*D + 256, +512)      float 1 / (255 * value_scale) (padding 0)
+ *       [128*D + 512, +4*D)      int32 128 * (sum over the 64 keys of the V codes), per
+ *                                      feature: the affine correction of the PV product
  */
+#define PIPER_KV_TILE_BYTES(head_dim) (128 * (head_dim) + 512 + 4 * (head_dim))
+
 typedef struct piper_prepared {
   int8_t* query_code;
   float* query_scale;
-  int8_t* key_code;
   float* key_scale;
-  int8_t* value_code;
   float* value_scale;
-  float* value_log2_scale;
-  float* value_inv_multiplier;
-  int32_t* value_correction;
   float* key_mean;
   float* value_mean;
+  void* kv_tiles;
 } piper_prepared;
 
 /* Byte sizes of every caller-allocated buffer for a shape. */
 typedef struct piper_layout {
   int64_t query_code_bytes;
   int64_t query_scale_bytes;
-  int64_t key_code_bytes;
   int64_t key_scale_bytes;
-  int64_t value_code_bytes;
-  int64_t value_key_array_bytes; /* each of value_scale, value_log2_scale, value_inv_multiplier */
-  int64_t value_correction_bytes;
+  int64_t value_scale_bytes;
   int64_t mean_bytes; /* each of key_mean, value_mean */
+  int64_t kv_tile_bytes; /* one tile record */
+  int64_t kv_tiles_bytes; /* all tile records */
   int64_t workspace_bytes; /* scratch for piper_prepare (FP64 mean partials) */
 } piper_layout;
 

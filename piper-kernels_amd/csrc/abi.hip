@@ -73,12 +73,11 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
   const int64_t chunks = ceil_div(shape->key_length, PIPER_MEAN_CHUNK);
   layout->query_code_bytes = bh * sq32 * d;
   layout->query_scale_bytes = bh * (sq32 / PIPER_QUERY_BLOCK) * 4;
-  layout->key_code_bytes = bh * sk64 * d;
   layout->key_scale_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * 4;
-  layout->value_code_bytes = bh * sk64 * d;
-  layout->value_key_array_bytes = bh * sk64 * 4;
-  layout->value_correction_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * d * 4;
+  layout->value_scale_bytes = bh * sk64 * 4;
   layout->mean_bytes = bh * d * 4;
+  layout->kv_tile_bytes = PIPER_KV_TILE_BYTES(d);
+  layout->kv_tiles_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * PIPER_KV_TILE_BYTES(d);
   layout->workspace_bytes = 2 * bh * chunks * d * 8;
   g_last_error[0] = '\0';
   return PIPER_OK;
@@ -98,12 +97,10 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   if (int st = check_input("key", a->key)) return st;
   if (int st = check_input("value", a->value)) return st;
   const piper_prepared& o = a->prepared;
-  if (!o.query_code || !o.query_scale || !o.key_code || !o.key_scale || !o.value_code || !o.value_scale ||
-      !o.value_log2_scale || !o.value_inv_multiplier || !o.value_correction || !o.key_mean || !o.value_mean)
+  if (!o.query_code || !o.query_scale || !o.key_scale || !o.value_scale || !o.key_mean || !o.value_mean ||
+      !o.kv_tiles)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared output pointer is NULL");
-  if (!aligned16(o.query_code) || !aligned16(o.key_code) || !aligned16(o.value_code) ||
-      !aligned16(o.value_log2_scale) || !aligned16(o.value_inv_multiplier) || !aligned16(o.value_correction) ||
-      !aligned16(o.value_mean))
+  if (!aligned16(o.query_code) || !aligned16(o.kv_tiles) || !aligned16(o.value_mean))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte aligned");
   piper_layout layout;
   if (int st = piper_prepared_layout(&a->shape, &layout)) return st;
@@ -149,13 +146,9 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   qp.value_mean = o.value_mean;
   qp.query_code = o.query_code;
   qp.query_scale = o.query_scale;
-  qp.key_code = o.key_code;
   qp.key_scale = o.key_scale;
-  qp.value_code = o.value_code;
   qp.value_scale = o.value_scale;
-  qp.value_log2_scale = o.value_log2_scale;
-  qp.value_inv_multiplier = o.value_inv_multiplier;
-  qp.value_correction = o.value_correction;
+  qp.kv_tiles = static_cast<uint8_t*>(o.kv_tiles);
 
   const hipError_t err = piper::launch_prep(a->dtype == PIPER_BFLOAT16, d, mp, qp, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "prep launch failed: %s", hipGetErrorString(err));
@@ -177,12 +170,10 @@ int piper_attention_forward(const piper_attention_args* a, void* stream) {
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
   if (a->plan < 0 || a->plan > 1) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
   const piper_prepared& o = a->prepared;
-  if (!o.query_code || !o.query_scale || !o.key_code || !o.key_scale || !o.value_code || !o.value_log2_scale ||
-      !o.value_inv_multiplier || !o.value_correction || !o.value_mean || !a->output)
+  if (!o.query_code || !o.query_scale || !o.key_scale || !o.kv_tiles || !o.value_mean || !a->output)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared input or the output pointer is NULL");
-  if (!aligned16(o.query_code) || !aligned16(o.key_code) || !aligned16(o.value_code) ||
-      !aligned16(o.value_log2_scale) || !aligned16(o.value_inv_multiplier) || !aligned16(o.value_correction) ||
-      !aligned16(o.value_mean) || (reinterpret_cast<uintptr_t>(a->output) & 7u) != 0)
+  if (!aligned16(o.query_code) || !aligned16(o.kv_tiles) || !aligned16(o.value_mean) ||
+      (reinterpret_cast<uintptr_t>(a->output) & 7u) != 0)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
 
   const piper_shape& s = a->shape;
@@ -190,12 +181,8 @@ int piper_attention_forward(const piper_attention_args* a, void* stream) {
   piper::AttnParams ap{};
   ap.query_code = o.query_code;
   ap.query_scale = o.query_scale;
-  ap.key_code = o.key_code;
   ap.key_scale = o.key_scale;
-  ap.value_code = o.value_code;
-  ap.value_log2_scale = o.value_log2_scale;
-  ap.value_inv_multiplier = o.value_inv_multiplier;
-  ap.value_correction = o.value_correction;
+  ap.kv_tiles = static_cast<const uint8_t*>(o.kv_tiles);
   ap.value_mean = o.value_mean;
   ap.output = a->output;
   ap.batch_heads = static_cast<int>(s.batch * s.heads);

@@ -43,6 +43,7 @@ struct TileLayout {
   static constexpr int kChunksV = D * kKeyBlock / 16;
   static constexpr int kChunks = kChunksK + kChunksV + 16 + 16 + D / 4;
   static constexpr int kRounds = (kChunks + kThreads - 1) / kThreads;
+  static_assert(kChunks * 16 == kv_tile_bytes(D), "LDS stage order must match the tile record");
 };
 
 // Global -> register -> LDS staging of one 64-key block: kRounds 16-byte chunks per thread.
@@ -62,26 +63,14 @@ __device__ __forceinline__ int staging_chunk(int r) {
   return c < L::kChunks ? c : L::kChunks - 1;
 }
 
-// Loads block t (t must be a valid block index).
+// Loads the tile record of block t (t must be a valid block index): a uniform base address
+// plus a loop-invariant per-thread offset, so the loop spends no VALU on addressing.
 template <int D, int NW>
 __device__ __forceinline__ void fetch_block(const AttnParams& p, int bh, int t,
                                             v4i (&reg)[Staging<D, NW>::kRounds]) {
-  using L = TileLayout<D, NW>;
-  const v4i* kb = reinterpret_cast<const v4i*>(p.key_code + (static_cast<long>(bh) * p.sk64 + static_cast<long>(t) * kKeyBlock) * D);
-  const v4i* vb = reinterpret_cast<const v4i*>(p.value_code + (static_cast<long>(bh) * p.nkb + t) * static_cast<long>(D * kKeyBlock));
-  const v4i* lb = reinterpret_cast<const v4i*>(p.value_log2_scale + static_cast<long>(bh) * p.sk64 + t * kKeyBlock);
-  const v4i* ib = reinterpret_cast<const v4i*>(p.value_inv_multiplier + static_cast<long>(bh) * p.sk64 + t * kKeyBlock);
-  const v4i* cb = reinterpret_cast<const v4i*>(p.value_correction + (static_cast<long>(bh) * p.nkb + t) * D);
-  constexpr int kV = L::kChunksK;
-  constexpr int kL = kV + L::kChunksV;
-  constexpr int kI = kL + 16;
-  constexpr int kC = kI + 16;
+  const v4i* tile = reinterpret_cast<const v4i*>(p.kv_tiles + (static_cast<long>(bh) * p.nkb + t) * kv_tile_bytes(D));
 #pragma unroll
-  for (int r = 0; r < Staging<D, NW>::kRounds; ++r) {
-    const int i = staging_chunk<D, NW>(r);
-    const v4i* src = i < kV ? kb + i : i < kL ? vb + (i - kV) : i < kI ? lb + (i - kL) : i < kC ? ib + (i - kI) : cb + (i - kC);
-    reg[r] = *src;
-  }
+  for (int r = 0; r < Staging<D, NW>::kRounds; ++r) reg[r] = tile[staging_chunk<D, NW>(r)];
 }
 
 template <int D, int NW>
@@ -279,7 +268,8 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
 template <int D, int NW, bool kCausal>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                               const v4i (&qf)[D / 32], float cq, const float* key_scale, int q0,
-                                              int n, int h, int krow, v16i (&s_cur)[2], float (&num)[D / 32][16],
+                                              int n, int h, int krow, const v16i (&s_cur)[2], v16i (&s_next)[2],
+                                              float (&num)[D / 32][16],
                                               float& den, float& mref,
                                               v4i (&ready)[Staging<D, NW>::kRounds],
                                               v4i (&loading)[Staging<D, NW>::kRounds]) {
@@ -288,12 +278,9 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
   // unconditional (clamped) so every iteration issues the same loads: static vmcnt waits
   fetch_block<D, NW>(p, bh, min(t + 3, tiles - 1), loading);
   if (t < wave_tiles) {
-    v16i s_next[2];
     block_scores<D, NW>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, s_next);  // unused past the end
     block_update<D, NW, kCausal>(smem + (t % kStages) * L::kStageBytes, s_cur, cq * key_scale[t], t, q0, n, h, num,
                                  den, mref);
-    s_cur[0] = s_next[0];
-    s_cur[1] = s_next[1];
   }
   if (t + 2 < tiles) store_block<D, NW>(smem + ((t + 2) % kStages) * L::kStageBytes, ready);
   __syncthreads();
@@ -362,21 +349,21 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   fetch_block<D, NW>(p, bh, min(2, tiles - 1), reg_a);
   __syncthreads();
 
-  v16i s_cur[2];
-  if (wave_tiles > 0) block_scores<D, NW>(smem, qf, h, krow, s_cur);
+  v16i s_a[2], s_b[2];  // scores of the current and the next block, alternating
+  if (wave_tiles > 0) block_scores<D, NW>(smem, qf, h, krow, s_a);
 
   // Iteration t stores the set loaded at t - 1 and loads into the other one: unrolled by two
   // so both register sets keep static names.
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_cur, num,
-                                  den, mref, reg_a, reg_b);
-    pipeline_step<D, NW, kCausal>(p, smem, t + 1, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_cur,
+    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a, s_b,
+                                  num, den, mref, reg_a, reg_b);
+    pipeline_step<D, NW, kCausal>(p, smem, t + 1, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_b, s_a,
                                   num, den, mref, reg_b, reg_a);
   }
   if (t < tiles)
-    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_cur, num,
-                                  den, mref, reg_a, reg_b);
+    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a, s_b,
+                                  num, den, mref, reg_a, reg_b);
 
   // ---- epilogue: num / max(den, 1e-30) + mean(V), one query per lane ----
   const int query = q0 + n;

@@ -6,6 +6,10 @@
 
 namespace piper {
 
+// Bytes of one 64-key tile record: K codes, V^T codes, 64 log2 scales, 64 inverse
+// multipliers, D corrections.
+constexpr int kv_tile_bytes(int head_dim) { return 128 * head_dim + 512 + 4 * head_dim; }
+
 struct InputTensor {
   const void* data;  // 16-bit floats; the head_dim axis is contiguous
   long stride_batch;  // element strides
@@ -46,24 +50,16 @@ struct QuantParams {
   const float* value_mean;
   int8_t* query_code;
   float* query_scale;
-  int8_t* key_code;
   float* key_scale;
-  int8_t* value_code;
   float* value_scale;
-  float* value_log2_scale;
-  float* value_inv_multiplier;
-  int32_t* value_correction;
+  uint8_t* kv_tiles;  // [batch_heads][nkb][kv_tile_bytes(D)] (layout in piper_mi355x.h)
 };
 
 struct AttnParams {
   const int8_t* query_code;
   const float* query_scale;
-  const int8_t* key_code;
   const float* key_scale;
-  const int8_t* value_code;
-  const float* value_log2_scale;
-  const float* value_inv_multiplier;
-  const int32_t* value_correction;
+  const uint8_t* kv_tiles;
   const float* value_mean;
   void* output;
   int batch_heads;

@@ -206,9 +206,9 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
     const int kb = unit - bh * p.nkb;
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
-    quantize_block<kBf16, D, kKeyBlock, true>(
-        p.key, b, h, kb * kKeyBlock, p.key_length, p.key_mean + static_cast<long>(bh) * D,
-        p.key_code + (static_cast<long>(bh) * p.sk64 + kb * kKeyBlock) * D, p.key_scale + unit);
+    int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * kv_tile_bytes(D);
+    quantize_block<kBf16, D, kKeyBlock, true>(p.key, b, h, kb * kKeyBlock, p.key_length,
+                                              p.key_mean + static_cast<long>(bh) * D, tile, p.key_scale + unit);
     return;
   }
 
@@ -216,10 +216,9 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
   const int unit = (block - p.q_blocks_wg - p.k_blocks_wg) * 4 + wave;
   const bool active = unit < p.batch_heads * p.nkb;
   int8_t* lds = vt_lds[wave];
-  int bh = 0, kb = 0;
   if (active) {
-    bh = unit / p.nkb;
-    kb = unit - bh * p.nkb;
+    const int bh = unit / p.nkb;
+    const int kb = unit - bh * p.nkb;
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
     constexpr int kGroups = D / 8;
@@ -252,19 +251,21 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<int8_t>(code_of(f[i], scale));
       if (group == 0) {
-        const long k = static_cast<long>(bh) * p.sk64 + row;
-        p.value_scale[k] = valid ? scale : 0.0f;
-        p.value_log2_scale[k] = valid ? log2f(scale) : -__builtin_inff();
-        p.value_inv_multiplier[k] = valid ? 1.0f / (255.0f * scale) : 0.0f;
+        float* meta = reinterpret_cast<float*>(p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D) + 128 * D);
+        p.value_scale[static_cast<long>(bh) * p.sk64 + row] = valid ? scale : 0.0f;
+        meta[key_in_tile] = valid ? log2f(scale) : -__builtin_inff();
+        meta[kKeyBlock + key_in_tile] = valid ? 1.0f / (255.0f * scale) : 0.0f;
       }
     }
   }
   __syncthreads();
   if (!active) return;
   // transposed rows: lane owns features d = lane, lane + 64, ...
+  uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D);
+  int32_t* correction = reinterpret_cast<int32_t*>(tile + 128 * D + 512);
   for (int d = lane; d < D; d += kWave) {
     const uint4* src = reinterpret_cast<const uint4*>(lds + d * kVStride);
-    uint4* dst = reinterpret_cast<uint4*>(p.value_code + ((static_cast<long>(bh) * p.nkb + kb) * D + d) * kKeyBlock);
+    uint4* dst = reinterpret_cast<uint4*>(tile + 64 * D + d * kKeyBlock);
     int sum = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -275,7 +276,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
       sum = __builtin_amdgcn_sdot4(static_cast<int>(w.w), 0x01010101, sum, false);
       dst[j] = w;
     }
-    p.value_correction[(static_cast<long>(bh) * p.nkb + kb) * D + d] = 128 * sum;
+    correction[d] = 128 * sum;
   }
 }
 

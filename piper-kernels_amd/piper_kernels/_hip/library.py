@@ -56,15 +56,11 @@ class PiperPrepared(ctypes.Structure):
     _fields_ = [
         ("query_code", _ptr),
         ("query_scale", _ptr),
-        ("key_code", _ptr),
         ("key_scale", _ptr),
-        ("value_code", _ptr),
         ("value_scale", _ptr),
-        ("value_log2_scale", _ptr),
-        ("value_inv_multiplier", _ptr),
-        ("value_correction", _ptr),
         ("key_mean", _ptr),
         ("value_mean", _ptr),
+        ("kv_tiles", _ptr),
     ]
 
 
@@ -72,14 +68,18 @@ class PiperLayout(ctypes.Structure):
     _fields_ = [
         ("query_code_bytes", _i64),
         ("query_scale_bytes", _i64),
-        ("key_code_bytes", _i64),
         ("key_scale_bytes", _i64),
-        ("value_code_bytes", _i64),
-        ("value_key_array_bytes", _i64),
-        ("value_correction_bytes", _i64),
+        ("value_scale_bytes", _i64),
         ("mean_bytes", _i64),
+        ("kv_tile_bytes", _i64),
+        ("kv_tiles_bytes", _i64),
         ("workspace_bytes", _i64),
     ]
+
+
+def kv_tile_bytes(head_dim: int) -> int:
+    """Bytes of one 64-key tile record (PIPER_KV_TILE_BYTES in the C header)."""
+    return 128 * head_dim + 512 + 4 * head_dim
 
 
 class PiperPrepareArgs(ctypes.Structure):

@@ -28,15 +28,11 @@ class PreparedPiperAttention:
 
     query_code: torch.Tensor  # int8 [B, H, Sq32, D]
     query_scale: torch.Tensor  # fp32 [B, H, Sq32/32]
-    key_code: torch.Tensor  # int8 [B, H, Sk64, D]
     key_scale: torch.Tensor  # fp32 [B, H, Sk64/64]
-    value_code: torch.Tensor  # int8 [B, H, Sk64/64, D, 64] (V^T per 64-key tile)
     value_scale: torch.Tensor  # fp32 [B, H, Sk64]
-    value_log2_scale: torch.Tensor  # fp32 [B, H, Sk64]
-    value_inv_multiplier: torch.Tensor  # fp32 [B, H, Sk64]
-    value_correction: torch.Tensor  # int32 [B, H, Sk64/64, D]
     key_mean: torch.Tensor  # fp32 [B, H, D]
     value_mean: torch.Tensor  # fp32 [B, H, D]
+    kv_tiles: torch.Tensor  # uint8 [B, H, Sk64/64, kv_tile_bytes(D)]: K, V^T, log2 scale, 1/(255 s), 128 colsum
     output: torch.Tensor  # [B, H, Sq, D] in the input dtype
     shape: tuple[int, int, int, int, int]  # B, H, Sq, Sk, D
     scale: float
@@ -47,16 +43,34 @@ class PreparedPiperAttention:
         return native.PiperPrepared(
             self.query_code.data_ptr(),
             self.query_scale.data_ptr(),
-            self.key_code.data_ptr(),
             self.key_scale.data_ptr(),
-            self.value_code.data_ptr(),
             self.value_scale.data_ptr(),
-            self.value_log2_scale.data_ptr(),
-            self.value_inv_multiplier.data_ptr(),
-            self.value_correction.data_ptr(),
             self.key_mean.data_ptr(),
             self.value_mean.data_ptr(),
+            self.kv_tiles.data_ptr(),
         )
+
+    # views into the tile records (for inspection and tests)
+    def key_code(self) -> torch.Tensor:
+        b, h, _, _, d = self.shape
+        return self.kv_tiles[..., : 64 * d].view(torch.int8).reshape(b, h, -1, 64, d).reshape(b, h, -1, d)
+
+    def value_code_transposed(self) -> torch.Tensor:
+        """V codes as stored: [B, H, Sk64/64, D, 64]."""
+        b, h, _, _, d = self.shape
+        return self.kv_tiles[..., 64 * d : 128 * d].view(torch.int8).reshape(b, h, -1, d, 64)
+
+    def value_log2_scale(self) -> torch.Tensor:
+        d = self.shape[4]
+        return self.kv_tiles[..., 128 * d : 128 * d + 256].contiguous().view(torch.float32).flatten(2)
+
+    def value_inv_multiplier(self) -> torch.Tensor:
+        d = self.shape[4]
+        return self.kv_tiles[..., 128 * d + 256 : 128 * d + 512].contiguous().view(torch.float32).flatten(2)
+
+    def value_correction(self) -> torch.Tensor:
+        d = self.shape[4]
+        return self.kv_tiles[..., 128 * d + 512 :].contiguous().view(torch.int32)
 
 
 def _native_input(tensor: torch.Tensor) -> tuple[torch.Tensor, native.PiperTensor]:
@@ -101,15 +115,11 @@ def _prepare_piper_attention(
     prepared = PreparedPiperAttention(
         query_code=empty((batch, heads, sq32, d), torch.int8),
         query_scale=empty((batch, heads, sq32 // native.QUERY_BLOCK), torch.float32),
-        key_code=empty((batch, heads, sk64, d), torch.int8),
         key_scale=empty((batch, heads, nkb), torch.float32),
-        value_code=empty((batch, heads, nkb, d, native.KEY_BLOCK), torch.int8),
         value_scale=empty((batch, heads, sk64), torch.float32),
-        value_log2_scale=empty((batch, heads, sk64), torch.float32),
-        value_inv_multiplier=empty((batch, heads, sk64), torch.float32),
-        value_correction=empty((batch, heads, nkb, d), torch.int32),
         key_mean=empty((batch, heads, d), torch.float32),
         value_mean=empty((batch, heads, d), torch.float32),
+        kv_tiles=empty((batch, heads, nkb, native.kv_tile_bytes(d)), torch.uint8),
         output=empty((batch, heads, sq, d), query.dtype),
         shape=(batch, heads, sq, sk, d),
         scale=float(scale),

@@ -63,19 +63,18 @@ def gpu_attention(prepared, dtype=torch.float32) -> torch.Tensor:
 
 def prepared_numpy(prepared) -> dict:
     b, h, sq, sk, d = prepared.shape
-    nkb = -(-sk // 64)
-    vcode = prepared.value_code.cpu().numpy()  # [B,H,nkb,D,64]
-    vcode = vcode.transpose(0, 1, 2, 4, 3).reshape(b, h, nkb * 64, d)
+    vcode = prepared.value_code_transposed().cpu().numpy()  # [B,H,nkb,D,64]
+    vcode = vcode.transpose(0, 1, 2, 4, 3).reshape(b, h, -1, d)
     return {
         "query_code_padded": prepared.query_code.cpu().numpy(),
         "query_block_scale": prepared.query_scale.cpu().numpy(),
-        "key_code_padded": prepared.key_code.cpu().numpy(),
+        "key_code_padded": prepared.key_code().cpu().numpy(),
         "key_block_scale": prepared.key_scale.cpu().numpy(),
         "value_code_padded": vcode,
         "value_scale_padded": prepared.value_scale.cpu().numpy(),
-        "value_log2_scale": prepared.value_log2_scale.cpu().numpy(),
-        "value_inv_multiplier": prepared.value_inv_multiplier.cpu().numpy(),
-        "value_correction": prepared.value_correction.cpu().numpy(),
+        "value_log2_scale": prepared.value_log2_scale().cpu().numpy(),
+        "value_inv_multiplier": prepared.value_inv_multiplier().cpu().numpy(),
+        "value_correction": prepared.value_correction().cpu().numpy(),
         "key_mean": prepared.key_mean.cpu().numpy(),
         "value_mean": prepared.value_mean.cpu().numpy(),
     }

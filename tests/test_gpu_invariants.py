@@ -53,7 +53,7 @@ def test_large_value_scale_stays_finite(gfx950_device) -> None:
     v[:, :, 0] = 40000
     prepared = gpu_prepare(q, k, v, 64**-0.5, False, gfx950_device)
     out = gpu_attention(prepared, torch.float16)
-    assert torch.isfinite(prepared.value_inv_multiplier).all()
+    assert torch.isfinite(prepared.value_inv_multiplier()).all()
     assert torch.isfinite(out).all()
 
 

@@ -73,11 +73,12 @@ def test_prepared_layout_sizes(lib, shape) -> None:
     sq32, sk64 = -(-sq // 32) * 32, -(-sk // 64) * 64
     assert layout.query_code_bytes == b * h * sq32 * d
     assert layout.query_scale_bytes == b * h * (sq32 // 32) * 4
-    assert layout.key_code_bytes == layout.value_code_bytes == b * h * sk64 * d
     assert layout.key_scale_bytes == b * h * (sk64 // 64) * 4
-    assert layout.value_key_array_bytes == b * h * sk64 * 4
-    assert layout.value_correction_bytes == b * h * (sk64 // 64) * d * 4
+    assert layout.value_scale_bytes == b * h * sk64 * 4
     assert layout.mean_bytes == b * h * d * 4
+    # one record per 64-key tile: K codes, V^T codes, 64 log2 scales, 64 inverse multipliers, D corrections
+    assert layout.kv_tile_bytes == native.kv_tile_bytes(d) == 64 * d + d * 64 + 256 + 256 + 4 * d
+    assert layout.kv_tiles_bytes == b * h * (sk64 // 64) * layout.kv_tile_bytes
     assert layout.workspace_bytes == 2 * b * h * (-(-sk // 64)) * d * 8
 
 
