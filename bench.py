@@ -43,7 +43,7 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    parser.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     return parser.parse_args()
 
 
@@ -59,7 +59,11 @@ def traffic_from_profile(workload: str):
 
 
 def cpu_baseline(workload, seconds: float) -> dict:
-    """Time the CPU oracle (prep of one head + the streaming loop over a row slice)."""
+    """Time the CPU oracle on whole (batch 0) heads of the workload until ~`seconds` elapse.
+
+    Each head is the full reference computation for that head: prep (means, Q/K/V codes) and
+    the 64-key streaming loop over every query row, numpy on one thread.
+    """
     import platform
 
     import numpy as np
@@ -69,38 +73,28 @@ def cpu_baseline(workload, seconds: float) -> dict:
     from piper_kernels.measure import attention_operations
     from piper_kernels.workloads import make_inputs
 
-    q, k, v = make_inputs(workload, heads=[0], batches=[0])
     scale = workload.head_dim**-0.5
+    heads = 0
+    elapsed = 0.0
     with threadpool_limits(limits=1):
-        # calibrate on a small slice, then size the timed slice to ~`seconds`
-        prep = oracle.prepare(q, k, v, workload.is_causal, "per_thread")
-        rows = 64
-
-        def run(rows: int) -> float:
-            sub = dict(prep)
-            for key in ("query_code", "query_scale"):
-                sub[key] = prep[key][:, :, :rows]
+        while heads < workload.heads and (heads == 0 or elapsed < seconds):
+            q, k, v = make_inputs(workload, heads=[heads], batches=[0])
             start = time.perf_counter()
-            oracle.attention_from_prepared(sub, scale, workload.is_causal)
-            return time.perf_counter() - start
-
-        per_row = run(rows) / rows
-        rows = int(max(64, min(workload.query_length, seconds / max(per_row, 1e-9))))
-        start = time.perf_counter()
-        prep = oracle.prepare(q, k, v, workload.is_causal, "per_thread")
-        prep_s = time.perf_counter() - start
-        loop_s = run(rows)
-    total = prep_s + loop_s
-    ops = attention_operations(1, 1, rows, workload.key_length, workload.head_dim, workload.is_causal)
+            oracle.piper_attention_reference(q, k, v, scale, workload.is_causal, "per_thread")
+            elapsed += time.perf_counter() - start
+            heads += 1
+            log(f"[bench] cpu baseline: {heads} head(s), {elapsed:.1f} s")
+    ops = attention_operations(1, heads, workload.query_length, workload.key_length, workload.head_dim,
+                               workload.is_causal)
     return {
-        "value": ops / total / 1e12,
+        "value": ops / elapsed / 1e12,
         "unit": "TOPS",
         "cores": 1,
         "kind": "port",
         "sample": (
-            f"{workload.name} batch 0 head 0: prep of the full head (S={workload.key_length}) + "
-            f"the 64-key streaming loop for {rows} of {workload.query_length} query rows; "
-            f"{total:.1f} s wall; numpy {np.__version__}, 1 BLAS thread; "
+            f"{workload.name}: {heads} of {workload.batch * workload.heads} (batch, head) slices, each the full "
+            f"reference computation (K/V means, per_thread Q/K codes, V codes, 64-key streaming loop over all "
+            f"{workload.query_length} query rows); {elapsed:.1f} s wall; numpy {np.__version__} on 1 thread; "
             f"cpu={platform.processor() or platform.machine()} os.cpu_count={os.cpu_count()}"
         ),
     }

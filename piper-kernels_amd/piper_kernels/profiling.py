@@ -1,0 +1,65 @@
+"""Focused GPU workloads for rocprofv3 runs (kernel traces and PMC counters).
+
+    python -m piper_kernels.profiling attention --workload c3 --launches 3
+        prepare one workload once, then launch only the fused attention kernel
+    python -m piper_kernels.profiling prep --workload c3 --launches 3
+        run only the prep pipeline (mean partials, mean finalisation, quantisation)
+    python -m piper_kernels.profiling copy --bytes 1073741824 --launches 3
+        a plain device-to-device copy of a known size: the calibration that turns
+        FETCH_SIZE / WRITE_SIZE counter readings into bytes
+
+Run it from the repository root with ``piper-kernels_amd`` on ``sys.path`` (as below), e.g.
+``rocprofv3 --pmc FETCH_SIZE --kernel-include-regex attention_kernel -- python -m
+piper_kernels.profiling attention --workload c3``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("what", choices=["attention", "prep", "copy"])
+    parser.add_argument("--workload", default="c3")
+    parser.add_argument("--launches", type=int, default=3)
+    parser.add_argument("--bytes", type=int, default=1 << 30)
+    args = parser.parse_args(argv)
+
+    import torch
+
+    from piper_kernels.attention.piper_attention.hip import _launch_piper_attention, _prepare_piper_attention
+    from piper_kernels.workloads import WORKLOADS, make_inputs
+
+    device = torch.device("cuda", 0)
+    if args.what == "copy":
+        src = torch.empty(args.bytes // 4, dtype=torch.float32, device=device).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(args.launches):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copied {args.bytes} bytes x {args.launches}", flush=True)
+        return 0
+    w = WORKLOADS[args.workload]
+    q, k, v = make_inputs(w, device)
+    scale = w.head_dim**-0.5
+    with torch.no_grad():
+        prepared = _prepare_piper_attention(q, k, v, scale, w.is_causal)
+        for _ in range(args.launches):
+            if args.what == "attention":
+                _launch_piper_attention(prepared)
+            else:
+                _prepare_piper_attention(q, k, v, scale, w.is_causal)
+    torch.cuda.synchronize()
+    print(f"{args.what} {args.workload} x {args.launches} done", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
