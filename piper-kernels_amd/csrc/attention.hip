@@ -261,38 +261,39 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   }
 }
 
-// One loop iteration for one wave: consume block t (LDS stage t % 4), issue the QK MFMAs of
-// block t + 1 first so they run under the softmax VALU work, then write block t + 2 (loaded
-// into `ready` during the previous iteration) to stage (t + 2) % 4 and start loading block
-// t + 3 into `loading`.  Global loads therefore have two iterations to arrive.
-template <int D, int NW, bool kCausal>
+// LDS ring of kStages tile records.  Iteration t consumes block t (stage t % kStages), issues
+// the QK MFMAs of block t + 1 first so they run under the softmax VALU work, writes block
+// t + kLead (loaded into `ready` one iteration earlier) and starts loading block t + kLead + 1
+// into `loading`.  A workgroup barrier follows every second iteration only: with a write lead
+// of 3 and 5 stages, every written stage is separated from its first read (QK at iteration
+// t + kLead - 1) and from its previous reads (iteration t + kLead - kStages) by a barrier.
+constexpr int kStages = 5;
+constexpr int kLead = 3;
+
+template <int D, int NW, bool kCausal, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                               const v4i (&qf)[D / 32], float cq, const float* key_scale, int q0,
                                               int n, int h, int krow, const v16i (&s_cur)[2], v16i (&s_next)[2],
-                                              float (&num)[D / 32][16],
-                                              float& den, float& mref,
+                                              float (&num)[D / 32][16], float& den, float& mref,
                                               v4i (&ready)[Staging<D, NW>::kRounds],
                                               v4i (&loading)[Staging<D, NW>::kRounds]) {
   using L = TileLayout<D, NW>;
-  constexpr int kStages = 4;
   // unconditional (clamped) so every iteration issues the same loads: static vmcnt waits
-  fetch_block<D, NW>(p, bh, min(t + 3, tiles - 1), loading);
+  fetch_block<D, NW>(p, bh, min(t + kLead + 1, tiles - 1), loading);
   if (t < wave_tiles) {
     block_scores<D, NW>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, s_next);  // unused past the end
     block_update<D, NW, kCausal>(smem + (t % kStages) * L::kStageBytes, s_cur, cq * key_scale[t], t, q0, n, h, num,
                                  den, mref);
   }
-  if (t + 2 < tiles) store_block<D, NW>(smem + ((t + 2) % kStages) * L::kStageBytes, ready);
-  __syncthreads();
+  if (t + kLead < tiles) store_block<D, NW>(smem + ((t + kLead) % kStages) * L::kStageBytes, ready);
+  if constexpr (kBarrier) __syncthreads();
 }
 
-// K/V blocks stream through a 4-stage LDS ring, staged through two alternating register sets.
 template <int D, int NW, bool kCausal, int kOut>
 __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams p) {
   using L = TileLayout<D, NW>;
   using S = Staging<D, NW>;
   constexpr int kChunksD = D / 32;
-  constexpr int kStages = 4;
   __shared__ __attribute__((aligned(16))) char smem[kStages * L::kStageBytes];
 
   const int lane = threadIdx.x & 63;
@@ -339,31 +340,33 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
   const float* key_scale = p.key_scale + static_cast<long>(bh) * p.nkb;
 
-  // prologue: blocks 0 and 1 into LDS, block 2 into registers
+  // prologue: blocks 0 .. kLead-1 into LDS (missing blocks repeat the last one), block kLead
+  // into registers
   v4i reg_a[S::kRounds];
   v4i reg_b[S::kRounds];
-  fetch_block<D, NW>(p, bh, 0, reg_a);
-  fetch_block<D, NW>(p, bh, min(1, tiles - 1), reg_b);
-  store_block<D, NW>(smem, reg_a);
-  store_block<D, NW>(smem + L::kStageBytes, reg_b);  // a copy of block 0 when there is one block
-  fetch_block<D, NW>(p, bh, min(2, tiles - 1), reg_a);
+#pragma unroll
+  for (int b = 0; b < kLead; ++b) {
+    fetch_block<D, NW>(p, bh, min(b, tiles - 1), reg_a);
+    store_block<D, NW>(smem + b * L::kStageBytes, reg_a);
+  }
+  fetch_block<D, NW>(p, bh, min(kLead, tiles - 1), reg_a);
   __syncthreads();
 
   v16i s_a[2], s_b[2];  // scores of the current and the next block, alternating
   if (wave_tiles > 0) block_scores<D, NW>(smem, qf, h, krow, s_a);
 
-  // Iteration t stores the set loaded at t - 1 and loads into the other one: unrolled by two
-  // so both register sets keep static names.
+  // Iteration t stores the register set loaded at t - 1 and loads into the other one:
+  // unrolled by two so both register sets keep static names; one barrier per pair.
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a, s_b,
-                                  num, den, mref, reg_a, reg_b);
-    pipeline_step<D, NW, kCausal>(p, smem, t + 1, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_b, s_a,
-                                  num, den, mref, reg_b, reg_a);
+    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a,
+                                         s_b, num, den, mref, reg_a, reg_b);
+    pipeline_step<D, NW, kCausal, true>(p, smem, t + 1, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_b,
+                                        s_a, num, den, mref, reg_b, reg_a);
   }
   if (t < tiles)
-    pipeline_step<D, NW, kCausal>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a, s_b,
-                                  num, den, mref, reg_a, reg_b);
+    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a,
+                                         s_b, num, den, mref, reg_a, reg_b);
 
   // ---- epilogue: num / max(den, 1e-30) + mean(V), one query per lane ----
   const int query = q0 + n;
