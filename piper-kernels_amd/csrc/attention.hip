@@ -301,7 +301,8 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   const int h = lane >> 5;  // lane half
   const int n = lane & 31;  // query column within the wave
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int qtile = logical % p.query_tiles;
+  // causal: the longest query tiles (most key blocks) are dispatched first
+  const int qtile = kCausal ? p.query_tiles - 1 - logical % p.query_tiles : logical % p.query_tiles;
   const int bh = logical / p.query_tiles;
   const int q0 = qtile * (NW * 32) + wave * 32;  // first query of this wave
   const bool wave_live = q0 < p.query_length;

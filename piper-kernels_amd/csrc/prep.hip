@@ -69,8 +69,8 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
 
 // Means, pass 2: sum the chunk partials of one (tensor, batch-head, column) in chunk order,
 // divide by the length in FP64 and round to FP32.  Causal calls write a zero V mean.
-__global__ void __launch_bounds__(256) mean_finalize_kernel(const MeanParams p, int head_dim) {
-  const int gid = blockIdx.x * 256 + threadIdx.x;
+__global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, int head_dim) {
+  const int gid = blockIdx.x * 64 + threadIdx.x;
   const int per_tensor = p.batch_heads * head_dim;
   if (gid >= 2 * per_tensor) return;
   const int tensor = gid / per_tensor;
@@ -83,8 +83,18 @@ __global__ void __launch_bounds__(256) mean_finalize_kernel(const MeanParams p, 
   const int bh = rem / head_dim;
   const int d = rem - bh * head_dim;
   const double* src = p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks * head_dim + d;
+  // 16 loads in flight per step; the additions stay in chunk order
+  constexpr int kBatch = 16;
   double total = 0.0;
-  for (int c = 0; c < p.chunks; ++c) total += src[static_cast<long>(c) * head_dim];
+  int c = 0;
+  for (; c + kBatch <= p.chunks; c += kBatch) {
+    double part[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) part[i] = src[static_cast<long>(c + i) * head_dim];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) total += part[i];
+  }
+  for (; c < p.chunks; ++c) total += src[static_cast<long>(c) * head_dim];
   dst[rem] = static_cast<float>(total / static_cast<double>(p.length));
 }
 
@@ -291,7 +301,7 @@ static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp,
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int fin_threads = 2 * mp.batch_heads * D;
-  hipLaunchKernelGGL(mean_finalize_kernel, dim3((fin_threads + 255) / 256), dim3(256), 0, stream, mp, D);
+  hipLaunchKernelGGL(mean_finalize_kernel, dim3((fin_threads + 63) / 64), dim3(64), 0, stream, mp, D);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int blocks = qp.q_blocks_wg + qp.k_blocks_wg + qp.v_blocks_wg;
