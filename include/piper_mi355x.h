@@ -91,8 +91,10 @@ typedef struct piper_tensor {
  *                                      padding zero
  *       [128*D, 128*D + 256)     float log2(value_scale) of the 64 keys (padding -inf)
  *       [128*D + 256, +512)      float 1 / (255 * value_scale) (padding 0)
- *       [128*D + 512, +4*D)      int32 128 * (sum over the 64 keys of the V codes), per
- *                                      feature: the affine correction of the PV product
+ *       [128*D + 512, +4*D)      int32 0x4B400000 + 128 * (sum over the 64 keys of the V
+ *                                      codes), per feature: the affine correction of the PV
+ *                                      product plus the bias that makes the integer result
+ *                                      readable as FP32 1.5 * 2^23 + PV
  */
 #define PIPER_KV_TILE_BYTES(head_dim) (128 * (head_dim) + 512 + 4 * (head_dim))
 

@@ -256,8 +256,14 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
     const v4i a1 = *reinterpret_cast<const v4i*>(vrow + 32);
     acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, p0, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, p1, acc, 0, 0, 0);
+    // acc started from the biased correction: its bits are 1.5 * 2^23 + (u @ v) exactly.
+    // (The element goes through a scalar first: this clang's __builtin_bit_cast of an
+    // ext_vector subscript reads element 0.)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) num[j][r] = fmaf(static_cast<float>(acc[r]), weight, num[j][r]);
+    for (int r = 0; r < 16; ++r) {
+      const int bits = acc[r];
+      num[j][r] = fmaf(__builtin_bit_cast(float, bits) - kAccBiasValue, weight, num[j][r]);
+    }
   }
 }
 

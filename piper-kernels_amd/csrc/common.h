@@ -14,6 +14,11 @@ constexpr int kQueryBlock = 32;  // rows per Q scale (sage/reference.py:6)
 constexpr int kKeyBlock = 64;    // rows per K scale and keys per P block (reference.py:16)
 constexpr int kMeanChunk = 64;   // rows per FP64 partial of the order-defined mean
 constexpr float kLog2e = 1.4426950408889634f;
+// Integer accumulators that start from kAccBias read, as FP32 bits, 1.5 * 2^23 + value exactly
+// while |value| < 2^22: the FP32 mantissa at [2^23, 2^24) has unit spacing.  Subtracting
+// kAccBiasValue (exact) replaces an i32 -> f32 conversion with a plain FP32 subtraction.
+constexpr int kAccBias = 0x4B400000;
+constexpr float kAccBiasValue = 12582912.0f;  // 1.5 * 2^23
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));

@@ -286,7 +286,8 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
       sum = __builtin_amdgcn_sdot4(static_cast<int>(w.w), 0x01010101, sum, false);
       dst[j] = w;
     }
-    correction[d] = 128 * sum;
+    // |PV| <= 64 * 255 * 127 < 2^22, so the biased accumulator stays exact (common.h)
+    correction[d] = 128 * sum + kAccBias;
   }
 }
 

@@ -20,6 +20,7 @@ from ..._hip import library as native
 from ._plan import MI355XPlan, select_plan
 
 _DTYPE_CODES = {torch.float16: native.FLOAT16, torch.bfloat16: native.BFLOAT16, torch.float32: native.FLOAT32}
+ACC_BIAS = 0x4B400000  # integer accumulator bias: bits read as FP32 1.5 * 2^23 + value
 
 
 @dataclass(frozen=True)
@@ -69,8 +70,9 @@ class PreparedPiperAttention:
         return self.kv_tiles[..., 128 * d + 256 : 128 * d + 512].contiguous().view(torch.float32).flatten(2)
 
     def value_correction(self) -> torch.Tensor:
+        """128 * column sums of the V codes per tile (the stored words carry a 0x4B400000 bias)."""
         d = self.shape[4]
-        return self.kv_tiles[..., 128 * d + 512 :].contiguous().view(torch.int32)
+        return self.kv_tiles[..., 128 * d + 512 :].contiguous().view(torch.int32) - ACC_BIAS
 
 
 def _native_input(tensor: torch.Tensor) -> tuple[torch.Tensor, native.PiperTensor]:
