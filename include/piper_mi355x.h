@@ -85,18 +85,27 @@ typedef struct piper_tensor {
  *   key_mean       float   [B, H, D]         order-defined sequence mean of K
  *   value_mean     float   [B, H, D]         same for V; zeros when causal
  *   kv_tiles       bytes   [B, H, nkb, PIPER_KV_TILE_BYTES(D)]: one self-contained record
- *                  per 64-key tile, in the order the attention kernel stages it into LDS:
- *       [0, 64*D)                int8  K codes of K - mean(K), [64 keys][D]; padding zero
- *       [64*D, 128*D)            int8  V codes of V - mean(V), transposed: [D][64 keys];
- *                                      padding zero
- *       [128*D, 128*D + 256)     float log2(value_scale) of the 64 keys (padding -inf)
- *       [128*D + 256, +512)      float 1 / (255 * value_scale) (padding 0)
- *       [128*D + 512, +4*D)      int32 0x4B400000 + 128 * (sum over the 64 keys of the V
+ *                  per 64-key tile, byte for byte the LDS stage of the attention kernel (it is
+ *                  copied with direct global -> LDS loads in 1 KiB pieces):
+ *       [0, 64*(D+16))           int8  K codes of K - mean(K), [64 keys][D], rows of D + 16
+ *                                      bytes (padding rows of short tiles are zero codes);
+ *                                      bytes [D, D+4) of row 0 hold the tile's K scale (FP32)
+ *       [PIPER_KV_V_OFFSET(D), +80*D)
+ *                                int8  V codes of V - mean(V), transposed: [D][64 keys], rows
+ *                                      of 80 bytes
+ *       [PIPER_KV_LOG2_OFFSET(D), +256)  float log2(value_scale) of the 64 keys (padding -inf)
+ *       [.. + 256, +256)         float 1 / (255 * value_scale) (padding 0)
+ *       [.. + 512, +4*D)         int32 0x4B400000 + 128 * (sum over the 64 keys of the V
  *                                      codes), per feature: the affine correction of the PV
  *                                      product plus the bias that makes the integer result
  *                                      readable as FP32 1.5 * 2^23 + PV
+ *                  Any other byte (row padding, the tail up to the KiB multiple) is
+ *                  unspecified.
  */
-#define PIPER_KV_TILE_BYTES(head_dim) (128 * (head_dim) + 512 + 4 * (head_dim))
+#define PIPER_KV_V_OFFSET(head_dim) (64 * ((head_dim) + 16))
+#define PIPER_KV_LOG2_OFFSET(head_dim) (PIPER_KV_V_OFFSET(head_dim) + 80 * (head_dim))
+#define PIPER_KV_TILE_BYTES(head_dim) \
+  ((PIPER_KV_LOG2_OFFSET(head_dim) + 512 + 4 * (head_dim) + 1023) / 1024 * 1024)
 
 typedef struct piper_prepared {
   int8_t* query_code;

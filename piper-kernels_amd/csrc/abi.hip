@@ -10,6 +10,13 @@
 #include "kernels.h"
 #include "piper_mi355x.h"
 
+// The tile record documented in the header is the layout the kernels use.
+static_assert(PIPER_KV_TILE_BYTES(64) == piper::kv_tile_bytes(64), "tile record size (D = 64)");
+static_assert(PIPER_KV_TILE_BYTES(128) == piper::kv_tile_bytes(128), "tile record size (D = 128)");
+static_assert(PIPER_KV_V_OFFSET(128) == piper::kv_v_offset(128), "V^T offset");
+static_assert(PIPER_KV_LOG2_OFFSET(128) == piper::kv_log_offset(128), "log2 offset");
+static_assert(PIPER_KV_LOG2_OFFSET(64) == piper::kv_log_offset(64), "log2 offset");
+
 namespace {
 
 thread_local char g_last_error[512] = "";

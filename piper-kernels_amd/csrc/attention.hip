@@ -18,8 +18,9 @@
 // * O^T = V^T P^T on the same MFMA with the affine correction 128*colsum(v) as the
 //   accumulator input; v_cvt_pk_u8_f32 rounds half-to-even and saturates to [0, 255], which
 //   is round().clamp(0, 255) of the reference.
-// * K, V^T, per-key log2 scales, inverse multipliers and column sums of a tile are staged in
-//   LDS (double-buffered, padded rows against bank conflicts) with 16-byte global loads.
+// * K, V^T, per-key log2 scales, inverse multipliers and column sums of a tile form one
+//   record laid out exactly like its LDS stage (padded rows against bank conflicts); it is
+//   copied with direct global -> LDS loads into a 6-stage ring, 4 blocks ahead.
 #include "common.h"
 #include "kernels.h"
 
@@ -30,62 +31,61 @@ constexpr float kLog2Of255 = 7.994353436858858f;   // log2(255)
 
 template <int D, int NW>
 struct TileLayout {
-  static constexpr int kThreads = NW * kWave;
-  static constexpr int kKStride = D + 16;       // bytes per K row in LDS
-  static constexpr int kVStride = kKeyBlock + 16;  // bytes per V^T row in LDS
-  static constexpr int kKBytes = kKeyBlock * kKStride;
-  static constexpr int kVBytes = D * kVStride;
-  static constexpr int kLogOffset = kKBytes + kVBytes;  // 64 floats: log2 of V row scales
-  static constexpr int kInvOffset = kLogOffset + 256;   // 64 floats: 1 / (255 * scale)
-  static constexpr int kCorrOffset = kInvOffset + 256;  // D ints: 128 * colsum
-  static constexpr int kStageBytes = kCorrOffset + 4 * D;
-  static constexpr int kChunksK = kKeyBlock * D / 16;  // 16-byte chunks per region
-  static constexpr int kChunksV = D * kKeyBlock / 16;
-  static constexpr int kChunks = kChunksK + kChunksV + 16 + 16 + D / 4;
-  static constexpr int kRounds = (kChunks + kThreads - 1) / kThreads;
-  static_assert(kChunks * 16 == kv_tile_bytes(D), "LDS stage order must match the tile record");
+  static constexpr int kKStride = kv_k_stride(D);  // bytes per K row in LDS
+  static constexpr int kVStride = kv_v_stride();   // bytes per V^T row in LDS
+  static constexpr int kKBytes = kv_v_offset(D);
+  static constexpr int kLogOffset = kv_log_offset(D);  // 64 floats: log2 of V row scales
+  static constexpr int kInvOffset = kv_inv_offset(D);  // 64 floats: 1 / (255 * scale)
+  static constexpr int kCorrOffset = kv_corr_offset(D);  // D ints: biased 128 * colsum
+  static constexpr int kStageBytes = kv_tile_bytes(D);  // the tile record is the stage image
+  static constexpr int kPieces = kStageBytes / 1024;    // 1 KiB per wave-wide 16-byte load
+  static constexpr int kRounds = (kPieces + NW - 1) / NW;
+  static constexpr int kFullWaves = kPieces % NW == 0 ? NW : kPieces % NW;  // waves with kRounds pieces
 };
 
-// Global -> register -> LDS staging of one 64-key block: kRounds 16-byte chunks per thread.
-// Branch-free on purpose: a per-lane branch around a load makes the compiler wait for it at
-// the reconvergence point, which would serialise the prefetch.  Threads past the last chunk
-// load and store the last chunk again (identical data, benign).
-template <int D, int NW>
-struct Staging {
-  using L = TileLayout<D, NW>;
-  static constexpr int kRounds = (L::kChunks + L::kThreads - 1) / L::kThreads;
-};
-
-template <int D, int NW>
-__device__ __forceinline__ int staging_chunk(int r) {
-  using L = TileLayout<D, NW>;
-  const int c = threadIdx.x + r * L::kThreads;
-  return c < L::kChunks ? c : L::kChunks - 1;
+// One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from its global address to
+// LDS byte lds + 16 * i.  Issued as inline assembly so that the compiler's wait insertion does
+// not treat every later LDS read as dependent on it: the waits are explicit (stage_barrier,
+// and a drain before the waves end).
+__device__ __forceinline__ void copy_piece(const void* src, uint32_t lds) {
+  // s_nop: one wait state between the SALU write of M0 and the LDS DMA that reads it
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
-// Loads the tile record of block t (t must be a valid block index): a uniform base address
-// plus a loop-invariant per-thread offset, so the loop spends no VALU on addressing.
-template <int D, int NW>
-__device__ __forceinline__ void fetch_block(const AttnParams& p, int bh, int t,
-                                            v4i (&reg)[Staging<D, NW>::kRounds]) {
-  const v4i* tile = reinterpret_cast<const v4i*>(p.kv_tiles + (static_cast<long>(bh) * p.nkb + t) * kv_tile_bytes(D));
-#pragma unroll
-  for (int r = 0; r < Staging<D, NW>::kRounds; ++r) reg[r] = tile[staging_chunk<D, NW>(r)];
+__device__ __forceinline__ uint32_t lds_address(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
 }
 
+// Direct global -> LDS copy of the tile record of block t into one LDS stage: wave w copies
+// 1 KiB pieces w, w + NW, ... (each lane 16 bytes), so the per-lane addresses are loop
+// invariant and no VGPRs hold staged data.  Completion is tracked by this wave's vmcnt.
 template <int D, int NW>
-__device__ __forceinline__ void store_block(char* stage, const v4i (&reg)[Staging<D, NW>::kRounds]) {
+__device__ __forceinline__ void copy_block(const AttnParams& p, char* stage, int bh, int t, int wave, int lane) {
   using L = TileLayout<D, NW>;
+  const char* tile = reinterpret_cast<const char*>(p.kv_tiles) + (static_cast<long>(bh) * p.nkb + t) * L::kStageBytes;
+  const uint32_t base = lds_address(stage);
 #pragma unroll
-  for (int r = 0; r < Staging<D, NW>::kRounds; ++r) {
-    const int i = staging_chunk<D, NW>(r);
-    const int j = i - L::kChunksK;
-    const int k_dst = (i / (D / 16)) * L::kKStride + (i % (D / 16)) * 16;
-    const int v_dst = L::kKBytes + (j >> 2) * L::kVStride + (j & 3) * 16;
-    const int x_dst = L::kLogOffset + (j - L::kChunksV) * 16;  // log2, inv and corr are contiguous
-    const int dst = i < L::kChunksK ? k_dst : j < L::kChunksV ? v_dst : x_dst;
-    *reinterpret_cast<v4i*>(stage + dst) = reg[r];
+  for (int r = 0; r < L::kRounds; ++r) {
+    const int piece = wave + r * NW;  // wave-uniform: a scalar branch
+    if (piece < L::kPieces) copy_piece(tile + piece * 1024 + lane * 16, base + piece * 1024);
   }
+}
+
+// Workgroup barrier that lets this wave's newest kInFlight direct loads stay in flight.
+// (__syncthreads would drain every outstanding load.)  LDS reads are waited for as well, so
+// a stage is never overwritten under a pending read.
+template <int kInFlight>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kInFlight) : "memory");
+}
+
+template <int D, int NW>
+__device__ __forceinline__ void stage_barrier_keep_last(int wave) {
+  using L = TileLayout<D, NW>;
+  if (wave < L::kFullWaves)
+    stage_barrier<L::kRounds>();
+  else
+    stage_barrier<L::kRounds - 1>();
 }
 
 // Balanced max over 32 values (depth 4 instead of a 16-long v_max3 chain).
@@ -268,37 +268,38 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
 }
 
 // LDS ring of kStages tile records.  Iteration t consumes block t (stage t % kStages), issues
-// the QK MFMAs of block t + 1 first so they run under the softmax VALU work, writes block
-// t + kLead (loaded into `ready` one iteration earlier) and starts loading block t + kLead + 1
-// into `loading`.  A workgroup barrier follows every second iteration only: with a write lead
-// of 3 and 5 stages, every written stage is separated from its first read (QK at iteration
-// t + kLead - 1) and from its previous reads (iteration t + kLead - kStages) by a barrier.
-constexpr int kStages = 5;
-constexpr int kLead = 3;
+// the QK MFMAs of block t + 1 first so they run under the softmax VALU work, and starts the
+// direct copy of block t + kLead.  A workgroup barrier follows every second iteration; the
+// barrier after iteration i waits for every copy issued before iteration i.  With 6 stages
+// and a lead of 4: a copy issued at iteration t is complete and published by the barrier
+// after iteration t + 1 or t + 2, before its first read (QK at iteration t + kLead - 1), and
+// the stage it overwrites was last read at iteration t - 2, before the barrier after t - 2
+// or t - 1.
+constexpr int kStages = 6;
+constexpr int kLead = 4;
 
 template <int D, int NW, bool kCausal, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
-                                              const v4i (&qf)[D / 32], float cq, const float* key_scale, int q0,
-                                              int n, int h, int krow, const v16i (&s_cur)[2], v16i (&s_next)[2],
-                                              float (&num)[D / 32][16], float& den, float& mref,
-                                              v4i (&ready)[Staging<D, NW>::kRounds],
-                                              v4i (&loading)[Staging<D, NW>::kRounds]) {
+                                              int wave, int lane, const v4i (&qf)[D / 32], float cq,
+                                              int q0, int n, int h, int krow,
+                                              const v16i (&s_cur)[2], v16i (&s_next)[2], float (&num)[D / 32][16],
+                                              float& den, float& mref) {
   using L = TileLayout<D, NW>;
-  // unconditional (clamped) so every iteration issues the same loads: static vmcnt waits
-  fetch_block<D, NW>(p, bh, min(t + kLead + 1, tiles - 1), loading);
+  // unconditional (clamped) so every iteration issues the same number of copies; a clamped
+  // copy lands in a stage no iteration reads before it is written again
+  copy_block<D, NW>(p, smem + ((t + kLead) % kStages) * L::kStageBytes, bh, min(t + kLead, tiles - 1), wave, lane);
   if (t < wave_tiles) {
     block_scores<D, NW>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, s_next);  // unused past the end
-    block_update<D, NW, kCausal>(smem + (t % kStages) * L::kStageBytes, s_cur, cq * key_scale[t], t, q0, n, h, num,
-                                 den, mref);
+    const char* stage = smem + (t % kStages) * L::kStageBytes;
+    const float key_scale = *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
+    block_update<D, NW, kCausal>(stage, s_cur, cq * key_scale, t, q0, n, h, num, den, mref);
   }
-  if (t + kLead < tiles) store_block<D, NW>(smem + ((t + kLead) % kStages) * L::kStageBytes, ready);
-  if constexpr (kBarrier) __syncthreads();
+  if constexpr (kBarrier) stage_barrier_keep_last<D, NW>(wave);
 }
 
 template <int D, int NW, bool kCausal, int kOut>
 __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams p) {
   using L = TileLayout<D, NW>;
-  using S = Staging<D, NW>;
   constexpr int kChunksD = D / 32;
   __shared__ __attribute__((aligned(16))) char smem[kStages * L::kStageBytes];
 
@@ -308,8 +309,11 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   const int n = lane & 31;  // query column within the wave
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
   // causal: the longest query tiles (most key blocks) are dispatched first
-  const int qtile = kCausal ? p.query_tiles - 1 - logical % p.query_tiles : logical % p.query_tiles;
-  const int bh = logical / p.query_tiles;
+  // wave-uniform in SGPRs (the runtime division is VALU code): per-block key scales then come
+  // from scalar loads, which do not share the vmcnt counter with the direct LDS copies
+  const int bh = __builtin_amdgcn_readfirstlane(logical / p.query_tiles);
+  const int qtile_fwd = __builtin_amdgcn_readfirstlane(logical - bh * p.query_tiles);
+  const int qtile = kCausal ? p.query_tiles - 1 - qtile_fwd : qtile_fwd;
   const int q0 = qtile * (NW * 32) + wave * 32;  // first query of this wave
   const bool wave_live = q0 < p.query_length;
 
@@ -325,6 +329,12 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
   }
+  // Settle the Q loads here on every path: a load the compiler still counts as pending at the
+  // loop header would get its wait (in-order vmcnt, so a wait for all direct LDS copies in
+  // flight) inside every iteration.
+#pragma unroll
+  for (int c = 0; c < kChunksD; ++c) asm volatile("" ::"v"(qf[c]));
+  asm volatile("" ::"v"(cq));
 
   int tiles = p.nkb;
   int wave_tiles = wave_live ? p.nkb : 0;
@@ -345,35 +355,28 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   // MFMA row m of the K operand holds key 16*((m>>2)&1) + 4*(m>>3) + (m&3), so that output
   // register r of lane half h holds key 16h + r.
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
-  const float* key_scale = p.key_scale + static_cast<long>(bh) * p.nkb;
 
-  // prologue: blocks 0 .. kLead-1 into LDS (missing blocks repeat the last one), block kLead
-  // into registers
-  v4i reg_a[S::kRounds];
-  v4i reg_b[S::kRounds];
+  // prologue: blocks 0 .. kLead-1 (missing blocks repeat the last one), all copies waited for
 #pragma unroll
-  for (int b = 0; b < kLead; ++b) {
-    fetch_block<D, NW>(p, bh, min(b, tiles - 1), reg_a);
-    store_block<D, NW>(smem + b * L::kStageBytes, reg_a);
-  }
-  fetch_block<D, NW>(p, bh, min(kLead, tiles - 1), reg_a);
-  __syncthreads();
+  for (int b = 0; b < kLead; ++b) copy_block<D, NW>(p, smem + b * L::kStageBytes, bh, min(b, tiles - 1), wave, lane);
+  stage_barrier<0>();
 
   v16i s_a[2], s_b[2];  // scores of the current and the next block, alternating
   if (wave_tiles > 0) block_scores<D, NW>(smem, qf, h, krow, s_a);
 
-  // Iteration t stores the register set loaded at t - 1 and loads into the other one:
-  // unrolled by two so both register sets keep static names; one barrier per pair.
+  // unrolled by two so both score sets keep static names; one barrier per pair
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a,
-                                         s_b, num, den, mref, reg_a, reg_b);
-    pipeline_step<D, NW, kCausal, true>(p, smem, t + 1, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_b,
-                                        s_a, num, den, mref, reg_b, reg_a);
+    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
+                                         krow, s_a, s_b, num, den, mref);
+    pipeline_step<D, NW, kCausal, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
+                                        h, krow, s_b, s_a, num, den, mref);
   }
   if (t < tiles)
-    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, qf, cq, key_scale, q0, n, h, krow, s_a,
-                                         s_b, num, den, mref, reg_a, reg_b);
+    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
+                                         krow, s_a, s_b, num, den, mref);
+  // no direct copy may still be writing this workgroup's LDS when its waves end
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue: num / max(den, 1e-30) + mean(V), one query per lane ----
   const int query = q0 + n;

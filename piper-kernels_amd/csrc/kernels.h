@@ -6,9 +6,18 @@
 
 namespace piper {
 
-// Bytes of one 64-key tile record: K codes, V^T codes, 64 log2 scales, 64 inverse
-// multipliers, D corrections.
-constexpr int kv_tile_bytes(int head_dim) { return 128 * head_dim + 512 + 4 * head_dim; }
+// One 64-key tile record is byte for byte the attention kernel's LDS stage, so it is copied
+// with direct global -> LDS loads in 1 KiB pieces: K codes [64][D] in rows of D + 16 bytes,
+// V^T codes [D][64] in rows of 80 bytes (the 16 spare bytes per row spread LDS banks), 64
+// log2 scales, 64 inverse multipliers, D biased corrections, padded to a KiB multiple.
+// Bytes [D, D + 4) (padding of K row 0) hold the tile's K scale; other padding is unspecified.
+constexpr int kv_k_stride(int head_dim) { return head_dim + 16; }
+constexpr int kv_v_stride() { return 64 + 16; }
+constexpr int kv_v_offset(int head_dim) { return 64 * kv_k_stride(head_dim); }
+constexpr int kv_log_offset(int head_dim) { return kv_v_offset(head_dim) + head_dim * kv_v_stride(); }
+constexpr int kv_inv_offset(int head_dim) { return kv_log_offset(head_dim) + 256; }
+constexpr int kv_corr_offset(int head_dim) { return kv_inv_offset(head_dim) + 256; }
+constexpr int kv_tile_bytes(int head_dim) { return (kv_corr_offset(head_dim) + 4 * head_dim + 1023) / 1024 * 1024; }
 
 struct InputTensor {
   const void* data;  // 16-bit floats; the head_dim axis is contiguous

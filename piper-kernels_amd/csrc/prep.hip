@@ -133,7 +133,8 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 }
 
 // Q or K block of kRows rows: one scale over kRows x D values.
-template <bool kBf16, int D, int kRows, bool kCenter>
+// Codes go to rows of kStride bytes (D for query codes, the padded tile stride for keys).
+template <bool kBf16, int D, int kRows, bool kCenter, int kStride>
 __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int h, int row0, int length,
                                                const float* __restrict__ mean, int8_t* __restrict__ codes,
                                                float* __restrict__ scale_out) {
@@ -183,9 +184,13 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
       c[i] = code_of(x, scale);
     }
     uint2 packed = make_uint2(pack4(c[0], c[1], c[2], c[3]), pack4(c[4], c[5], c[6], c[7]));
-    *reinterpret_cast<uint2*>(codes + static_cast<long>(it * kRowsPerIter + sub) * D + group * 8) = packed;
+    *reinterpret_cast<uint2*>(codes + static_cast<long>(it * kRowsPerIter + sub) * kStride + group * 8) = packed;
   }
-  if (lane == 0) *scale_out = scale;
+  if (lane == 0) {
+    *scale_out = scale;
+    // key tiles also carry their scale in the padding of K row 0 (bytes [D, D + 4))
+    if constexpr (kStride != D) *reinterpret_cast<float*>(codes + D) = scale;
+  }
 }
 
 template <bool kBf16, int D>
@@ -204,7 +209,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
     const int qb = unit - bh * p.nqb;
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
-    quantize_block<kBf16, D, kQueryBlock, false>(
+    quantize_block<kBf16, D, kQueryBlock, false, D>(
         p.query, b, h, qb * kQueryBlock, p.query_length, nullptr,
         p.query_code + (static_cast<long>(bh) * p.sq32 + qb * kQueryBlock) * D, p.query_scale + unit);
     return;
@@ -217,7 +222,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
     int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * kv_tile_bytes(D);
-    quantize_block<kBf16, D, kKeyBlock, true>(p.key, b, h, kb * kKeyBlock, p.key_length,
+    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D)>(p.key, b, h, kb * kKeyBlock, p.key_length,
                                               p.key_mean + static_cast<long>(bh) * D, tile, p.key_scale + unit);
     return;
   }
@@ -261,7 +266,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<int8_t>(code_of(f[i], scale));
       if (group == 0) {
-        float* meta = reinterpret_cast<float*>(p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D) + 128 * D);
+        float* meta = reinterpret_cast<float*>(p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D) + kv_log_offset(D));
         p.value_scale[static_cast<long>(bh) * p.sk64 + row] = valid ? scale : 0.0f;
         meta[key_in_tile] = valid ? log2f(scale) : -__builtin_inff();
         meta[kKeyBlock + key_in_tile] = valid ? 1.0f / (255.0f * scale) : 0.0f;
@@ -272,10 +277,10 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
   if (!active) return;
   // transposed rows: lane owns features d = lane, lane + 64, ...
   uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D);
-  int32_t* correction = reinterpret_cast<int32_t*>(tile + 128 * D + 512);
+  int32_t* correction = reinterpret_cast<int32_t*>(tile + kv_corr_offset(D));
   for (int d = lane; d < D; d += kWave) {
     const uint4* src = reinterpret_cast<const uint4*>(lds + d * kVStride);
-    uint4* dst = reinterpret_cast<uint4*>(tile + 64 * D + d * kKeyBlock);
+    uint4* dst = reinterpret_cast<uint4*>(tile + kv_v_offset(D) + d * kv_v_stride());
     int sum = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

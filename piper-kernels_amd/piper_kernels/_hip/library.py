@@ -77,9 +77,24 @@ class PiperLayout(ctypes.Structure):
     ]
 
 
+def kv_k_stride(head_dim: int) -> int:
+    """Bytes per K row in a tile record (D codes + 16 bytes of padding)."""
+    return head_dim + 16
+
+
+KV_V_STRIDE = 64 + 16  # bytes per V^T row in a tile record (64 codes + 16 bytes of padding)
+
+
+def kv_offsets(head_dim: int) -> dict:
+    """Byte offsets of the regions of one tile record (PIPER_KV_* in the C header)."""
+    v = 64 * kv_k_stride(head_dim)
+    log2 = v + head_dim * KV_V_STRIDE
+    return {"key": 0, "key_scale": head_dim, "value": v, "log2": log2, "inv": log2 + 256, "corr": log2 + 512}
+
+
 def kv_tile_bytes(head_dim: int) -> int:
-    """Bytes of one 64-key tile record (PIPER_KV_TILE_BYTES in the C header)."""
-    return 128 * head_dim + 512 + 4 * head_dim
+    """Bytes of one 64-key tile record (PIPER_KV_TILE_BYTES in the C header): a KiB multiple."""
+    return (kv_offsets(head_dim)["corr"] + 4 * head_dim + 1023) // 1024 * 1024
 
 
 class PiperPrepareArgs(ctypes.Structure):

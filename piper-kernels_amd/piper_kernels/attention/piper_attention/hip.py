@@ -52,27 +52,35 @@ class PreparedPiperAttention:
         )
 
     # views into the tile records (for inspection and tests)
+    def _region(self, name: str, length: int) -> torch.Tensor:
+        off = native.kv_offsets(self.shape[4])[name]
+        return self.kv_tiles[..., off : off + length]
+
     def key_code(self) -> torch.Tensor:
+        """K codes [B, H, Sk64, D] (the stored rows carry 16 bytes of padding)."""
         b, h, _, _, d = self.shape
-        return self.kv_tiles[..., : 64 * d].view(torch.int8).reshape(b, h, -1, 64, d).reshape(b, h, -1, d)
+        rows = self._region("key", 64 * native.kv_k_stride(d)).reshape(b, h, -1, 64, native.kv_k_stride(d))
+        return rows[..., :d].contiguous().view(torch.int8).reshape(b, h, -1, d)
+
+    def key_tile_scale(self) -> torch.Tensor:
+        """Copy of each tile's K scale kept in the padding of its first K row: [B, H, nkb]."""
+        return self._region("key_scale", 4).contiguous().view(torch.float32).flatten(2)
 
     def value_code_transposed(self) -> torch.Tensor:
         """V codes as stored: [B, H, Sk64/64, D, 64]."""
         b, h, _, _, d = self.shape
-        return self.kv_tiles[..., 64 * d : 128 * d].view(torch.int8).reshape(b, h, -1, d, 64)
+        rows = self._region("value", d * native.KV_V_STRIDE).reshape(b, h, -1, d, native.KV_V_STRIDE)
+        return rows[..., :64].contiguous().view(torch.int8)
 
     def value_log2_scale(self) -> torch.Tensor:
-        d = self.shape[4]
-        return self.kv_tiles[..., 128 * d : 128 * d + 256].contiguous().view(torch.float32).flatten(2)
+        return self._region("log2", 256).contiguous().view(torch.float32).flatten(2)
 
     def value_inv_multiplier(self) -> torch.Tensor:
-        d = self.shape[4]
-        return self.kv_tiles[..., 128 * d + 256 : 128 * d + 512].contiguous().view(torch.float32).flatten(2)
+        return self._region("inv", 256).contiguous().view(torch.float32).flatten(2)
 
     def value_correction(self) -> torch.Tensor:
         """128 * column sums of the V codes per tile (the stored words carry a 0x4B400000 bias)."""
-        d = self.shape[4]
-        return self.kv_tiles[..., 128 * d + 512 :].contiguous().view(torch.int32) - ACC_BIAS
+        return self._region("corr", 4 * self.shape[4]).contiguous().view(torch.int32) - ACC_BIAS
 
 
 def _native_input(tensor: torch.Tensor) -> tuple[torch.Tensor, native.PiperTensor]:

@@ -70,6 +70,7 @@ def prepared_numpy(prepared) -> dict:
         "query_block_scale": prepared.query_scale.cpu().numpy(),
         "key_code_padded": prepared.key_code().cpu().numpy(),
         "key_block_scale": prepared.key_scale.cpu().numpy(),
+        "key_tile_scale": prepared.key_tile_scale().cpu().numpy(),
         "value_code_padded": vcode,
         "value_scale_padded": prepared.value_scale.cpu().numpy(),
         "value_log2_scale": prepared.value_log2_scale().cpu().numpy(),
@@ -97,6 +98,7 @@ def assert_prep_bit_exact(got: dict, expected: dict, shape, is_causal: bool) -> 
     assert np.array_equal(kc[:, :, :sk], expected["key_code"]), "key codes differ"
     assert not kc[:, :, sk:].any(), "key padding rows must be zero"
     assert _bits_equal(got["key_block_scale"], expected["key_block_scale"]), "key scales differ"
+    assert _bits_equal(got["key_tile_scale"], expected["key_block_scale"]), "tile copies of the key scales differ"
     assert _bits_equal(got["key_mean"], expected["key_mean"]), "key means differ"
     assert _bits_equal(got["value_mean"], expected["value_mean"]), "value means differ"
     if is_causal:

@@ -76,8 +76,12 @@ def test_prepared_layout_sizes(lib, shape) -> None:
     assert layout.key_scale_bytes == b * h * (sk64 // 64) * 4
     assert layout.value_scale_bytes == b * h * sk64 * 4
     assert layout.mean_bytes == b * h * d * 4
-    # one record per 64-key tile: K codes, V^T codes, 64 log2 scales, 64 inverse multipliers, D corrections
-    assert layout.kv_tile_bytes == native.kv_tile_bytes(d) == 64 * d + d * 64 + 256 + 256 + 4 * d
+    # one record per 64-key tile, laid out as the attention kernel's LDS stage: K rows of D + 16
+    # bytes, V^T rows of 80 bytes, 64 log2 scales, 64 inverse multipliers, D corrections,
+    # rounded up to a KiB multiple (the unit of the direct global -> LDS copy)
+    raw = 64 * (d + 16) + d * 80 + 256 + 256 + 4 * d
+    assert layout.kv_tile_bytes == native.kv_tile_bytes(d) == -(-raw // 1024) * 1024
+    assert layout.kv_tile_bytes % 1024 == 0 and layout.kv_tile_bytes - raw < 1024
     assert layout.kv_tiles_bytes == b * h * (sk64 // 64) * layout.kv_tile_bytes
     assert layout.workspace_bytes == 2 * b * h * (-(-sk // 64)) * d * 8
 
