@@ -137,13 +137,20 @@ __device__ __forceinline__ void store4(void* out, long index, float a, float b, 
   }
 }
 
+// Value of an integer accumulator that started from kAccBias: one exact FP32 subtraction.
+// (The element arrives as a scalar: this clang's __builtin_bit_cast of an ext_vector
+// subscript reads element 0.)
+__device__ __forceinline__ float unbias(int bits) { return __builtin_bit_cast(float, bits) - kAccBiasValue; }
+
 // Integer scores S^T = K Q^T of one 64-key block: s[0] keys 0..31, s[1] keys 32..63 (each
 // lane: its query column, keys 16h + r after the K-row permutation).
 template <int D, int NW>
 __device__ __forceinline__ void block_scores(const char* stage, const v4i (&qf)[D / 32], int h, int krow,
-                                             v16i (&s)[2]) {
+                                             const v16i& bias, v16i (&s)[2]) {
   using L = TileLayout<D, NW>;
-  s[0] = s[1] = v16i{};
+  // accumulators start from the bias: |K Q^T| <= D * 128 * 128 < 2^22, so each result reads as
+  // FP32 1.5 * 2^23 + score exactly
+  s[0] = s[1] = bias;
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
     const char* kb = stage + 32 * c + 16 * h;
@@ -168,14 +175,14 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   for (int q = 0; q < 4; ++q) {
     const float4 la = lk4[4 * h + q];
     const float4 lb = lk4[8 + 4 * h + q];
-    x[4 * q + 0] = fmaf(static_cast<float>(s[0][4 * q + 0]), ct, la.x);
-    x[4 * q + 1] = fmaf(static_cast<float>(s[0][4 * q + 1]), ct, la.y);
-    x[4 * q + 2] = fmaf(static_cast<float>(s[0][4 * q + 2]), ct, la.z);
-    x[4 * q + 3] = fmaf(static_cast<float>(s[0][4 * q + 3]), ct, la.w);
-    x[16 + 4 * q + 0] = fmaf(static_cast<float>(s[1][4 * q + 0]), ct, lb.x);
-    x[16 + 4 * q + 1] = fmaf(static_cast<float>(s[1][4 * q + 1]), ct, lb.y);
-    x[16 + 4 * q + 2] = fmaf(static_cast<float>(s[1][4 * q + 2]), ct, lb.z);
-    x[16 + 4 * q + 3] = fmaf(static_cast<float>(s[1][4 * q + 3]), ct, lb.w);
+    x[4 * q + 0] = fmaf(unbias(s[0][4 * q + 0]), ct, la.x);
+    x[4 * q + 1] = fmaf(unbias(s[0][4 * q + 1]), ct, la.y);
+    x[4 * q + 2] = fmaf(unbias(s[0][4 * q + 2]), ct, la.z);
+    x[4 * q + 3] = fmaf(unbias(s[0][4 * q + 3]), ct, la.w);
+    x[16 + 4 * q + 0] = fmaf(unbias(s[1][4 * q + 0]), ct, lb.x);
+    x[16 + 4 * q + 1] = fmaf(unbias(s[1][4 * q + 1]), ct, lb.y);
+    x[16 + 4 * q + 2] = fmaf(unbias(s[1][4 * q + 2]), ct, lb.z);
+    x[16 + 4 * q + 3] = fmaf(unbias(s[1][4 * q + 3]), ct, lb.w);
   }
   if constexpr (kCausal) {
     if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // block crosses this wave's diagonal
@@ -257,13 +264,8 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
     acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, p0, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, p1, acc, 0, 0, 0);
     // acc started from the biased correction: its bits are 1.5 * 2^23 + (u @ v) exactly.
-    // (The element goes through a scalar first: this clang's __builtin_bit_cast of an
-    // ext_vector subscript reads element 0.)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int bits = acc[r];
-      num[j][r] = fmaf(__builtin_bit_cast(float, bits) - kAccBiasValue, weight, num[j][r]);
-    }
+    for (int r = 0; r < 16; ++r) num[j][r] = fmaf(unbias(acc[r]), weight, num[j][r]);
   }
 }
 
@@ -281,7 +283,7 @@ constexpr int kLead = 4;
 template <int D, int NW, bool kCausal, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                               int wave, int lane, const v4i (&qf)[D / 32], float cq,
-                                              int q0, int n, int h, int krow,
+                                              int q0, int n, int h, int krow, const v16i& bias,
                                               const v16i (&s_cur)[2], v16i (&s_next)[2], float (&num)[D / 32][16],
                                               float& den, float& mref) {
   using L = TileLayout<D, NW>;
@@ -289,7 +291,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
   // copy lands in a stage no iteration reads before it is written again
   copy_block<D, NW>(p, smem + ((t + kLead) % kStages) * L::kStageBytes, bh, min(t + kLead, tiles - 1), wave, lane);
   if (t < wave_tiles) {
-    block_scores<D, NW>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, s_next);  // unused past the end
+    block_scores<D, NW>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, bias, s_next);  // unused past the end
     const char* stage = smem + (t % kStages) * L::kStageBytes;
     const float key_scale = *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
     block_update<D, NW, kCausal>(stage, s_cur, cq * key_scale, t, q0, n, h, num, den, mref);
@@ -361,20 +363,24 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   for (int b = 0; b < kLead; ++b) copy_block<D, NW>(p, smem + b * L::kStageBytes, bh, min(b, tiles - 1), wave, lane);
   stage_barrier<0>();
 
+  // QK accumulator bias, kept in registers for the whole loop (opaque, so not rematerialised)
+  v16i bias = {kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias,
+               kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias};
+  asm volatile("" : "+v"(bias));
   v16i s_a[2], s_b[2];  // scores of the current and the next block, alternating
-  if (wave_tiles > 0) block_scores<D, NW>(smem, qf, h, krow, s_a);
+  if (wave_tiles > 0) block_scores<D, NW>(smem, qf, h, krow, bias, s_a);
 
   // unrolled by two so both score sets keep static names; one barrier per pair
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
     pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
-                                         krow, s_a, s_b, num, den, mref);
+                                         krow, bias, s_a, s_b, num, den, mref);
     pipeline_step<D, NW, kCausal, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
-                                        h, krow, s_b, s_a, num, den, mref);
+                                        h, krow, bias, s_b, s_a, num, den, mref);
   }
   if (t < tiles)
     pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
-                                         krow, s_a, s_b, num, den, mref);
+                                         krow, bias, s_a, s_b, num, den, mref);
   // no direct copy may still be writing this workgroup's LDS when its waves end
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
