@@ -122,8 +122,25 @@ __device__ __forceinline__ float scale_from_amax(float amax) {
   return __fadd_rn(q, 1e-7f);
 }
 
-__device__ __forceinline__ int code_of(float x, float scale) {
-  const float r = __builtin_rintf(x / scale);  // IEEE division, round half to even
+// A quantisation scale with its correctly rounded reciprocal, shared by all elements it divides.
+struct Divisor {
+  float s;  // the scale, or 0 for an infinite scale (see quotient)
+  float y;  // RN(1 / scale), IEEE division
+  __device__ explicit Divisor(float scale) : s(__builtin_isinf(scale) ? 0.0f : scale), y(1.0f / scale) {}
+  // RN(x / scale) without a per-element division (Markstein: with y = RN(1/s) and a faithful
+  // q0 = RN(x y), the remainder x - s q0 is exact in one FMA and RN(q0 + r y) = RN(x / s) for
+  // normal x; subnormal x only moves a quotient far below 1/2 by an ulp, so the rounded code is
+  // unchanged).  For an infinite scale (non-finite input) y = 0 and s = 0 give x / inf = +-0
+  // for finite x and NaN for infinite x, as the division does.
+  __device__ float quotient(float x) const {
+    const float q0 = __fmul_rn(x, y);
+    const float r = fmaf(-s, q0, x);
+    return fmaf(r, y, q0);
+  }
+};
+
+__device__ __forceinline__ int code_of(float x, const Divisor& d) {
+  const float r = __builtin_rintf(d.quotient(x));  // round half to even
   return static_cast<int>(fminf(fmaxf(r, -127.0f), 127.0f));
 }
 
@@ -172,6 +189,7 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
   }
   amax = wave_max(amax);
   const float scale = scale_from_amax(amax);
+  const Divisor divisor(scale);
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
     const int row = row0 + it * kRowsPerIter + sub;
@@ -181,7 +199,7 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
-      c[i] = code_of(x, scale);
+      c[i] = code_of(x, divisor);
     }
     uint2 packed = make_uint2(pack4(c[0], c[1], c[2], c[3]), pack4(c[4], c[5], c[6], c[7]));
     *reinterpret_cast<uint2*>(codes + static_cast<long>(it * kRowsPerIter + sub) * kStride + group * 8) = packed;
@@ -263,8 +281,10 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
       }
       amax = group_max<kGroups>(amax);
       const float scale = scale_from_amax(amax);
+      const Divisor divisor(scale);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<int8_t>(code_of(f[i], scale));
+      for (int i = 0; i < 8; ++i)
+        lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<int8_t>(code_of(f[i], divisor));
       if (group == 0) {
         float* meta = reinterpret_cast<float*>(p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D) + kv_log_offset(D));
         p.value_scale[static_cast<long>(bh) * p.sk64 + row] = valid ? scale : 0.0f;
