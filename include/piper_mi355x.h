@@ -143,11 +143,19 @@ typedef struct piper_prepare_args {
   int64_t workspace_bytes;
 } piper_prepare_args;
 
+/* Launch-plan bits of piper_attention_args.plan (results are identical for every plan; only
+ * the speed differs).  Default (0): 8 query waves of 32 queries per workgroup, causal query
+ * tiles dispatched longest first, workgroups of one head kept on one XCD. */
+#define PIPER_PLAN_FOUR_WAVES 1     /* 4 query waves per workgroup (for grids below the CU count) */
+#define PIPER_PLAN_CAUSAL_FORWARD 2 /* causal: query tiles in forward order */
+#define PIPER_PLAN_NO_XCD_REMAP 4   /* hardware workgroup order */
+#define PIPER_PLAN_MASK 7
+
 typedef struct piper_attention_args {
   int32_t abi_version;  /* PIPER_ABI_VERSION */
   int32_t output_dtype; /* PIPER_FLOAT16, PIPER_BFLOAT16 or PIPER_FLOAT32 */
   int32_t is_causal;
-  int32_t plan;         /* 0 = default MI355X launch plan */
+  int32_t plan;         /* launch plan: OR of PIPER_PLAN_* bits; 0 = the default plan */
   piper_shape shape;
   float scale;          /* softmax scale, finite and > 0 */
   int32_t reserved;

@@ -175,7 +175,7 @@ int piper_attention_forward(const piper_attention_args* a, void* stream) {
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
   if (!(std::isfinite(a->scale) && a->scale > 0.0f))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
-  if (a->plan < 0 || a->plan > 1) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
+  if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
   const piper_prepared& o = a->prepared;
   if (!o.query_code || !o.query_scale || !o.key_scale || !o.kv_tiles || !o.value_mean || !a->output)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared input or the output pointer is NULL");
@@ -184,7 +184,7 @@ int piper_attention_forward(const piper_attention_args* a, void* stream) {
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
 
   const piper_shape& s = a->shape;
-  const int waves = a->plan == 1 ? 4 : 8;
+  const int waves = (a->plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
   piper::AttnParams ap{};
   ap.query_code = o.query_code;
   ap.query_scale = o.query_scale;
@@ -201,6 +201,8 @@ int piper_attention_forward(const piper_attention_args* a, void* stream) {
   ap.nkb = ap.sk64 / PIPER_KEY_BLOCK;
   ap.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * waves));
   ap.scale_log2e = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
+  ap.causal_forward = (a->plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
+  ap.xcd_remap = (a->plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
   if (static_cast<int64_t>(ap.query_tiles) * ap.batch_heads > 0x7fffffff)
     return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
 

@@ -80,6 +80,8 @@ struct AttnParams {
   int nkb;
   int query_tiles;  // workgroup query tiles per (batch, head)
   float scale_log2e;
+  int causal_forward;  // causal grids: 1 = query tiles in forward order, 0 = longest first
+  int xcd_remap;       // 1 = consecutive workgroups of a head share an XCD, 0 = hardware order
 };
 
 hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream);

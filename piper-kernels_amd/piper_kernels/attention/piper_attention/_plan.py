@@ -3,26 +3,43 @@
 Plays the role of the reference's ``PiperAttentionExecutionPlan`` /
 ``select_execution_plan`` (``src/piper_kernels/attention/piper_attention/_policy.py:14-96``)
 for gfx950: an immutable record chosen from the shape, never autotuned at call time.
+``select_plan`` looks the shape up in the frozen table ``mi355x_plans.json`` (written offline
+by ``piper_kernels.attention.piper_attention.tune``, the counterpart of the reference's
+``benchmarks/tune_piper_attention.py``) and falls back to a heuristic for other shapes.
+Every plan computes bit-identical results; only the speed differs.
 """
 
 from __future__ import annotations
 
+import json
 from dataclasses import asdict, dataclass
+from functools import lru_cache
+from pathlib import Path
 
 COMPUTE_UNITS = 256  # MI355X
 KEY_BLOCK = 64  # keys per streamed tile and per P block (reference.py:16)
 QUERIES_PER_WAVE = 32  # one v_mfma_i32_32x32x32_i8 column block
+PLAN_TABLE = Path(__file__).with_name("mi355x_plans.json")
+
+# piper_attention_args.plan bits (include/piper_mi355x.h)
+PLAN_FOUR_WAVES = 1
+PLAN_CAUSAL_FORWARD = 2
+PLAN_NO_XCD_REMAP = 4
 
 
 @dataclass(frozen=True)
 class MI355XPlan:
-    """Workgroup shape of the fused kernel.
+    """Launch plan of the fused kernel.
 
-    ``waves`` query waves of 32 queries share each K/V tile staged in LDS (8 waves: 256
-    queries per workgroup, one workgroup per CU; 4 waves: 128 queries, two per CU).
+    ``waves``: query waves of 32 queries sharing each K/V tile staged in LDS (8: 256 queries
+    per workgroup, one workgroup per CU; 4: 128 queries). ``causal_longest_first``: causal
+    grids dispatch the query tiles with the most key blocks first. ``xcd_remap``: consecutive
+    workgroups of one head run on one XCD (its L2 then serves the head's K/V tiles).
     """
 
     waves: int = 8
+    causal_longest_first: bool = True
+    xcd_remap: bool = True
 
     def __post_init__(self) -> None:
         if self.waves not in (4, 8):
@@ -34,8 +51,22 @@ class MI355XPlan:
 
     @property
     def plan_id(self) -> int:
-        """The ``plan`` field of ``piper_attention_args`` (0 = 8 waves, 1 = 4 waves)."""
-        return 0 if self.waves == 8 else 1
+        """The ``plan`` field of ``piper_attention_args`` (an OR of PIPER_PLAN_* bits)."""
+        return (
+            (PLAN_FOUR_WAVES if self.waves == 4 else 0)
+            | (0 if self.causal_longest_first else PLAN_CAUSAL_FORWARD)
+            | (0 if self.xcd_remap else PLAN_NO_XCD_REMAP)
+        )
+
+    @classmethod
+    def from_id(cls, plan_id: int) -> "MI355XPlan":
+        if not 0 <= plan_id <= PLAN_FOUR_WAVES | PLAN_CAUSAL_FORWARD | PLAN_NO_XCD_REMAP:
+            raise ValueError(f"unknown plan id {plan_id}")
+        return cls(
+            waves=4 if plan_id & PLAN_FOUR_WAVES else 8,
+            causal_longest_first=not plan_id & PLAN_CAUSAL_FORWARD,
+            xcd_remap=not plan_id & PLAN_NO_XCD_REMAP,
+        )
 
     def workgroups(self, batch: int, heads: int, query_length: int) -> int:
         return batch * heads * (-(-query_length // self.block_m))
@@ -44,9 +75,34 @@ class MI355XPlan:
         return {**asdict(self), "block_m": self.block_m, "block_n": KEY_BLOCK}
 
 
-def select_plan(batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool) -> MI355XPlan:
+def shape_key(batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool) -> tuple:
+    """Table key: heads are independent, so only batch * heads matters."""
+    return (batch * heads, query_length, key_length, head_dim, bool(is_causal))
+
+
+@lru_cache(maxsize=1)
+def frozen_plans() -> dict:
+    """The committed tuner table: shape key -> plan (empty if the file is absent)."""
+    if not PLAN_TABLE.exists():
+        return {}
+    table = json.loads(PLAN_TABLE.read_text())
+    plans = {}
+    for entry in table.get("entries", []):
+        k = entry["key"]
+        key = (k["batch_heads"], k["query_length"], k["key_length"], k["head_dim"], bool(k["is_causal"]))
+        plans[key] = MI355XPlan(**entry["plan"])
+    return plans
+
+
+def heuristic_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
     """8-wave workgroups unless that leaves most CUs idle; then 4-wave workgroups."""
     wide = MI355XPlan(waves=8)
     if wide.workgroups(batch, heads, query_length) >= COMPUTE_UNITS:
         return wide
     return MI355XPlan(waves=4)
+
+
+def select_plan(batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool) -> MI355XPlan:
+    """The frozen table's plan for a tuned shape, else the heuristic."""
+    plan = frozen_plans().get(shape_key(batch, heads, query_length, key_length, head_dim, is_causal))
+    return plan if plan is not None else heuristic_plan(batch, heads, query_length)

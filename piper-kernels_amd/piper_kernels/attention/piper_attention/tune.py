@@ -1,0 +1,135 @@
+"""Offline launch-plan tuner for the MI355X backend (never called at run time).
+
+Counterpart of the reference's ``benchmarks/tune_piper_attention.py:53-221``: a bounded
+search over the plan axes the gfx950 kernel exposes (query waves per workgroup, causal
+query-tile order, XCD-aware workgroup order), quality-gated, whose result is frozen into
+``mi355x_plans.json`` for ``select_plan``.
+
+    python -m piper_kernels.attention.piper_attention.tune --workloads c1 c2 c3 c4 c5 --write
+
+For each shape: synthetic inputs are prepared once; every candidate plan is launched on the
+same prepared operands, timed with HIP events on the launch stream (warm-up, then rounds that
+interleave the candidates so clock drift does not favour one), and gated: its FP32 output must
+equal the default plan's bit for bit (every plan performs the same arithmetic per query; only
+the order of workgroups differs). The fastest passing plan is recorded; a plan within
+``--margin`` of the default keeps the default.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import sys
+from dataclasses import replace
+from itertools import product
+from pathlib import Path
+
+if __package__ in (None, ""):
+    sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
+
+
+def candidate_plans(is_causal: bool):
+    from piper_kernels.attention.piper_attention._plan import MI355XPlan
+
+    orders = (True, False) if is_causal else (True,)
+    return [MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x) for w, o, x in product((8, 4), orders, (True, False))]
+
+
+def tune_shape(q, k, v, is_causal: bool, *, warmup: int, rounds: int, launches: int, margin: float) -> dict:
+    import torch
+
+    from piper_kernels.attention.piper_attention._plan import MI355XPlan, shape_key
+    from piper_kernels.attention.piper_attention.hip import _launch_piper_attention, _prepare_piper_attention
+
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    default = MI355XPlan()
+    prepared = _prepare_piper_attention(q, k, v, d**-0.5, is_causal, plan=default)
+    plans = candidate_plans(is_causal)
+    reference = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+    _launch_piper_attention(prepared, output=reference)
+    candidate_out = torch.empty_like(reference)
+    passed = {}
+    for plan in plans:
+        _launch_piper_attention(replace(prepared, plan=plan), output=candidate_out)
+        torch.cuda.synchronize()
+        passed[plan] = bool(torch.equal(candidate_out, reference))
+    times = {plan: [] for plan in plans}
+    for plan in plans:
+        for _ in range(warmup):
+            _launch_piper_attention(replace(prepared, plan=plan))
+    stream = torch.cuda.current_stream()
+    for _ in range(rounds):
+        for plan in plans:
+            run = replace(prepared, plan=plan)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(launches):
+                _launch_piper_attention(run)
+            end.record(stream)
+            end.synchronize()
+            times[plan].append(start.elapsed_time(end) / launches)
+    medians = {plan: statistics.median(ts) for plan, ts in times.items()}
+    best = min((p for p in plans if passed[p]), key=lambda p: medians[p])
+    if medians[best] > medians[default] * (1.0 - margin):
+        best = default
+    batch_heads, ql, kl, hd, causal = shape_key(b, h, sq, sk, d, is_causal)
+    return {
+        "key": {"batch_heads": batch_heads, "query_length": ql, "key_length": kl, "head_dim": hd, "is_causal": causal},
+        "plan": {"waves": best.waves, "causal_longest_first": best.causal_longest_first, "xcd_remap": best.xcd_remap},
+        "candidates": [
+            {"plan_id": p.plan_id, **p.as_dict(), "median_ms": round(medians[p], 5), "bitwise_equal_to_default": passed[p]}
+            for p in plans
+        ],
+        "default_ms": round(medians[default], 5),
+        "chosen_ms": round(medians[best], 5),
+    }
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--workloads", nargs="+", default=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--rounds", type=int, default=5)
+    parser.add_argument("--launches", type=int, default=3)
+    parser.add_argument("--margin", type=float, default=0.01, help="minimum gain over the default plan")
+    parser.add_argument("--write", action="store_true", help="write the frozen table next to _plan.py")
+    parser.add_argument("--out", type=Path, help="also write the table here")
+    args = parser.parse_args(argv)
+
+    import torch
+
+    from piper_kernels.attention.piper_attention._plan import PLAN_TABLE
+    from piper_kernels.workloads import WORKLOADS, make_inputs
+
+    device = torch.device("cuda", 0)
+    entries = []
+    with torch.no_grad():
+        for name in args.workloads:
+            w = WORKLOADS[name]
+            q, k, v = make_inputs(w, device)
+            entry = tune_shape(q, k, v, w.is_causal, warmup=args.warmup, rounds=args.rounds, launches=args.launches,
+                               margin=args.margin)
+            entry["workload"] = name
+            entries.append(entry)
+            print(f"[tune] {name}: default {entry['default_ms']:.4f} ms, chosen {entry['plan']} {entry['chosen_ms']:.4f} ms",
+                  file=sys.stderr, flush=True)
+            del q, k, v
+            torch.cuda.empty_cache()
+    table = {
+        "device": torch.cuda.get_device_properties(device).gcnArchName,
+        "tuner": "python -m piper_kernels.attention.piper_attention.tune " + " ".join(argv if argv is not None else sys.argv[1:]),
+        "entries": entries,
+    }
+    text = json.dumps(table, indent=1) + "\n"
+    if args.write:
+        PLAN_TABLE.write_text(text)
+    if args.out:
+        args.out.write_text(text)
+    print(text)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -9,6 +9,7 @@ tests/benchmark_support/test_quality.py:8-22 and test_benchmark_attention.py:349
 from __future__ import annotations
 
 import math
+from pathlib import Path
 from types import SimpleNamespace
 
 import pytest
@@ -22,6 +23,8 @@ from piper_kernels.attention.piper_attention import dispatch
 from piper_kernels.attention.piper_attention._plan import MI355XPlan, select_plan
 from piper_kernels.measure import attention_operations, measure_quality, prep_algorithmic_bytes
 from piper_kernels.workloads import WORKLOADS, make_inputs
+
+REPO = Path(__file__).resolve().parents[1]
 
 
 def _inputs():
@@ -165,12 +168,65 @@ def test_gfx950_without_library_raises(monkeypatch, tmp_path) -> None:
 
 # ---- plan ----------------------------------------------------------------------------
 def test_plan_selection() -> None:
-    assert select_plan(1, 24, 16384, 16384, 128, False) == MI355XPlan(waves=8)
-    assert select_plan(1, 2, 193, 193, 128, False) == MI355XPlan(waves=4)
+    from piper_kernels.attention.piper_attention import _plan
+
+    assert _plan.heuristic_plan(1, 24, 16384) == MI355XPlan(waves=8)
+    assert _plan.heuristic_plan(1, 2, 193) == MI355XPlan(waves=4)
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
-    assert MI355XPlan(8).as_dict() == {"waves": 8, "block_m": 256, "block_n": 64}
+    assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
+                                        "block_m": 256, "block_n": 64}
     with pytest.raises(ValueError):
         MI355XPlan(waves=2)
+    with pytest.raises(ValueError):
+        MI355XPlan.from_id(8)
+
+
+def test_plan_ids_round_trip_and_match_the_header() -> None:
+    from piper_kernels.attention.piper_attention import _plan
+
+    header = (REPO / "include" / "piper_mi355x.h").read_text()
+    for name, value in (("FOUR_WAVES", 1), ("CAUSAL_FORWARD", 2), ("NO_XCD_REMAP", 4), ("MASK", 7)):
+        assert f"#define PIPER_PLAN_{name} {value}" in header
+    assert _plan.PLAN_FOUR_WAVES == 1 and _plan.PLAN_CAUSAL_FORWARD == 2 and _plan.PLAN_NO_XCD_REMAP == 4
+    ids = set()
+    for plan_id in range(8):
+        plan = MI355XPlan.from_id(plan_id)
+        assert plan.plan_id == plan_id
+        ids.add(plan)
+    assert len(ids) == 8
+
+
+def test_frozen_plan_table_lookup_and_fallback(tmp_path, monkeypatch) -> None:
+    import json
+
+    from piper_kernels.attention.piper_attention import _plan
+
+    table = {"entries": [{"key": {"batch_heads": 24, "query_length": 4096, "key_length": 4096, "head_dim": 128,
+                                  "is_causal": False},
+                          "plan": {"waves": 4, "causal_longest_first": True, "xcd_remap": False}}]}
+    path = tmp_path / "plans.json"
+    path.write_text(json.dumps(table))
+    monkeypatch.setattr(_plan, "PLAN_TABLE", path)
+    _plan.frozen_plans.cache_clear()
+    try:
+        # batch * heads is the key: B2 H12 is the same shape as B1 H24
+        assert _plan.select_plan(2, 12, 4096, 4096, 128, False) == MI355XPlan(4, True, False)
+        assert _plan.select_plan(1, 24, 4096, 4096, 128, True) == _plan.heuristic_plan(1, 24, 4096)
+        assert _plan.select_plan(1, 24, 16384, 16384, 128, False) == MI355XPlan()
+    finally:
+        _plan.frozen_plans.cache_clear()
+
+
+def test_committed_plan_table_is_well_formed() -> None:
+    from piper_kernels.attention.piper_attention import _plan
+
+    _plan.frozen_plans.cache_clear()
+    plans = _plan.frozen_plans()
+    if not _plan.PLAN_TABLE.exists():
+        pytest.skip("no tuned table committed")
+    assert plans, "the committed table has no entries"
+    for key, plan in plans.items():
+        assert len(key) == 5 and isinstance(plan, MI355XPlan)
 
 
 # ---- custom op -----------------------------------------------------------------------

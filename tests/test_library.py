@@ -126,7 +126,7 @@ def test_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 7
+    args.plan = 8
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward(args, 0)
     args.plan = 0
