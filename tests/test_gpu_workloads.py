@@ -105,3 +105,50 @@ def test_c4_future_value_rows_do_not_change_earlier_outputs(gfx950_device) -> No
     torch.cuda.synchronize()
     assert torch.equal(a[:, :, :4096], b[:, :, :4096])
     assert not torch.equal(a[:, :, 4096:], b[:, :, 4096:])
+
+
+def _sdpa_rows_float64(q, k, v, rows: slice, scale: float, causal: bool) -> np.ndarray:
+    """FP64 softmax attention for query rows `rows` (causal rows see keys <= their index)."""
+    q64 = oracle.as_float32(q[:, :, rows]).astype(np.float64)
+    k64 = oracle.as_float32(k).astype(np.float64)
+    v64 = oracle.as_float32(v).astype(np.float64)
+    logits = np.matmul(q64, np.swapaxes(k64, -1, -2)) * scale
+    if causal:
+        query = np.arange(rows.start, rows.stop)[:, None]
+        logits = np.where(np.arange(k64.shape[2])[None, :] > query, -np.inf, logits)
+    logits -= logits.max(axis=-1, keepdims=True)
+    weights = np.exp(logits)
+    weights /= weights.sum(axis=-1, keepdims=True)
+    return np.matmul(weights, v64)
+
+
+@pytest.mark.parametrize(
+    "name,batches,heads,rows",
+    [("c1", [0], list(range(8)), slice(0, 1024)), ("c2", [0], [0, 23], slice(0, 512)),
+     ("c4", [2], [5], slice(7680, 8192))],
+    ids=["c1", "c2", "c4"],
+)
+def test_output_against_fp64_sdpa(gfx950_device, name, batches, heads, rows) -> None:
+    """The second correctness level of the task statement, against full-precision attention.
+
+    Gate: cosine similarity >= 0.9995 against FP64 SDPA (the stated example tolerance), and a
+    max-abs error no larger than the quantized reference's own distance to FP64 SDPA plus 2e-3:
+    the stated example max-abs (2e-3) is below what the reference algorithm itself reaches
+    against SDPA (INT8 Q/K/V and UINT8 P quantisation), so the kernel is held to "no further
+    from SDPA than the reference, within the 2e-3 the kernel may differ from the reference".
+    """
+    w = WORKLOADS[name]
+    q, k, v = make_inputs(w, batches=batches, heads=heads)
+    scale = w.head_dim**-0.5
+    log(f"[case] sdpa envelope {name} batches={batches} heads={heads} rows={rows.start}:{rows.stop}")
+    prepared = gpu_prepare(q, k, v, scale, w.is_causal, device=gfx950_device)
+    got = gpu_attention(prepared, torch.float32).cpu().numpy()[:, :, rows].astype(np.float64)
+    expected = _sdpa_rows_float64(q, k, v, rows, scale, w.is_causal)
+    reference = _oracle_rows(oracle.prepare(q, k, v, w.is_causal, "per_warp"), rows, scale, w.is_causal)
+    reference_max = np.abs(reference.astype(np.float64) - expected).max()
+    err = np.abs(got - expected)
+    cosine = (got * expected).sum() / np.sqrt((got * got).sum() * (expected * expected).sum())
+    log(f"[quality] {name} vs fp64 sdpa: max {err.max():.3e} (reference {reference_max:.3e}) mean {err.mean():.3e} "
+        f"cos {cosine:.6f}")
+    assert cosine >= 0.9995
+    assert err.max() <= reference_max + 2e-3
