@@ -3,8 +3,10 @@
 
 Workload (the headline shape): B1 H24 S16384 D128 fp16,
 non-causal, synthetic seeded inputs already resident in HBM.  One *step* is one complete
-operator call: the HIP prep pipeline (K/V means, INT8 Q/K/V quantisation) followed by the
-fused INT8-MFMA attention kernel -- exactly what ``piper_attention`` runs.
+operator call, exactly what ``piper_attention`` runs: the HIP prep pipeline (K/V means,
+INT8 K and V quantisation) followed by the fused INT8-MFMA attention kernel, which
+quantises each query block in its prologue (``--two-step``: the prep quantises Q as well
+and the kernel reads the prepared query codes; the output is bit-identical).
 
 Prints ONE JSON line.  ``value`` = whole-call TOPS (reference op count 4*B*H*Sq*Skv*D per
 call, benchmarks/benchmark_attention.py:184-193).  ``roofline`` prices the dominant
@@ -13,7 +15,7 @@ average duration measured by HIP events recorded on the launch stream inside the
 region.  ``cpu_baseline`` times the CPU oracle (a numpy restatement of the reference's
 portable path) on a bounded slice of the same workload, on one host thread.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline] [--two-step]
 """
 
 from __future__ import annotations
@@ -44,6 +46,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
+    parser.add_argument(
+        "--two-step", action="store_true", help="time the prep of Q, K, V + attention on prepared query codes"
+    )
     return parser.parse_args()
 
 
@@ -127,7 +132,7 @@ def main() -> int:
     def step(events=None):
         if events is not None:
             events[0].record()
-        prepared = _prepare_piper_attention(q, k, v, scale, workload.is_causal)
+        prepared = _prepare_piper_attention(q, k, v, scale, workload.is_causal, quantize_query=args.two_step)
         if events is not None:
             events[1].record()
         out = _launch_piper_attention(prepared)
@@ -155,7 +160,7 @@ def main() -> int:
     attn_mean = sum(attn_ms) / len(attn_ms)
     prep_mean = sum(prep_ms) / len(prep_ms)
     attn_tops = ops / (attn_mean * 1e-3) / 1e12
-    prep_bytes = prep_algorithmic_bytes(b, h, sq, sk, d, workload.is_causal)
+    prep_bytes = prep_algorithmic_bytes(b, h, sq, sk, d, workload.is_causal, quantize_query=args.two_step)
     value = ops / (ms_per_step * 1e-3) / 1e12
     log(f"[bench] step {ms_per_step:.4f} ms ({value:.1f} TOPS); attention {attn_mean:.4f} ms "
         f"({attn_tops:.1f} TOPS, {100 * attn_tops / INT8_PEAK_TOPS:.1f}% of INT8 peak); prep {prep_mean:.4f} ms")
@@ -175,7 +180,11 @@ def main() -> int:
         "data": "synthetic (seeded numpy PCG64 per head, fp16 inputs resident in HBM)",
         "config": {
             **workload.as_dict(),
-            "step": "complete operator call: HIP prep + fused attention kernel",
+            "step": (
+                "complete operator call: HIP prep of Q, K, V + fused attention kernel"
+                if args.two_step
+                else "complete operator call: HIP prep of K, V + fused attention kernel quantising Q in its prologue"
+            ),
             "plan": None,
         },
         "percent_of_int8_peak": round(100 * value / INT8_PEAK_TOPS, 2),

@@ -16,6 +16,11 @@
  *   piper_attention_forward  <- _launch_piper_attention
  *                               src/piper_kernels/attention/piper_attention/triton.py:893-951
  *                               (fused kernel _piper_attention_kernel triton.py:303-635)
+ *   piper_attention_forward_fused
+ *                            <- piper_prepare (Q pass) + piper_attention_forward in one launch;
+ *                               no Piper counterpart.  Precedent: the fused query quantisation
+ *                               flag of SageAttention2++
+ *                               src/piper_kernels/attention/sage_attention_2pp/_policy.py:24,118
  *   piper_prepared_layout    <- the buffer allocations of _prepare_piper_attention
  *                               (triton.py:797-874); the sizes the caller must provide
  *   piper_abi_version,
@@ -129,11 +134,15 @@ typedef struct piper_layout {
   int64_t workspace_bytes; /* scratch for piper_prepare (FP64 mean partials) */
 } piper_layout;
 
+/* piper_prepare_args.flags */
+#define PIPER_PREPARE_SKIP_QUERY 1 /* leave query_code / query_scale alone (they may be NULL):
+                                      for piper_attention_forward_fused, which quantises Q itself */
+
 typedef struct piper_prepare_args {
   int32_t abi_version; /* PIPER_ABI_VERSION */
   int32_t dtype;       /* PIPER_FLOAT16 or PIPER_BFLOAT16: dtype of query, key and value */
   int32_t is_causal;   /* causal calls leave V uncentred (value_mean = 0) */
-  int32_t reserved;
+  int32_t flags;       /* OR of PIPER_PREPARE_* (0: quantise Q, K and V) */
   piper_shape shape;
   piper_tensor query;
   piper_tensor key;
@@ -163,17 +172,38 @@ typedef struct piper_attention_args {
   void* output;            /* [B, H, Sq, D] dense row-major, output_dtype */
 } piper_attention_args;
 
+/* The fused entry point: like piper_attention_forward, but each query wave quantises its own
+ * 32-row query block from `query` in the kernel (the same arithmetic as piper_prepare, so the
+ * result is bit-identical), after a piper_prepare with PIPER_PREPARE_SKIP_QUERY.  Saves the
+ * query pass of the prep and the query-code round trip through HBM. */
+typedef struct piper_attention_fused_args {
+  int32_t abi_version;  /* PIPER_ABI_VERSION */
+  int32_t dtype;        /* of query: PIPER_FLOAT16 or PIPER_BFLOAT16 */
+  int32_t output_dtype; /* PIPER_FLOAT16, PIPER_BFLOAT16 or PIPER_FLOAT32 */
+  int32_t is_causal;
+  int32_t plan;         /* OR of PIPER_PLAN_* bits */
+  float scale;          /* softmax scale, finite and > 0 */
+  piper_shape shape;
+  piper_tensor query;      /* [B, H, Sq, D], the layout rules of piper_prepare_args.query */
+  piper_prepared prepared; /* from piper_prepare; query_code and query_scale are not read */
+  void* output;            /* [B, H, Sq, D] dense row-major, output_dtype */
+} piper_attention_fused_args;
+
 int piper_abi_version(void);
 
 /* Fill *layout with the buffer sizes piper_prepare / piper_attention_forward expect. */
 int piper_prepared_layout(const piper_shape* shape, piper_layout* layout);
 
-/* Quantise Q, K, V into args->prepared on `stream` (a hipStream_t; NULL = default stream).
+/* Quantise Q, K, V into args->prepared on `stream` (a hipStream_t; NULL = default stream);
+ * with PIPER_PREPARE_SKIP_QUERY only K and V.
  * Launches: FP64 mean partials, mean finalisation, one quantisation kernel. */
 int piper_prepare(const piper_prepare_args* args, void* stream);
 
 /* Fused INT8-QK / UINT8-P x INT8-V online-softmax attention on `stream`. */
 int piper_attention_forward(const piper_attention_args* args, void* stream);
+
+/* The same with the query quantised inside the kernel (see piper_attention_fused_args). */
+int piper_attention_forward_fused(const piper_attention_fused_args* args, void* stream);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* piper_last_error(void);

@@ -62,6 +62,71 @@ piper::InputTensor to_input(const piper_tensor& t) {
                             static_cast<long>(t.stride_seq)};
 }
 
+// Validation and launch shared by piper_attention_forward (prepared query codes) and
+// piper_attention_forward_fused (query != NULL: the kernel quantises the query itself).
+int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_causal, int32_t plan,
+                          const piper_shape& s, float scale, const piper_prepared& o, void* output,
+                          const piper_tensor* query, int32_t query_dtype, void* stream) {
+  if (abi_version != PIPER_ABI_VERSION)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", abi_version,
+                PIPER_ABI_VERSION);
+  if (output_dtype != PIPER_FLOAT16 && output_dtype != PIPER_BFLOAT16 && output_dtype != PIPER_FLOAT32)
+    return fail(PIPER_ERROR_UNSUPPORTED, "output dtype must be float16, bfloat16 or float32");
+  if (int st = check_shape(&s)) return st;
+  if (is_causal && s.query_length != s.key_length)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
+  if (!(std::isfinite(scale) && scale > 0.0f))
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
+  if (plan < 0 || plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", plan);
+  if (query != nullptr) {
+    if (query_dtype != PIPER_FLOAT16 && query_dtype != PIPER_BFLOAT16)
+      return fail(PIPER_ERROR_UNSUPPORTED, "query dtype must be float16 or bfloat16");
+    if (int st = check_input("query", *query)) return st;
+  } else if (!o.query_code || !o.query_scale) {
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared query pointer is NULL");
+  } else if (!aligned16(o.query_code)) {
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared query codes must be 16-byte aligned");
+  }
+  if (!o.key_scale || !o.kv_tiles || !o.value_mean || !output)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared input or the output pointer is NULL");
+  if (!aligned16(o.kv_tiles) || !aligned16(o.value_mean) || (reinterpret_cast<uintptr_t>(output) & 7u) != 0)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
+
+  const int waves = (plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
+  piper::AttnParams ap{};
+  ap.query_code = o.query_code;
+  ap.query_scale = o.query_scale;
+  ap.key_scale = o.key_scale;
+  ap.kv_tiles = static_cast<const uint8_t*>(o.kv_tiles);
+  ap.value_mean = o.value_mean;
+  ap.output = output;
+  ap.batch_heads = static_cast<int>(s.batch * s.heads);
+  ap.query_length = static_cast<int>(s.query_length);
+  ap.key_length = static_cast<int>(s.key_length);
+  ap.sq32 = static_cast<int>(ceil_div(s.query_length, PIPER_QUERY_BLOCK) * PIPER_QUERY_BLOCK);
+  ap.sk64 = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK);
+  ap.nqb = ap.sq32 / PIPER_QUERY_BLOCK;
+  ap.nkb = ap.sk64 / PIPER_KEY_BLOCK;
+  ap.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * waves));
+  ap.scale_log2e = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  ap.causal_forward = (plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
+  ap.xcd_remap = (plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
+  ap.heads = static_cast<int>(s.heads);
+  if (query != nullptr) {
+    ap.fused_query = 1;
+    ap.query_bf16 = query_dtype == PIPER_BFLOAT16 ? 1 : 0;
+    ap.query = to_input(*query);
+  }
+  if (static_cast<int64_t>(ap.query_tiles) * ap.batch_heads > 0x7fffffff)
+    return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
+
+  const hipError_t err = piper::launch_attention(static_cast<int>(s.head_dim), is_causal != 0, output_dtype, waves,
+                                                 ap, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "attention launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return PIPER_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -100,14 +165,17 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   if (int st = check_shape(&a->shape)) return st;
   if (a->is_causal && a->shape.query_length != a->shape.key_length)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
-  if (int st = check_input("query", a->query)) return st;
+  if ((a->flags & ~PIPER_PREPARE_SKIP_QUERY) != 0) return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
+  const bool with_query = (a->flags & PIPER_PREPARE_SKIP_QUERY) == 0;
+  if (with_query)
+    if (int st = check_input("query", a->query)) return st;
   if (int st = check_input("key", a->key)) return st;
   if (int st = check_input("value", a->value)) return st;
   const piper_prepared& o = a->prepared;
-  if (!o.query_code || !o.query_scale || !o.key_scale || !o.value_scale || !o.key_mean || !o.value_mean ||
-      !o.kv_tiles)
+  if ((with_query && (!o.query_code || !o.query_scale)) || !o.key_scale || !o.value_scale || !o.key_mean ||
+      !o.value_mean || !o.kv_tiles)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared output pointer is NULL");
-  if (!aligned16(o.query_code) || !aligned16(o.kv_tiles) || !aligned16(o.value_mean))
+  if ((with_query && !aligned16(o.query_code)) || !aligned16(o.kv_tiles) || !aligned16(o.value_mean))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte aligned");
   piper_layout layout;
   if (int st = piper_prepared_layout(&a->shape, &layout)) return st;
@@ -145,7 +213,7 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   qp.sk64 = sk64;
   qp.nqb = sq32 / PIPER_QUERY_BLOCK;
   qp.nkb = sk64 / PIPER_KEY_BLOCK;
-  qp.q_blocks_wg = static_cast<int>(ceil_div(static_cast<int64_t>(bh) * qp.nqb, 4));
+  qp.q_blocks_wg = with_query ? static_cast<int>(ceil_div(static_cast<int64_t>(bh) * qp.nqb, 4)) : 0;
   qp.k_blocks_wg = static_cast<int>(ceil_div(static_cast<int64_t>(bh) * qp.nkb, 4));
   qp.v_blocks_wg = qp.k_blocks_wg;
   qp.center_value = a->is_causal ? 0 : 1;
@@ -165,52 +233,14 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
 
 int piper_attention_forward(const piper_attention_args* a, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
-  if (a->abi_version != PIPER_ABI_VERSION)
-    return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", a->abi_version,
-                PIPER_ABI_VERSION);
-  if (a->output_dtype != PIPER_FLOAT16 && a->output_dtype != PIPER_BFLOAT16 && a->output_dtype != PIPER_FLOAT32)
-    return fail(PIPER_ERROR_UNSUPPORTED, "output dtype must be float16, bfloat16 or float32");
-  if (int st = check_shape(&a->shape)) return st;
-  if (a->is_causal && a->shape.query_length != a->shape.key_length)
-    return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
-  if (!(std::isfinite(a->scale) && a->scale > 0.0f))
-    return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
-  if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
-  const piper_prepared& o = a->prepared;
-  if (!o.query_code || !o.query_scale || !o.key_scale || !o.kv_tiles || !o.value_mean || !a->output)
-    return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared input or the output pointer is NULL");
-  if (!aligned16(o.query_code) || !aligned16(o.kv_tiles) || !aligned16(o.value_mean) ||
-      (reinterpret_cast<uintptr_t>(a->output) & 7u) != 0)
-    return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
+  return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->shape, a->scale,
+                               a->prepared, a->output, nullptr, 0, stream);
+}
 
-  const piper_shape& s = a->shape;
-  const int waves = (a->plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
-  piper::AttnParams ap{};
-  ap.query_code = o.query_code;
-  ap.query_scale = o.query_scale;
-  ap.key_scale = o.key_scale;
-  ap.kv_tiles = static_cast<const uint8_t*>(o.kv_tiles);
-  ap.value_mean = o.value_mean;
-  ap.output = a->output;
-  ap.batch_heads = static_cast<int>(s.batch * s.heads);
-  ap.query_length = static_cast<int>(s.query_length);
-  ap.key_length = static_cast<int>(s.key_length);
-  ap.sq32 = static_cast<int>(ceil_div(s.query_length, PIPER_QUERY_BLOCK) * PIPER_QUERY_BLOCK);
-  ap.sk64 = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK);
-  ap.nqb = ap.sq32 / PIPER_QUERY_BLOCK;
-  ap.nkb = ap.sk64 / PIPER_KEY_BLOCK;
-  ap.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * waves));
-  ap.scale_log2e = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
-  ap.causal_forward = (a->plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
-  ap.xcd_remap = (a->plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
-  if (static_cast<int64_t>(ap.query_tiles) * ap.batch_heads > 0x7fffffff)
-    return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
-
-  const hipError_t err = piper::launch_attention(static_cast<int>(s.head_dim), a->is_causal != 0, a->output_dtype,
-                                                 waves, ap, static_cast<hipStream_t>(stream));
-  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "attention launch failed: %s", hipGetErrorString(err));
-  g_last_error[0] = '\0';
-  return PIPER_OK;
+int piper_attention_forward_fused(const piper_attention_fused_args* a, void* stream) {
+  if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
+  return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->shape, a->scale,
+                               a->prepared, a->output, &a->query, a->dtype, stream);
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@
 //   copied with direct global -> LDS loads into a 6-stage ring, 4 blocks ahead.
 #include "common.h"
 #include "kernels.h"
+#include "quant.h"
 
 namespace piper {
 
@@ -141,6 +142,73 @@ __device__ __forceinline__ void store4(void* out, long index, float a, float b, 
 // (The element arrives as a scalar: this clang's __builtin_bit_cast of an ext_vector
 // subscript reads element 0.)
 __device__ __forceinline__ float unbias(int bits) { return __builtin_bit_cast(float, bits) - kAccBiasValue; }
+
+// A 16-byte global load the compiler does not track: the caller waits for it with an explicit
+// s_waitcnt, which lets later direct LDS copies stay in flight.  (A tracked load would get a
+// compiler wait that also drains every copy issued after it: vmcnt completes in order.)
+__device__ __forceinline__ v4i load_untracked(const void* src) {
+  v4i r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=&v"(r) : "v"(src) : "memory");
+  return r;
+}
+
+// Fused query quantisation, part 1: lane (n, h) issues the loads of elements [32c + 16h, +16)
+// of query row q0 + n (row q0 for rows past the end: their values are replaced by zeros).
+template <int D>
+__device__ __forceinline__ void issue_query_loads(const AttnParams& p, int bh, int q0, int n, int h,
+                                                  v4i (&raw)[D / 16]) {
+  const int b = bh / p.heads;
+  const int head = bh - b * p.heads;
+  const int row = min(q0 + n, p.query_length - 1);
+  const uint16_t* src = static_cast<const uint16_t*>(p.query.data) + b * p.query.stride_batch +
+                        head * p.query.stride_head + static_cast<long>(row) * p.query.stride_seq + 16 * h;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+    raw[2 * c] = load_untracked(src + 32 * c);
+    raw[2 * c + 1] = load_untracked(src + 32 * c + 8);
+  }
+}
+
+// Part 2, after the wait: the wave's 32-row query block quantised in registers exactly as the
+// prep kernel does it (sage/reference.py:61-77: one scale amax / 127 + 1e-7 over the
+// zero-padded 32 x D block, codes round-half-even(x / scale) clamped to +-127).  The block amax
+// is a wave-wide max; the 16 codes of each chunk are packed in element order, the layout of
+// the prepared code rows.  Returns the scale.
+template <int D>
+__device__ __forceinline__ float quantize_query_block(const AttnParams& p, int q0, int n, const v4i (&raw)[D / 16],
+                                                     v4i (&qf)[D / 32]) {
+  constexpr int kChunksD = D / 32;
+  const bool valid = q0 + n < p.query_length;
+  float f[2 * kChunksD][8];
+#pragma unroll
+  for (int i = 0; i < 2 * kChunksD; ++i) {
+    const uint4 bits = valid ? make_uint4(raw[i].x, raw[i].y, raw[i].z, raw[i].w) : make_uint4(0, 0, 0, 0);
+    if (p.query_bf16) widen8<true>(bits, f[i]);
+    else widen8<false>(bits, f[i]);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2 * kChunksD; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[i][e]));
+  amax = wave_max(amax);
+  const float scale = scale_from_amax(amax);
+  const Divisor divisor(scale);
+#pragma unroll
+  for (int c = 0; c < kChunksD; ++c) {
+    uint32_t w[4];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t code[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) code[e] = code_word(f[2 * c + half][e], divisor);
+      w[2 * half] = pack_low_bytes(code[0], code[1], code[2], code[3]);
+      w[2 * half + 1] = pack_low_bytes(code[4], code[5], code[6], code[7]);
+    }
+    qf[c] = v4i{static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]), static_cast<int>(w[3])};
+  }
+  return scale;
+}
 
 // Integer scores S^T = K Q^T of one 64-key block: s[0] keys 0..31, s[1] keys 32..63 (each
 // lane: its query column, keys 16h + r after the K-row permutation).
@@ -319,31 +387,51 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   const int q0 = qtile * (NW * 32) + wave * 32;  // first query of this wave
   const bool wave_live = q0 < p.query_length;
 
-  // Q^T fragments (B operand): query q0 + n, bytes [32c + 16h, +16) of each 32-dim chunk.
-  v4i qf[kChunksD];
-  float cq = 0.0f;
-  if (q0 < p.sq32) {
-    const int8_t* qrow = p.query_code + (static_cast<long>(bh) * p.sq32 + q0 + n) * D + 16 * h;
-#pragma unroll
-    for (int c = 0; c < kChunksD; ++c) qf[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
-    cq = p.query_scale[static_cast<long>(bh) * p.nqb + (q0 >> 5)] * p.scale_log2e;
-  } else {
-#pragma unroll
-    for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
-  }
-  // Settle the Q loads here on every path: a load the compiler still counts as pending at the
-  // loop header would get its wait (in-order vmcnt, so a wait for all direct LDS copies in
-  // flight) inside every iteration.
-#pragma unroll
-  for (int c = 0; c < kChunksD; ++c) asm volatile("" ::"v"(qf[c]));
-  asm volatile("" ::"v"(cq));
-
   int tiles = p.nkb;
   int wave_tiles = wave_live ? p.nkb : 0;
   if constexpr (kCausal) {
     const int last_query = min(p.query_length, (qtile + 1) * NW * 32) - 1;
     tiles = last_query / kKeyBlock + 1;
     wave_tiles = wave_live ? (min(p.query_length, q0 + 32) - 1) / kKeyBlock + 1 : 0;
+  }
+
+  // Q^T fragments (B operand): query q0 + n, bytes [32c + 16h, +16) of each 32-dim chunk.
+  v4i qf[kChunksD];
+  float cq = 0.0f;
+  const bool fused_live = p.fused_query && wave_live;
+  v4i raw[D / 16];
+  if (fused_live) issue_query_loads<D>(p, bh, q0, n, h, raw);
+  if (!p.fused_query && q0 < p.sq32) {
+    const int8_t* qrow = p.query_code + (static_cast<long>(bh) * p.sq32 + q0 + n) * D + 16 * h;
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) qf[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
+    cq = p.query_scale[static_cast<long>(bh) * p.nqb + (q0 >> 5)] * p.scale_log2e;
+    // Settle the prepared Q loads inside this branch: a load the compiler still counts as
+    // pending at the loop header would get its wait (in-order vmcnt, so a wait for all direct
+    // LDS copies in flight) inside every iteration, and a wait at the join would also drain
+    // the untracked query loads of the fused path.
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) asm volatile("" ::"v"(qf[c]));
+    asm volatile("" ::"v"(cq));
+  } else {
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
+  }
+
+  // prologue copies: blocks 0 .. kLead-1 (missing blocks repeat the last one)
+#pragma unroll
+  for (int b = 0; b < kLead; ++b) copy_block<D, NW>(p, smem + b * L::kStageBytes, bh, min(b, tiles - 1), wave, lane);
+
+  if (fused_live) {
+    // wait for the query loads only (issued before this wave's kLead * kRounds or
+    // kLead * (kRounds - 1) copies), then quantise while the copies land
+    if (wave < L::kFullWaves)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLead * L::kRounds) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLead * (L::kRounds - 1)) : "memory");
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
+    cq = quantize_query_block<D>(p, q0, n, raw, qf) * p.scale_log2e;
   }
 
   float num[kChunksD][16];
@@ -358,10 +446,7 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   // register r of lane half h holds key 16h + r.
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
 
-  // prologue: blocks 0 .. kLead-1 (missing blocks repeat the last one), all copies waited for
-#pragma unroll
-  for (int b = 0; b < kLead; ++b) copy_block<D, NW>(p, smem + b * L::kStageBytes, bh, min(b, tiles - 1), wave, lane);
-  stage_barrier<0>();
+  stage_barrier<0>();  // all prologue copies landed
 
   // QK accumulator bias, kept in registers for the whole loop (opaque, so not rematerialised)
   v16i bias = {kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias,

@@ -82,6 +82,12 @@ struct AttnParams {
   float scale_log2e;
   int causal_forward;  // causal grids: 1 = query tiles in forward order, 0 = longest first
   int xcd_remap;       // 1 = consecutive workgroups of a head share an XCD, 0 = hardware order
+  // Fused query quantisation: each wave quantises its own 32-row query block from `query`
+  // (query_code and query_scale are then unused).
+  int fused_query;
+  int query_bf16;
+  int heads;
+  InputTensor query;
 };
 
 hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream);

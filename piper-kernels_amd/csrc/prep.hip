@@ -10,6 +10,7 @@
 // round to FP32).
 #include "common.h"
 #include "kernels.h"
+#include "quant.h"
 
 namespace piper {
 
@@ -103,52 +104,6 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
 // tile.  A workgroup (4 waves) holds units of one kind only, so V workgroups can use
 // workgroup barriers around their LDS transpose.
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
-
-template <int kLanes>
-__device__ __forceinline__ float group_max(float v) {  // max over aligned groups of kLanes lanes
-#pragma unroll
-  for (int m = kLanes / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
-
-__device__ __forceinline__ float scale_from_amax(float amax) {
-  // amax / 127 + 1e-7: correctly rounded FP32 division, then an FP32 add (no contraction).
-  const float q = amax / 127.0f;
-  return __fadd_rn(q, 1e-7f);
-}
-
-// A quantisation scale with its correctly rounded reciprocal, shared by all elements it divides.
-struct Divisor {
-  float s;  // the scale, or 0 for an infinite scale (see quotient)
-  float y;  // RN(1 / scale), IEEE division
-  __device__ explicit Divisor(float scale) : s(__builtin_isinf(scale) ? 0.0f : scale), y(1.0f / scale) {}
-  // RN(x / scale) without a per-element division (Markstein: with y = RN(1/s) and a faithful
-  // q0 = RN(x y), the remainder x - s q0 is exact in one FMA and RN(q0 + r y) = RN(x / s) for
-  // normal x; subnormal x only moves a quotient far below 1/2 by an ulp, so the rounded code is
-  // unchanged).  For an infinite scale (non-finite input) y = 0 and s = 0 give x / inf = +-0
-  // for finite x and NaN for infinite x, as the division does.
-  __device__ float quotient(float x) const {
-    const float q0 = __fmul_rn(x, y);
-    const float r = fmaf(-s, q0, x);
-    return fmaf(r, y, q0);
-  }
-};
-
-__device__ __forceinline__ int code_of(float x, const Divisor& d) {
-  const float r = __builtin_rintf(d.quotient(x));  // round half to even
-  return static_cast<int>(fminf(fmaxf(r, -127.0f), 127.0f));
-}
-
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
-         ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
-}
-
 // Q or K block of kRows rows: one scale over kRows x D values.
 // Codes go to rows of kStride bytes (D for query codes, the padded tile stride for keys).
 template <bool kBf16, int D, int kRows, bool kCenter, int kStride>
@@ -195,13 +150,13 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
     const int row = row0 + it * kRowsPerIter + sub;
     float f[8];
     widen8<kBf16>(raw[it], f);
-    int c[8];
+    uint32_t c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
-      c[i] = code_of(x, divisor);
+      c[i] = code_word(x, divisor);
     }
-    uint2 packed = make_uint2(pack4(c[0], c[1], c[2], c[3]), pack4(c[4], c[5], c[6], c[7]));
+    uint2 packed = make_uint2(pack_low_bytes(c[0], c[1], c[2], c[3]), pack_low_bytes(c[4], c[5], c[6], c[7]));
     *reinterpret_cast<uint2*>(codes + static_cast<long>(it * kRowsPerIter + sub) * kStride + group * 8) = packed;
   }
   if (lane == 0) {

@@ -30,8 +30,11 @@ EXPORTED_SYMBOLS = (
     "piper_prepared_layout",
     "piper_prepare",
     "piper_attention_forward",
+    "piper_attention_forward_fused",
     "piper_last_error",
 )
+
+PREPARE_SKIP_QUERY = 1  # piper_prepare_args.flags
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -102,7 +105,7 @@ class PiperPrepareArgs(ctypes.Structure):
         ("abi_version", _i32),
         ("dtype", _i32),
         ("is_causal", _i32),
-        ("reserved", _i32),
+        ("flags", _i32),
         ("shape", PiperShape),
         ("query", PiperTensor),
         ("key", PiperTensor),
@@ -122,6 +125,21 @@ class PiperAttentionArgs(ctypes.Structure):
         ("shape", PiperShape),
         ("scale", ctypes.c_float),
         ("reserved", _i32),
+        ("prepared", PiperPrepared),
+        ("output", _ptr),
+    ]
+
+
+class PiperAttentionFusedArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("dtype", _i32),
+        ("output_dtype", _i32),
+        ("is_causal", _i32),
+        ("plan", _i32),
+        ("scale", ctypes.c_float),
+        ("shape", PiperShape),
+        ("query", PiperTensor),
         ("prepared", PiperPrepared),
         ("output", _ptr),
     ]
@@ -148,6 +166,8 @@ class NativeLibrary:
         lib.piper_prepare.restype = ctypes.c_int
         lib.piper_attention_forward.argtypes = [ctypes.POINTER(PiperAttentionArgs), _ptr]
         lib.piper_attention_forward.restype = ctypes.c_int
+        lib.piper_attention_forward_fused.argtypes = [ctypes.POINTER(PiperAttentionFusedArgs), _ptr]
+        lib.piper_attention_forward_fused.restype = ctypes.c_int
         version = lib.piper_abi_version()
         if version != ABI_VERSION:
             raise LibraryUnavailableError(
@@ -177,6 +197,11 @@ class NativeLibrary:
 
     def attention_forward(self, args: PiperAttentionArgs, stream: int) -> None:
         self._check(self._lib.piper_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_attention_forward")
+
+    def attention_forward_fused(self, args: PiperAttentionFusedArgs, stream: int) -> None:
+        self._check(
+            self._lib.piper_attention_forward_fused(ctypes.byref(args), _ptr(stream)), "piper_attention_forward_fused"
+        )
 
 
 _lock = threading.Lock()

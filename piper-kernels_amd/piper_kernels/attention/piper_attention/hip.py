@@ -12,7 +12,7 @@ current stream and never synchronises.
 from __future__ import annotations
 
 import ctypes
-from dataclasses import dataclass
+from dataclasses import dataclass, replace
 
 import torch
 
@@ -27,8 +27,8 @@ ACC_BIAS = 0x4B400000  # integer accumulator bias: bits read as FP32 1.5 * 2^23 
 class PreparedPiperAttention:
     """Quantised operands (layouts documented in ``include/piper_mi355x.h``)."""
 
-    query_code: torch.Tensor  # int8 [B, H, Sq32, D]
-    query_scale: torch.Tensor  # fp32 [B, H, Sq32/32]
+    query_code: torch.Tensor | None  # int8 [B, H, Sq32, D]; None when the kernel quantises Q
+    query_scale: torch.Tensor | None  # fp32 [B, H, Sq32/32]; None when the kernel quantises Q
     key_scale: torch.Tensor  # fp32 [B, H, Sk64/64]
     value_scale: torch.Tensor  # fp32 [B, H, Sk64]
     key_mean: torch.Tensor  # fp32 [B, H, D]
@@ -39,11 +39,17 @@ class PreparedPiperAttention:
     scale: float
     is_causal: bool
     plan: MI355XPlan
+    query: torch.Tensor | None = None  # [B, H, Sq, D] input, kept for the fused launch
+
+    @property
+    def fused_query(self) -> bool:
+        """True when the attention kernel quantises the query itself (no query codes here)."""
+        return self.query_code is None
 
     def native_prepared(self) -> native.PiperPrepared:
         return native.PiperPrepared(
-            self.query_code.data_ptr(),
-            self.query_scale.data_ptr(),
+            None if self.query_code is None else self.query_code.data_ptr(),
+            None if self.query_scale is None else self.query_scale.data_ptr(),
             self.key_scale.data_ptr(),
             self.value_scale.data_ptr(),
             self.key_mean.data_ptr(),
@@ -105,8 +111,14 @@ def _prepare_piper_attention(
     *,
     plan: MI355XPlan | None = None,
     workspace: torch.Tensor | None = None,
+    quantize_query: bool = True,
 ) -> PreparedPiperAttention:
-    """Quantise Q/K/V on the GPU (one HIP prep pipeline) and allocate the output."""
+    """Quantise Q/K/V on the GPU (one HIP prep pipeline) and allocate the output.
+
+    With ``quantize_query=False`` only K and V are quantised and the bundle keeps the query
+    itself: ``_launch_piper_attention`` then runs the fused entry point, whose kernel
+    quantises each query block in its prologue (bit-identical codes and scales).
+    """
     lib = native.load_library()
     batch, heads, sq, d = query.shape
     sk = key.shape[2]
@@ -123,8 +135,8 @@ def _prepare_piper_attention(
         return torch.empty(shape_, device=device, dtype=dtype)
 
     prepared = PreparedPiperAttention(
-        query_code=empty((batch, heads, sq32, d), torch.int8),
-        query_scale=empty((batch, heads, sq32 // native.QUERY_BLOCK), torch.float32),
+        query_code=empty((batch, heads, sq32, d), torch.int8) if quantize_query else None,
+        query_scale=empty((batch, heads, sq32 // native.QUERY_BLOCK), torch.float32) if quantize_query else None,
         key_scale=empty((batch, heads, nkb), torch.float32),
         value_scale=empty((batch, heads, sk64), torch.float32),
         key_mean=empty((batch, heads, d), torch.float32),
@@ -136,16 +148,18 @@ def _prepare_piper_attention(
         is_causal=bool(is_causal),
         plan=plan,
     )
+    query, q_arg = _native_input(query)
+    if not quantize_query:
+        prepared = replace(prepared, query=query)
     if workspace is None or workspace.numel() < layout.workspace_bytes:
         workspace = empty((max(layout.workspace_bytes, 1),), torch.uint8)
-    query, q_arg = _native_input(query)
     key, k_arg = _native_input(key)
     value, v_arg = _native_input(value)
     args = native.PiperPrepareArgs(
         abi_version=native.ABI_VERSION,
         dtype=_DTYPE_CODES[query.dtype],
         is_causal=int(bool(is_causal)),
-        reserved=0,
+        flags=0 if quantize_query else native.PREPARE_SKIP_QUERY,
         shape=shape,
         query=q_arg,
         key=k_arg,
@@ -166,12 +180,36 @@ def _prepare_piper_attention(
 def _launch_piper_attention(
     prepared: PreparedPiperAttention, *, output: torch.Tensor | None = None
 ) -> torch.Tensor:
-    """Run only the fused kernel on prepared operands; ``output`` may be FP32 for tests."""
+    """Run only the fused kernel on prepared operands; ``output`` may be FP32 for tests.
+
+    A bundle prepared with ``quantize_query=False`` goes through
+    ``piper_attention_forward_fused`` (query quantisation in the kernel prologue).
+    """
     lib = native.load_library()
     batch, heads, sq, sk, d = prepared.shape
     out = prepared.output if output is None else output
     if out.shape != (batch, heads, sq, d) or not out.is_contiguous() or out.dtype not in _DTYPE_CODES:
         raise ValueError("output must be a contiguous [B, H, Sq, D] float16/bfloat16/float32 tensor")
+    device = out.device
+    if prepared.fused_query:
+        query = prepared.query
+        fused = native.PiperAttentionFusedArgs(
+            abi_version=native.ABI_VERSION,
+            dtype=_DTYPE_CODES[query.dtype],
+            output_dtype=_DTYPE_CODES[out.dtype],
+            is_causal=int(prepared.is_causal),
+            plan=prepared.plan.plan_id,
+            scale=ctypes.c_float(prepared.scale).value,
+            shape=_native_shape(batch, heads, sq, sk, d),
+            query=native.PiperTensor(query.data_ptr(), *query.stride()[:3]),
+            prepared=prepared.native_prepared(),
+            output=out.data_ptr(),
+        )
+        with torch.cuda.device(device):
+            stream = torch.cuda.current_stream(device)
+            lib.attention_forward_fused(fused, stream.cuda_stream)
+        query.record_stream(stream)
+        return out
     args = native.PiperAttentionArgs(
         abi_version=native.ABI_VERSION,
         output_dtype=_DTYPE_CODES[out.dtype],
@@ -183,7 +221,6 @@ def _launch_piper_attention(
         prepared=prepared.native_prepared(),
         output=out.data_ptr(),
     )
-    device = out.device
     with torch.cuda.device(device):
         lib.attention_forward(args, torch.cuda.current_stream(device).cuda_stream)
     return out
@@ -197,8 +234,11 @@ def _run_piper_attention(
     is_causal: bool,
     *,
     plan: MI355XPlan | None = None,
+    fuse_query: bool = True,
 ) -> torch.Tensor:
-    prepared = _prepare_piper_attention(query, key, value, scale, is_causal, plan=plan)
+    """The operator: prep of K and V, then the attention kernel, which quantises the query in
+    its prologue (``fuse_query=False``: the prep quantises Q too; the output is the same)."""
+    prepared = _prepare_piper_attention(query, key, value, scale, is_causal, plan=plan, quantize_query=not fuse_query)
     return _launch_piper_attention(prepared)
 
 
@@ -210,7 +250,8 @@ def hip_piper_attention(
     scale: float,
     is_causal: bool,
 ) -> torch.Tensor:
-    """Piper Attention prep + fused INT8 kernel on MI355X (schema of triton.py:984-999)."""
+    """Piper Attention K/V prep + fused INT8 kernel (query quantised in its prologue) on MI355X
+    (schema of triton.py:984-999)."""
     return _run_piper_attention(query, key, value, scale, is_causal)
 
 

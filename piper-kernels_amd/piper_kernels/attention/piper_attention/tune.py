@@ -7,12 +7,16 @@ query-tile order, XCD-aware workgroup order), quality-gated, whose result is fro
 
     python -m piper_kernels.attention.piper_attention.tune --workloads c1 c2 c3 c4 c5 --write
 
-For each shape: synthetic inputs are prepared once; every candidate plan is launched on the
-same prepared operands, timed with HIP events on the launch stream (warm-up, then rounds that
-interleave the candidates so clock drift does not favour one), and gated: its FP32 output must
-equal the default plan's bit for bit (every plan performs the same arithmetic per query; only
-the order of workgroups differs). The fastest passing plan is recorded; a plan within
-``--margin`` of the default keeps the default.
+For each shape: synthetic inputs are prepared once (K and V; the kernel quantises the query,
+as the operator runs it); every candidate plan is launched on the same prepared operands and
+gated: its FP32 output must equal the default plan's bit for bit (every plan performs the
+same arithmetic per query; only the order of workgroups differs).  Timing: the GPU first runs
+the candidates for ``--warmup-ms`` so the clock has ramped, then ``--rounds`` rounds each
+launch every candidate ``--launches`` times back to back, bracketed by HIP events on the
+launch stream with no host synchronisation inside a round (the GPU never idles between
+candidates), in an order rotated by one each round (no candidate always runs first).  The
+fastest passing plan by median is recorded; a plan within ``--margin`` of the default keeps
+the default.
 """
 
 from __future__ import annotations
@@ -36,7 +40,7 @@ def candidate_plans(is_causal: bool):
     return [MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x) for w, o, x in product((8, 4), orders, (True, False))]
 
 
-def tune_shape(q, k, v, is_causal: bool, *, warmup: int, rounds: int, launches: int, margin: float) -> dict:
+def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launches: int, margin: float) -> dict:
     import torch
 
     from piper_kernels.attention.piper_attention._plan import MI355XPlan, shape_key
@@ -45,7 +49,7 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup: int, rounds: int, launches: 
     b, h, sq, d = q.shape
     sk = k.shape[2]
     default = MI355XPlan()
-    prepared = _prepare_piper_attention(q, k, v, d**-0.5, is_causal, plan=default)
+    prepared = _prepare_piper_attention(q, k, v, d**-0.5, is_causal, plan=default, quantize_query=False)
     plans = candidate_plans(is_causal)
     reference = torch.empty(q.shape, device=q.device, dtype=torch.float32)
     _launch_piper_attention(prepared, output=reference)
@@ -56,19 +60,30 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup: int, rounds: int, launches: 
         torch.cuda.synchronize()
         passed[plan] = bool(torch.equal(candidate_out, reference))
     times = {plan: [] for plan in plans}
-    for plan in plans:
-        for _ in range(warmup):
-            _launch_piper_attention(replace(prepared, plan=plan))
+    runs = {plan: replace(prepared, plan=plan) for plan in plans}
     stream = torch.cuda.current_stream()
-    for _ in range(rounds):
+    warm_start = torch.cuda.Event(enable_timing=True)
+    warm_start.record(stream)
+    while True:
         for plan in plans:
-            run = replace(prepared, plan=plan)
+            _launch_piper_attention(runs[plan])
+        warm_end = torch.cuda.Event(enable_timing=True)
+        warm_end.record(stream)
+        warm_end.synchronize()
+        if warm_start.elapsed_time(warm_end) >= warmup_ms:
+            break
+    for r in range(rounds):
+        order = plans[r % len(plans) :] + plans[: r % len(plans)]
+        events = []
+        for plan in order:
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record(stream)
             for _ in range(launches):
-                _launch_piper_attention(run)
+                _launch_piper_attention(runs[plan])
             end.record(stream)
-            end.synchronize()
+            events.append((plan, start, end))
+        torch.cuda.synchronize()
+        for plan, start, end in events:
             times[plan].append(start.elapsed_time(end) / launches)
     medians = {plan: statistics.median(ts) for plan, ts in times.items()}
     best = min((p for p in plans if passed[p]), key=lambda p: medians[p])
@@ -90,8 +105,8 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup: int, rounds: int, launches: 
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--workloads", nargs="+", default=["c1", "c2", "c3", "c4", "c5"])
-    parser.add_argument("--warmup", type=int, default=3)
-    parser.add_argument("--rounds", type=int, default=5)
+    parser.add_argument("--warmup-ms", type=float, default=1000.0, help="GPU time of warm-up launches per shape")
+    parser.add_argument("--rounds", type=int, default=8)
     parser.add_argument("--launches", type=int, default=3)
     parser.add_argument("--margin", type=float, default=0.01, help="minimum gain over the default plan")
     parser.add_argument("--write", action="store_true", help="write the frozen table next to _plan.py")
@@ -109,8 +124,8 @@ def main(argv: list[str] | None = None) -> int:
         for name in args.workloads:
             w = WORKLOADS[name]
             q, k, v = make_inputs(w, device)
-            entry = tune_shape(q, k, v, w.is_causal, warmup=args.warmup, rounds=args.rounds, launches=args.launches,
-                               margin=args.margin)
+            entry = tune_shape(q, k, v, w.is_causal, warmup_ms=args.warmup_ms, rounds=args.rounds,
+                               launches=args.launches, margin=args.margin)
             entry["workload"] = name
             entries.append(entry)
             print(f"[tune] {name}: default {entry['default_ms']:.4f} ms, chosen {entry['plan']} {entry['chosen_ms']:.4f} ms",

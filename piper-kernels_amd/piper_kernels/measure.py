@@ -110,12 +110,20 @@ def measure_quality(actual: torch.Tensor, reference: torch.Tensor) -> QualityMet
 
 
 def prep_algorithmic_bytes(
-    batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool
+    batch: int,
+    heads: int,
+    query_length: int,
+    key_length: int,
+    head_dim: int,
+    is_causal: bool,
+    quantize_query: bool = True,
 ) -> int:
     """Minimum HBM bytes of the prep stage: fp16/bf16 reads of Q, K, V, int8 code writes,
-    FP32 scales (Q per 32 rows, K per 64 rows, V per key) and the K/V means."""
-    eq = batch * heads * query_length * head_dim
+    FP32 scales (Q per 32 rows, K per 64 rows, V per key) and the K/V means.  Without the
+    query (``quantize_query=False``: the attention kernel quantises it) only K and V count."""
+    eq = batch * heads * query_length * head_dim if quantize_query else 0
     ekv = batch * heads * key_length * head_dim
-    scales = 4 * batch * heads * (-(-query_length // 32) + -(-key_length // 64) + key_length)
+    q_scales = -(-query_length // 32) if quantize_query else 0
+    scales = 4 * batch * heads * (q_scales + -(-key_length // 64) + key_length)
     means = (4 if is_causal else 8) * batch * heads * head_dim
     return 2 * (eq + 2 * ekv) + (eq + 2 * ekv) + scales + means

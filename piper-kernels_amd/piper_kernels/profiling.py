@@ -1,9 +1,11 @@
 """Focused GPU workloads for rocprofv3 runs (kernel traces and PMC counters).
 
     python -m piper_kernels.profiling attention --workload c3 --launches 3
-        prepare one workload once, then launch only the fused attention kernel
+        prepare one workload once, then launch only the fused attention kernel (the operator's
+        path: the kernel quantises the query itself; --two-step: prepared query codes)
     python -m piper_kernels.profiling prep --workload c3 --launches 3
-        run only the prep pipeline (mean partials, mean finalisation, quantisation)
+        run only the prep pipeline (mean partials, mean finalisation, quantisation; K and V
+        only unless --two-step)
     python -m piper_kernels.profiling copy --bytes 1073741824 --launches 3
         a plain device-to-device copy of a known size: the calibration that turns
         FETCH_SIZE / WRITE_SIZE counter readings into bytes
@@ -30,6 +32,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--workload", default="c3")
     parser.add_argument("--launches", type=int, default=3)
     parser.add_argument("--bytes", type=int, default=1 << 30)
+    parser.add_argument("--two-step", action="store_true", help="quantise the query in the prep, not the kernel")
     args = parser.parse_args(argv)
 
     import torch
@@ -49,13 +52,14 @@ def main(argv: list[str] | None = None) -> int:
     w = WORKLOADS[args.workload]
     q, k, v = make_inputs(w, device)
     scale = w.head_dim**-0.5
+    fused = not args.two_step
     with torch.no_grad():
-        prepared = _prepare_piper_attention(q, k, v, scale, w.is_causal)
+        prepared = _prepare_piper_attention(q, k, v, scale, w.is_causal, quantize_query=not fused)
         for _ in range(args.launches):
             if args.what == "attention":
                 _launch_piper_attention(prepared)
             else:
-                _prepare_piper_attention(q, k, v, scale, w.is_causal)
+                _prepare_piper_attention(q, k, v, scale, w.is_causal, quantize_query=not fused)
     torch.cuda.synchronize()
     print(f"{args.what} {args.workload} x {args.launches} done", flush=True)
     return 0

@@ -42,11 +42,13 @@ def load_golden(path: Path) -> dict:
     return data
 
 
-def gpu_prepare(q, k, v, scale, is_causal, device, plan=None):
+def gpu_prepare(q, k, v, scale, is_causal, device, plan=None, quantize_query=True):
     from piper_kernels.attention.piper_attention.hip import _prepare_piper_attention
 
     with torch.no_grad():
-        prepared = _prepare_piper_attention(q.to(device), k.to(device), v.to(device), scale, is_causal, plan=plan)
+        prepared = _prepare_piper_attention(
+            q.to(device), k.to(device), v.to(device), scale, is_causal, plan=plan, quantize_query=quantize_query
+        )
     torch.cuda.synchronize(device)
     return prepared
 

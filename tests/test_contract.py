@@ -267,6 +267,9 @@ def test_effective_operations_account_for_causal_triangle() -> None:
 
 def test_prep_algorithmic_bytes_for_headline_shape() -> None:
     assert prep_algorithmic_bytes(1, 24, 16384, 16384, 128, False) == 454_656_000
+    # without the query: fp16 read (2 B), code write (1 B) and one scale per 32 rows of Q drop out
+    q_bytes = 3 * 24 * 16384 * 128 + 4 * 24 * 512
+    assert prep_algorithmic_bytes(1, 24, 16384, 16384, 128, False, quantize_query=False) == 454_656_000 - q_bytes
 
 
 def test_workload_inputs_are_reproducible_per_head() -> None:

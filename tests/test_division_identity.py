@@ -1,11 +1,17 @@
-"""The prep kernels' quantisation quotient equals IEEE division on the codes it produces.
+"""The kernels' quantisation codes equal clip(rint(x / s), -127, 127) with IEEE division.
 
-``csrc/prep.hip`` (``Divisor``) computes round-half-even(x / s) as rint(fma(fma(-s, q0, x), y, q0))
-with y = RN(1/s) and q0 = RN(x * y), once per element, instead of an IEEE division per
-element.  This checks that identity against IEEE single-precision division with gcc's
-correctly rounded ``fmaf`` on the scales prep produces (s = amax/127 + 1e-7, |x| <= amax):
-random elements and elements constructed within a few ulps of half-integers (where a
-one-ulp quotient error would flip the code), and the infinite-scale case.
+``csrc/quant.h`` computes the code of x in two steps, once per element:
+
+* the quotient RN(x / s) as fma(fma(-s, q0, x), y, q0) with y = RN(1/s) and q0 = RN(x * y)
+  (``Divisor``), instead of an IEEE division per element;
+* the rounded code as the low byte of the bits of RN(quotient + 1.5 * 2^23) (``code_word``),
+  instead of rint, a clamp and a conversion: that add rounds half to even, and the clamp never
+  acts because |x| <= amax bounds the quotient by 127 (1 + 2^-23).
+
+This checks both against IEEE single-precision division, rintf and the clamp, with gcc's
+correctly rounded ``fmaf`` on the scales the kernels produce (s = amax/127 + 1e-7, |x| <= amax):
+random elements, elements within a few ulps of half-integers (where a one-ulp quotient error
+would flip the code), x = +-amax (the largest quotients), and the infinite-scale case.
 """
 
 from __future__ import annotations
@@ -32,15 +38,22 @@ static inline float quotient(float x, float scale) {
   return fmaf(r, y, q0);
 }
 static inline float code(float q) { return fminf(fmaxf(rintf(q), -127.0f), 127.0f); }
+static inline float code_magic(float q) {
+  const float t = q + 12582912.0f;
+  uint32_t bits;
+  memcpy(&bits, &t, 4);
+  return (float)(int8_t)(bits & 0xffu);
+}
 int main(void) {
-  long n = 0, bad = 0, near = 0;
+  long n = 0, bad = 0, near = 0, edge = 0;
   for (long it = 0; it < 3000000L; ++it) {
     float amax = ldexpf(1.0f + u01(), (int)(rnd() % 44) - 26);
     if (rnd() % 3 == 0) amax = (float)((rnd() % 65504) + 1) / 64.0f;
     const float s = amax / 127.0f + 1e-7f;
     float x;
-    switch (rnd() % 3) {
+    switch (rnd() % 4) {
       case 0: x = amax * (2.0f * u01() - 1.0f); break;
+      case 3: x = (rnd() & 1) ? amax : -amax; ++edge; break;
       case 1: {
         const float k = (float)((int)(rnd() % 255) - 127) + 0.5f;
         x = k * s;
@@ -57,6 +70,7 @@ int main(void) {
     if (!(fabsf(x) <= amax)) continue;
     ++n;
     bad += code(quotient(x, s)) != code(x / s);
+    bad += code_magic(quotient(x, s)) != code(x / s);
   }
   /* infinite scale (non-finite input): finite x -> signed zero quotient, infinite x -> NaN */
   const float inf = INFINITY;
@@ -66,18 +80,19 @@ int main(void) {
     bad += memcmp(&a, &b, 4) != 0;
   }
   bad += !isnan(quotient(inf, inf));
-  printf("%ld %ld %ld\n", n, near, bad);
+  bad += code_magic(quotient(inf, inf)) != 0.0f; /* NaN quotient -> code 0 */
+  printf("%ld %ld %ld %ld\n", n, near, edge, bad);
   return 0;
 }
 """
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
-def test_fma_quotient_matches_ieee_division_codes(tmp_path: Path) -> None:
+def test_kernel_codes_match_ieee_division_rint_and_clamp(tmp_path: Path) -> None:
     src = tmp_path / "division_identity.c"
     exe = tmp_path / "division_identity"
     src.write_text(SOURCE)
     subprocess.run(["gcc", "-O2", "-ffp-contract=off", str(src), "-o", str(exe), "-lm"], check=True)
-    n, near, bad = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
-    assert n > 2_000_000 and near > 1_000_000
+    n, near, edge, bad = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
+    assert n > 2_000_000 and near > 1_000_000 and edge > 500_000
     assert bad == 0

@@ -46,6 +46,7 @@ def test_ctypes_structures_match_the_c_header(tmp_path) -> None:
         "piper_layout": native.PiperLayout,
         "piper_prepare_args": native.PiperPrepareArgs,
         "piper_attention_args": native.PiperAttentionArgs,
+        "piper_attention_fused_args": native.PiperAttentionFusedArgs,
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "piper_mi355x.h"', "int main(void) {"]
     for cname, cls in structs.items():
@@ -136,3 +137,57 @@ def test_attention_validates_before_launching(lib) -> None:
     args.shape = native.PiperShape(1, 1, 8, 9, 64)
     with pytest.raises(RuntimeError, match="equal query and key lengths"):
         lib.attention_forward(args, 0)
+
+
+def test_prepare_flags(lib) -> None:
+    args = native.PiperPrepareArgs(abi_version=native.ABI_VERSION, dtype=native.FLOAT16, shape=native.PiperShape(1, 1, 8, 8, 64))
+    args.flags = 2
+    with pytest.raises(RuntimeError, match="unknown flags"):
+        lib.prepare(args, 0)
+    # skipping the query: its (NULL) pointer is not inspected, the key's is
+    args.flags = native.PREPARE_SKIP_QUERY
+    with pytest.raises(RuntimeError, match="key pointer is NULL"):
+        lib.prepare(args, 0)
+    fake = 0x1000
+    args.key = native.PiperTensor(fake, 512, 512, 64)
+    args.value = native.PiperTensor(fake, 512, 512, 64)
+    args.prepared = native.PiperPrepared(None, None, fake, fake, fake, fake, fake)
+    args.workspace, args.workspace_bytes = None, 0
+    with pytest.raises(RuntimeError, match="workspace"):
+        lib.prepare(args, 0)
+    args.flags = 0
+    args.query = native.PiperTensor(fake, 512, 512, 64)
+    with pytest.raises(RuntimeError, match="prepared output pointer is NULL"):
+        lib.prepare(args, 0)
+
+
+def test_fused_attention_validates_before_launching(lib) -> None:
+    fake = 0x1000
+    args = native.PiperAttentionFusedArgs(
+        abi_version=native.ABI_VERSION,
+        dtype=native.FLOAT32,
+        output_dtype=native.FLOAT16,
+        shape=native.PiperShape(1, 1, 8, 8, 64),
+        scale=0.125,
+        query=native.PiperTensor(fake, 512, 512, 64),
+        # no query codes or scales: the fused kernel quantises the query itself
+        prepared=native.PiperPrepared(None, None, fake, fake, fake, fake, fake),
+    )
+    with pytest.raises(RuntimeError, match="query dtype"):
+        lib.attention_forward_fused(args, 0)
+    args.dtype = native.BFLOAT16
+    args.query = native.PiperTensor(None, 512, 512, 64)
+    with pytest.raises(RuntimeError, match="query pointer is NULL"):
+        lib.attention_forward_fused(args, 0)
+    args.query = native.PiperTensor(fake + 2, 512, 512, 64)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        lib.attention_forward_fused(args, 0)
+    args.query = native.PiperTensor(fake, 512, 512, 64)
+    with pytest.raises(RuntimeError, match="output pointer is NULL"):
+        lib.attention_forward_fused(args, 0)
+    args.plan = 8
+    with pytest.raises(RuntimeError, match="unknown plan"):
+        lib.attention_forward_fused(args, 0)
+    args.plan, args.abi_version = 0, 2
+    with pytest.raises(RuntimeError, match="ABI version mismatch"):
+        lib.attention_forward_fused(args, 0)
