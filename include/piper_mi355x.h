@@ -21,6 +21,14 @@
  *                               no Piper counterpart.  Precedent: the fused query quantisation
  *                               flag of SageAttention2++
  *                               src/piper_kernels/attention/sage_attention_2pp/_policy.py:24,118
+ *   piper_sage_prepare       <- the K/V part of _prepare_sage_attention_2pp
+ *                               src/piper_kernels/attention/sage_attention_2pp/triton.py:1000-1063
+ *                               (statistics :60-151, FP8 V :154-195, K codes through
+ *                               qk_quantization.prepare_key, as reference.py:44-49)
+ *   piper_sage_attention_forward <- _launch_sage_attention_2pp (triton.py:1066-1102) with the
+ *                               fused query quantisation of _prepare_query (:983-997);
+ *                               kernel _sage_attention_2pp_kernel (:513-788)
+ *   piper_sage_prepared_layout <- the buffer allocations of _prepare_sage_attention_2pp
  *   piper_prepared_layout    <- the buffer allocations of _prepare_piper_attention
  *                               (triton.py:797-874); the sizes the caller must provide
  *   piper_abi_version,
@@ -189,6 +197,62 @@ typedef struct piper_attention_fused_args {
   void* output;            /* [B, H, Sq, D] dense row-major, output_dtype */
 } piper_attention_fused_args;
 
+/* ---------------------------------------------------------------------------------------
+ * SageAttention2++ (src/piper_kernels/attention/sage_attention_2pp/, reference.py:15-104):
+ * INT8 Q/K with K smoothing (per 32 query rows / 64 key rows), per-channel FP8 E4M3 V
+ * (scale = amax_S|v| / 2.25 + 1e-7), FP8 probabilities in a frame shifted by ln 448.
+ * The prep quantises K and V; the attention kernel quantises each query block itself.
+ *
+ * Tile record (PIPER_SAGE_TILE_BYTES(D) bytes per 64 keys, the kernel's LDS stage image):
+ *   [0, PIPER_SAGE_V_OFFSET(D))  int8 K codes [64][D] in rows of D + 16 bytes; bytes
+ *                                [D, D + 4) of row 0 hold the tile's K scale (float)
+ *   [PIPER_SAGE_V_OFFSET(D), +80 * D)  FP8 E4M3 V^T codes [D][64] in rows of 80 bytes
+ *   padding to a KiB multiple; padding bytes are unspecified.
+ * ------------------------------------------------------------------------------------- */
+#define PIPER_SAGE_V_OFFSET(head_dim) (64 * ((head_dim) + 16))
+#define PIPER_SAGE_TILE_BYTES(head_dim) ((PIPER_SAGE_V_OFFSET(head_dim) + 80 * (head_dim) + 1023) / 1024 * 1024)
+
+typedef struct piper_sage_prepared {
+  float* key_scale;   /* [B, H, Sk64/64] INT8 K scales */
+  float* key_mean;    /* [B, H, D] the K smoothing mean (order-defined, as piper_prepared) */
+  float* value_scale; /* [B, H, D] FP8 V scales, per channel */
+  void* kv_tiles;     /* [B, H, Sk64/64] tile records, 16-byte aligned */
+} piper_sage_prepared;
+
+typedef struct piper_sage_layout {
+  int64_t key_scale_bytes;
+  int64_t mean_bytes;        /* key_mean and value_scale, each */
+  int64_t kv_tile_bytes;     /* one tile record */
+  int64_t kv_tiles_bytes;    /* all tile records */
+  int64_t workspace_bytes;   /* scratch for piper_sage_prepare */
+} piper_sage_layout;
+
+typedef struct piper_sage_prepare_args {
+  int32_t abi_version; /* PIPER_ABI_VERSION */
+  int32_t dtype;       /* PIPER_FLOAT16 or PIPER_BFLOAT16: dtype of key and value */
+  int32_t reserved0;
+  int32_t reserved1;
+  piper_shape shape;   /* query_length is not used by the prep */
+  piper_tensor key;
+  piper_tensor value;
+  piper_sage_prepared prepared; /* outputs */
+  void* workspace;
+  int64_t workspace_bytes;
+} piper_sage_prepare_args;
+
+typedef struct piper_sage_attention_args {
+  int32_t abi_version;  /* PIPER_ABI_VERSION */
+  int32_t dtype;        /* of query: PIPER_FLOAT16 or PIPER_BFLOAT16 */
+  int32_t output_dtype; /* PIPER_FLOAT16, PIPER_BFLOAT16 or PIPER_FLOAT32 */
+  int32_t is_causal;
+  int32_t plan;         /* OR of PIPER_PLAN_* bits (the same launch plans) */
+  float scale;          /* softmax scale, finite and > 0 */
+  piper_shape shape;
+  piper_tensor query;   /* [B, H, Sq, D], the layout rules of piper_prepare_args.query */
+  piper_sage_prepared prepared; /* from piper_sage_prepare */
+  void* output;         /* [B, H, Sq, D] dense row-major, output_dtype */
+} piper_sage_attention_args;
+
 int piper_abi_version(void);
 
 /* Fill *layout with the buffer sizes piper_prepare / piper_attention_forward expect. */
@@ -204,6 +268,12 @@ int piper_attention_forward(const piper_attention_args* args, void* stream);
 
 /* The same with the query quantised inside the kernel (see piper_attention_fused_args). */
 int piper_attention_forward_fused(const piper_attention_fused_args* args, void* stream);
+
+/* SageAttention2++: buffer sizes, K/V prep (statistics, INT8 K, FP8 V^T tile records) and the
+ * fused attention kernel (INT8 QK, FP8 PV on v_mfma_f32_32x32x64_f8f6f4, FP32 accumulation). */
+int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layout);
+int piper_sage_prepare(const piper_sage_prepare_args* args, void* stream);
+int piper_sage_attention_forward(const piper_sage_attention_args* args, void* stream);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* piper_last_error(void);

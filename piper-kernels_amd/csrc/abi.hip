@@ -16,6 +16,9 @@ static_assert(PIPER_KV_TILE_BYTES(128) == piper::kv_tile_bytes(128), "tile recor
 static_assert(PIPER_KV_V_OFFSET(128) == piper::kv_v_offset(128), "V^T offset");
 static_assert(PIPER_KV_LOG2_OFFSET(128) == piper::kv_log_offset(128), "log2 offset");
 static_assert(PIPER_KV_LOG2_OFFSET(64) == piper::kv_log_offset(64), "log2 offset");
+static_assert(PIPER_SAGE_TILE_BYTES(64) == piper::sage_tile_bytes(64), "SageAttention2++ record size (D = 64)");
+static_assert(PIPER_SAGE_TILE_BYTES(128) == piper::sage_tile_bytes(128), "SageAttention2++ record size (D = 128)");
+static_assert(PIPER_SAGE_V_OFFSET(128) == piper::sage_v_offset(128), "SageAttention2++ V^T offset");
 
 namespace {
 
@@ -241,6 +244,132 @@ int piper_attention_forward_fused(const piper_attention_fused_args* a, void* str
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
   return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->shape, a->scale,
                                a->prepared, a->output, &a->query, a->dtype, stream);
+}
+
+int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layout) {
+  if (int st = check_shape(shape)) return st;
+  if (layout == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "layout is NULL");
+  const int64_t bh = shape->batch * shape->heads;
+  const int64_t d = shape->head_dim;
+  const int64_t nkb = ceil_div(shape->key_length, PIPER_KEY_BLOCK);
+  const int64_t chunks = ceil_div(shape->key_length, PIPER_MEAN_CHUNK);
+  layout->key_scale_bytes = bh * nkb * 4;
+  layout->mean_bytes = bh * d * 4;
+  layout->kv_tile_bytes = PIPER_SAGE_TILE_BYTES(d);
+  layout->kv_tiles_bytes = bh * nkb * PIPER_SAGE_TILE_BYTES(d);
+  layout->workspace_bytes = 2 * bh * chunks * d * 8;
+  g_last_error[0] = '\0';
+  return PIPER_OK;
+}
+
+int piper_sage_prepare(const piper_sage_prepare_args* a, void* stream) {
+  if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != PIPER_ABI_VERSION)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", a->abi_version,
+                PIPER_ABI_VERSION);
+  if (a->dtype != PIPER_FLOAT16 && a->dtype != PIPER_BFLOAT16)
+    return fail(PIPER_ERROR_UNSUPPORTED, "input dtype must be float16 or bfloat16");
+  if (int st = check_shape(&a->shape)) return st;
+  if (int st = check_input("key", a->key)) return st;
+  if (int st = check_input("value", a->value)) return st;
+  const piper_sage_prepared& o = a->prepared;
+  if (!o.key_scale || !o.key_mean || !o.value_scale || !o.kv_tiles)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared output pointer is NULL");
+  if (!aligned16(o.kv_tiles) || !aligned16(o.value_scale))
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte aligned");
+  piper_sage_layout layout;
+  if (int st = piper_sage_prepared_layout(&a->shape, &layout)) return st;
+  if (a->workspace == nullptr || a->workspace_bytes < layout.workspace_bytes)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "workspace needs %lld bytes, got %lld",
+                (long long)layout.workspace_bytes, (long long)a->workspace_bytes);
+
+  const piper_shape& s = a->shape;
+  const int bh = static_cast<int>(s.batch * s.heads);
+  const int nkb = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK));
+
+  // statistics: the K sum (the order-defined mean) and the per-column max |v|
+  piper::MeanParams mp{};
+  mp.key = to_input(a->key);
+  mp.value = to_input(a->value);
+  mp.partials = static_cast<double*>(a->workspace);
+  mp.key_mean = o.key_mean;
+  mp.value_mean = nullptr;
+  mp.batch_heads = bh;
+  mp.heads = static_cast<int>(s.heads);
+  mp.length = static_cast<int>(s.key_length);
+  mp.chunks = static_cast<int>(ceil_div(s.key_length, PIPER_MEAN_CHUNK));
+  mp.tensors = 2;
+  mp.value_absmax = 1;
+  mp.value_scale = o.value_scale;
+
+  piper::SageQuantParams qp{};
+  qp.key = to_input(a->key);
+  qp.value = to_input(a->value);
+  qp.batch_heads = bh;
+  qp.heads = static_cast<int>(s.heads);
+  qp.key_length = static_cast<int>(s.key_length);
+  qp.nkb = nkb;
+  qp.k_blocks_wg = static_cast<int>(ceil_div(static_cast<int64_t>(bh) * nkb, 4));
+  qp.v_blocks_wg = qp.k_blocks_wg;
+  qp.key_mean = o.key_mean;
+  qp.value_scale = o.value_scale;
+  qp.key_scale = o.key_scale;
+  qp.kv_tiles = static_cast<uint8_t*>(o.kv_tiles);
+
+  const hipError_t err =
+      piper::launch_sage_prep(a->dtype == PIPER_BFLOAT16, static_cast<int>(s.head_dim), mp, qp, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "prep launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return PIPER_OK;
+}
+
+int piper_sage_attention_forward(const piper_sage_attention_args* a, void* stream) {
+  if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != PIPER_ABI_VERSION)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", a->abi_version,
+                PIPER_ABI_VERSION);
+  if (a->dtype != PIPER_FLOAT16 && a->dtype != PIPER_BFLOAT16)
+    return fail(PIPER_ERROR_UNSUPPORTED, "query dtype must be float16 or bfloat16");
+  if (a->output_dtype != PIPER_FLOAT16 && a->output_dtype != PIPER_BFLOAT16 && a->output_dtype != PIPER_FLOAT32)
+    return fail(PIPER_ERROR_UNSUPPORTED, "output dtype must be float16, bfloat16 or float32");
+  const piper_shape& s = a->shape;
+  if (int st = check_shape(&s)) return st;
+  if (a->is_causal && s.query_length != s.key_length)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
+  if (!(std::isfinite(a->scale) && a->scale > 0.0f))
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
+  if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
+  if (int st = check_input("query", a->query)) return st;
+  const piper_sage_prepared& o = a->prepared;
+  if (!o.value_scale || !o.kv_tiles || !a->output)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared input or the output pointer is NULL");
+  if (!aligned16(o.kv_tiles) || !aligned16(o.value_scale) || (reinterpret_cast<uintptr_t>(a->output) & 7u) != 0)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
+
+  const int waves = (a->plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
+  piper::SageParams sp{};
+  sp.kv_tiles = static_cast<const uint8_t*>(o.kv_tiles);
+  sp.value_scale = o.value_scale;
+  sp.output = a->output;
+  sp.query = to_input(a->query);
+  sp.query_bf16 = a->dtype == PIPER_BFLOAT16 ? 1 : 0;
+  sp.heads = static_cast<int>(s.heads);
+  sp.batch_heads = static_cast<int>(s.batch * s.heads);
+  sp.query_length = static_cast<int>(s.query_length);
+  sp.key_length = static_cast<int>(s.key_length);
+  sp.nkb = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK));
+  sp.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * waves));
+  sp.scale_log2e = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
+  sp.causal_forward = (a->plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
+  sp.xcd_remap = (a->plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
+  if (static_cast<int64_t>(sp.query_tiles) * sp.batch_heads > 0x7fffffff)
+    return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
+
+  const hipError_t err = piper::launch_sage_attention(static_cast<int>(s.head_dim), a->is_causal != 0,
+                                                      a->output_dtype, waves, sp, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "attention launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return PIPER_OK;
 }
 
 }  // extern "C"

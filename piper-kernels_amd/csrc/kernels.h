@@ -19,6 +19,14 @@ constexpr int kv_inv_offset(int head_dim) { return kv_log_offset(head_dim) + 256
 constexpr int kv_corr_offset(int head_dim) { return kv_inv_offset(head_dim) + 256; }
 constexpr int kv_tile_bytes(int head_dim) { return (kv_corr_offset(head_dim) + 4 * head_dim + 1023) / 1024 * 1024; }
 
+// SageAttention2++ tile record: the same K rows (and K scale in the padding of row 0),
+// then FP8 E4M3 V^T codes [D][64] in rows of 80 bytes; no softmax metadata (the V scale is
+// per channel and applied in the epilogue).  A whole number of KiB for D = 64 and 128.
+constexpr int sage_v_offset(int head_dim) { return 64 * kv_k_stride(head_dim); }
+constexpr int sage_tile_bytes(int head_dim) {
+  return (sage_v_offset(head_dim) + head_dim * kv_v_stride() + 1023) / 1024 * 1024;
+}
+
 struct InputTensor {
   const void* data;  // 16-bit floats; the head_dim axis is contiguous
   long stride_batch;  // element strides
@@ -37,6 +45,10 @@ struct MeanParams {
   int length;  // key length
   int chunks;  // ceil(length / 64)
   int tensors; // 1 = K only (causal), 2 = K and V
+  // 1: the V statistic is the per-column max of |v| (SageAttention2++), finalised into
+  // value_scale = amax / 2.25 + 1e-7; 0: the V sum, finalised into value_mean
+  int value_absmax;
+  float* value_scale;  // [batch_heads][D] (value_absmax only)
 };
 
 struct QuantParams {
@@ -90,7 +102,45 @@ struct AttnParams {
   InputTensor query;
 };
 
+// SageAttention2++: the prep quantises K (per 64-row block, after K smoothing) and V (FP8
+// per channel) into tile records; the attention kernel quantises each query block itself.
+struct SageQuantParams {
+  InputTensor key;
+  InputTensor value;
+  int batch_heads;
+  int heads;
+  int key_length;
+  int nkb;
+  int k_blocks_wg;  // workgroups (4 units each) per unit kind
+  int v_blocks_wg;
+  const float* key_mean;
+  const float* value_scale;
+  float* key_scale;
+  uint8_t* kv_tiles;  // [batch_heads][nkb][sage_tile_bytes(D)]
+};
+
+struct SageParams {
+  const uint8_t* kv_tiles;
+  const float* value_scale;  // [batch_heads][D]
+  void* output;
+  InputTensor query;
+  int query_bf16;
+  int heads;
+  int batch_heads;
+  int query_length;
+  int key_length;
+  int nkb;
+  int query_tiles;  // workgroup query tiles per (batch, head)
+  float scale_log2e;
+  int causal_forward;
+  int xcd_remap;
+};
+
 hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream);
+hipError_t launch_sage_prep(bool bf16, int head_dim, const MeanParams& mp, const SageQuantParams& qp,
+                            hipStream_t stream);
+hipError_t launch_sage_attention(int head_dim, bool causal, int out_dtype, int waves, const SageParams& sp,
+                                 hipStream_t stream);
 
 // out_dtype: 0 = fp16, 1 = bf16, 2 = fp32.  waves: 4 or 8 query waves per workgroup.
 hipError_t launch_attention(int head_dim, bool causal, int out_dtype, int waves, const AttnParams& ap,

@@ -1,4 +1,5 @@
-// Prep kernels: order-defined K/V sequence means, per-block INT8 Q/K and per-key INT8 V.
+// Prep kernels: order-defined K/V sequence means, per-block INT8 Q/K and per-key INT8 V
+// (Piper Attention); K means, per-channel V scales, INT8 K and FP8 V (SageAttention2++).
 //
 // Behaviour follows the reference's portable algorithm (jumbledpoophj/piper-kernels 0.2.1):
 //   K smoothing and per-block ("per_warp") Q/K codes  sage/reference.py:61-108
@@ -41,6 +42,8 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
   double acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0;
+  // the V statistic of SageAttention2++ is max |v| (exact in any order); otherwise a sum
+  const bool absmax = tensor == 1 && p.value_absmax;
   int row = row0;
   for (; row + 8 <= row1; row += 8) {  // 8 loads in flight, adds still in row order
     uint4 raw[8];
@@ -52,7 +55,8 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
       float f[8];
       widen8<kBf16>(raw[u], f);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += static_cast<double>(f[i]);
+      for (int i = 0; i < 8; ++i)
+        acc[i] = absmax ? fmax(acc[i], static_cast<double>(fabsf(f[i]))) : acc[i] + static_cast<double>(f[i]);
     }
   }
   for (; row < row1; ++row) {
@@ -60,7 +64,8 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
     float f[8];
     widen8<kBf16>(raw, f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += static_cast<double>(f[i]);
+    for (int i = 0; i < 8; ++i)
+      acc[i] = absmax ? fmax(acc[i], static_cast<double>(fabsf(f[i]))) : acc[i] + static_cast<double>(f[i]);
   }
   double* out = p.partials + ((static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks + chunk) * D +
                 group * 8;
@@ -70,6 +75,8 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
 
 // Means, pass 2: sum the chunk partials of one (tensor, batch-head, column) in chunk order,
 // divide by the length in FP64 and round to FP32.  Causal calls write a zero V mean.
+// SageAttention2++ (value_absmax): the V column's max |v| over the chunks gives its FP8 scale
+// amax / 2.25 + 1e-7 (sage_attention_2pp/reference.py:22-23: FP32 division, FP32 add).
 __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, int head_dim) {
   const int gid = blockIdx.x * 64 + threadIdx.x;
   const int per_tensor = p.batch_heads * head_dim;
@@ -84,6 +91,12 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
   const int bh = rem / head_dim;
   const int d = rem - bh * head_dim;
   const double* src = p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks * head_dim + d;
+  if (tensor == 1 && p.value_absmax) {
+    double amax = 0.0;
+    for (int c = 0; c < p.chunks; ++c) amax = fmax(amax, src[static_cast<long>(c) * head_dim]);
+    p.value_scale[rem] = __fadd_rn(static_cast<float>(amax) / 2.25f, 1e-7f);
+    return;
+  }
   // 16 loads in flight per step; the additions stay in chunk order
   constexpr int kBatch = 16;
   double total = 0.0;
@@ -272,6 +285,83 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// SageAttention2++ quantisation (sage_attention_2pp/reference.py:22-25, 44-49).  Each wave
+// owns a 64-row K block (the Piper K path, into the SageAttention2++ tile record) or a
+// 64-key V tile: FP8 E4M3 codes of v / scale[channel] (the correctly rounded FP32 quotient,
+// then v_cvt_pk_fp8_f32: round to nearest even, bit-identical to torch's float8_e4m3fn
+// cast), transposed through LDS into the record's V^T rows.  Keys past the end get code 0.
+// ---------------------------------------------------------------------------------------
+template <bool kBf16, int D>
+__global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParams p) {
+  constexpr int kVStride = kKeyBlock + 16;  // LDS row stride of a V^T tile (bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[4][D * kVStride];
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int block = blockIdx.x;
+
+  if (block < p.k_blocks_wg) {
+    const int unit = block * 4 + wave;
+    if (unit >= p.batch_heads * p.nkb) return;
+    const int bh = unit / p.nkb;
+    const int kb = unit - bh * p.nkb;
+    const int b = bh / p.heads;
+    const int h = bh - b * p.heads;
+    int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * sage_tile_bytes(D);
+    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D)>(p.key, b, h, kb * kKeyBlock, p.key_length,
+                                              p.key_mean + static_cast<long>(bh) * D, tile, p.key_scale + unit);
+    return;
+  }
+
+  const int unit = (block - p.k_blocks_wg) * 4 + wave;
+  const bool active = unit < p.batch_heads * p.nkb;
+  uint8_t* lds = vt_lds[wave];
+  if (active) {
+    const int bh = unit / p.nkb;
+    const int kb = unit - bh * p.nkb;
+    const int b = bh / p.heads;
+    const int h = bh - b * p.heads;
+    constexpr int kGroups = D / 8;
+    constexpr int kRowsPerIter = kWave / kGroups;
+    constexpr int kIters = kKeyBlock / kRowsPerIter;
+    const int group = lane % kGroups;
+    const int sub = lane / kGroups;
+    const uint16_t* base = static_cast<const uint16_t*>(p.value.data) + b * p.value.stride_batch +
+                           h * p.value.stride_head + group * 8;
+    Divisor divisor[8];  // this lane's 8 channels
+#pragma unroll
+    for (int i = 0; i < 8; ++i) divisor[i] = Divisor(p.value_scale[static_cast<long>(bh) * D + group * 8 + i]);
+#pragma unroll 4
+    for (int it = 0; it < kIters; ++it) {
+      const int key_in_tile = it * kRowsPerIter + sub;
+      const int row = kb * kKeyBlock + key_in_tile;
+      const bool valid = row < p.key_length;
+      const uint4 raw = valid ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
+                              : make_uint4(0, 0, 0, 0);
+      float f[8];
+      widen8<kBf16>(raw, f);
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(
+            divisor[i].quotient(f[i]), divisor[i + 1].quotient(f[i + 1]), 0, false));
+        lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<uint8_t>(w);
+        lds[(group * 8 + i + 1) * kVStride + key_in_tile] = static_cast<uint8_t>(w >> 8);
+      }
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  // transposed rows: lane owns features d = lane, lane + 64, ...
+  uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * sage_tile_bytes(D);
+  for (int d = lane; d < D; d += kWave) {
+    const uint4* src = reinterpret_cast<const uint4*>(lds + d * kVStride);
+    uint4* dst = reinterpret_cast<uint4*>(tile + sage_v_offset(D) + d * kv_v_stride());
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[j] = src[j];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------------------
 template <bool kBf16, int D>
@@ -288,6 +378,32 @@ static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp,
   const int blocks = qp.q_blocks_wg + qp.k_blocks_wg + qp.v_blocks_wg;
   hipLaunchKernelGGL((quantize_kernel<kBf16, D>), dim3(blocks), dim3(256), 0, stream, qp);
   return hipGetLastError();
+}
+
+template <bool kBf16, int D>
+static hipError_t launch_sage_prep_typed(const MeanParams& mp, const SageQuantParams& qp, hipStream_t stream) {
+  const long stat_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 8) * mp.tensors;
+  hipLaunchKernelGGL((mean_partial_kernel<kBf16, D>), dim3(static_cast<unsigned>((stat_threads + 255) / 256)),
+                     dim3(256), 0, stream, mp);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int fin_threads = 2 * mp.batch_heads * D;
+  hipLaunchKernelGGL(mean_finalize_kernel, dim3((fin_threads + 63) / 64), dim3(64), 0, stream, mp, D);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((sage_quantize_kernel<kBf16, D>), dim3(qp.k_blocks_wg + qp.v_blocks_wg), dim3(256), 0, stream,
+                     qp);
+  return hipGetLastError();
+}
+
+hipError_t launch_sage_prep(bool bf16, int head_dim, const MeanParams& mp, const SageQuantParams& qp,
+                            hipStream_t stream) {
+  if (bf16) {
+    return head_dim == 128 ? launch_sage_prep_typed<true, 128>(mp, qp, stream)
+                           : launch_sage_prep_typed<true, 64>(mp, qp, stream);
+  }
+  return head_dim == 128 ? launch_sage_prep_typed<false, 128>(mp, qp, stream)
+                         : launch_sage_prep_typed<false, 64>(mp, qp, stream);
 }
 
 hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {

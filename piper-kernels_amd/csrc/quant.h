@@ -46,6 +46,7 @@ __device__ __forceinline__ float scale_from_amax(float amax) {
 struct Divisor {
   float s;  // the scale, or 0 for an infinite scale (see quotient)
   float y;  // RN(1 / scale), IEEE division
+  Divisor() = default;
   __device__ explicit Divisor(float scale) : s(__builtin_isinf(scale) ? 0.0f : scale), y(1.0f / scale) {}
   // RN(x / scale) without a per-element division (Markstein: with y = RN(1/s) and a faithful
   // q0 = RN(x y), the remainder x - s q0 is exact in one FMA and RN(q0 + r y) = RN(x / s) for

@@ -1,0 +1,278 @@
+// Fused SageAttention2++ forward for gfx950: INT8 MFMA QK^T, FP32 online softmax whose frame
+// is shifted by log2(448), FP8 E4M3 probabilities times FP8 E4M3 V on
+// v_mfma_f32_32x32x64_f8f6f4, accumulated in FP32 across all key blocks.
+//
+// Behaviour follows the reference recurrence (jumbledpoophj/piper-kernels 0.2.1,
+// src/piper_kernels/attention/sage_attention_2pp/reference.py:58-104; the GPU kernel it
+// models is sage_attention_2pp/triton.py:391-510): per 64-key block, bm = max(s) - log2 448,
+// m' = max(m, bm), acc = acc * exp2(m - m') + fp8(exp2(s - m')) @ v8, den = den * exp2(m - m')
+// + sum(exp2(s - m')), and the epilogue acc * scale_v / max(den, 1e-30).  Scores are in the
+// log2 domain (the softmax scale carries log2 e).
+//
+// The one arithmetic difference from the reference: its 64-key partial products are rounded
+// to FP16 (a model of NVIDIA's FP16-accumulating FP8 MMA, reference.py:95-98).  gfx950's FP8
+// MFMA accumulates in FP32, so the products of every block accumulate in the MFMA's own FP32
+// registers, rescaled only when the running maximum moves, and the per-channel V scale is
+// applied once at the end.  This removes all per-block VALU work on the D outputs (the
+// reference applies a scale per block): per block and lane, the VALU work is the 32 scores'
+// subtraction, max, FMA, exp2, sum and FP8 packing.
+//
+// Design shared with the Piper Attention kernel (stream.h): one workgroup = NW waves x 32
+// queries of one head; S^T = K Q^T with K rows loaded in a permuted order, so each lane owns
+// one query and keys {16h .. 16h+15} and {32+16h .. 32+16h+15} of every block -- which, packed
+// in that order, is directly the B operand of the FP8 MFMA (which contracts over any key order
+// the A operand shares: V^T rows are read at bytes [16h, +16) and [32 + 16h, +16)); the query
+// is quantised in the prologue; tile records are copied straight into a 6-stage LDS ring.
+#include "common.h"
+#include "kernels.h"
+#include "quant.h"
+#include "stream.h"
+
+namespace piper {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2Of448 = 8.807354922057604f;  // log2(448): probabilities are born in [0, 448]
+
+template <int D, int NW>
+struct SageLayout : StagePieces<sage_tile_bytes(D), NW> {  // the tile record is the stage image
+  static constexpr int kKStride = kv_k_stride(D);   // bytes per K row in LDS
+  static constexpr int kVStride = kv_v_stride();    // bytes per V^T row in LDS
+  static constexpr int kVOffset = sage_v_offset(D);
+};
+
+__device__ __forceinline__ uint32_t pack_fp8(float a, float b, float c, float d) {
+  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
+}
+
+// Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave.
+// ct = query scale * key scale * softmax scale * log2 e; mrun is the running maximum (log2
+// units, per query), den this lane half's share of the denominator.
+template <int D, int NW, bool kCausal>
+__device__ __forceinline__ void sage_block_update(const char* stage, const v16i (&s)[2], float ct, int t, int q0,
+                                                  int n, int h, int key_length, v16f (&acc)[D / 32], float& den,
+                                                  float& mrun) {
+  using L = SageLayout<D, NW>;
+  constexpr int kChunksD = D / 32;
+
+  // ---- raw scores (exact integers as FP32) and their block maximum ----
+  float x[32];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    x[r] = unbias(s[0][r]);
+    x[16 + r] = unbias(s[1][r]);
+  }
+  if (t * kKeyBlock + kKeyBlock > key_length) {  // the last tile: its padding keys score -inf
+    const int key_base = t * kKeyBlock + 16 * h;
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int key = key_base + (r < 16 ? r : 16 + r);
+      if (key >= key_length) x[r] = -__builtin_inff();
+    }
+  }
+  if constexpr (kCausal) {
+    if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // block crosses this wave's diagonal
+      const int query = q0 + n;
+      const int key_base = t * kKeyBlock + 16 * h;
+#pragma unroll
+      for (int r = 0; r < 32; ++r) {
+        const int key = key_base + (r < 16 ? r : 16 + r);
+        if (key > query) x[r] = -__builtin_inff();
+      }
+    }
+  }
+  // ct > 0, so the maximum commutes with the scaling: max(RN(x ct)) = RN(max(x) ct)
+  const float raw_max = cross_half_max(max32(x));
+  const float block_max = raw_max * ct - kLog2Of448;
+  const float next = fmaxf(mrun, block_max);
+
+  // ---- move the frame when the running maximum grows (exact: otherwise the weight is 1) ----
+  const bool grow = next > mrun;
+  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    const float w = grow ? __builtin_amdgcn_exp2f(mrun - next) : 1.0f;  // exp2(-inf) = 0 at the start
+#pragma unroll
+    for (int j = 0; j < kChunksD; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][r] *= w;
+    den *= w;
+    mrun = next;
+  }
+
+  // ---- p = exp2(s ct - m') in [0, 448], the denominator share and the FP8 codes ----
+  float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  uint32_t pw[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float e0 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 0], ct, -mrun));
+    const float e1 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 1], ct, -mrun));
+    const float e2 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 2], ct, -mrun));
+    const float e3 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 3], ct, -mrun));
+    ps[0] += e0;
+    ps[1] += e1;
+    ps[2] += e2;
+    ps[3] += e3;
+    pw[q] = pack_fp8(e0, e1, e2, e3);
+  }
+  den += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+  const v8i p = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]), static_cast<int>(pw[3]),
+                 static_cast<int>(pw[4]), static_cast<int>(pw[5]), static_cast<int>(pw[6]), static_cast<int>(pw[7])};
+
+  // ---- O^T += V^T P^T on the FP8 MFMA, accumulating in FP32 ----
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j) {
+    const char* vrow = stage + L::kVOffset + (32 * j + n) * L::kVStride + 16 * h;
+    const v4i a0 = *reinterpret_cast<const v4i*>(vrow);
+    const v4i a1 = *reinterpret_cast<const v4i*>(vrow + 32);
+    const v8i a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, p, acc[j], 0, 0, 0, 0, 0, 0);
+  }
+}
+
+// The LDS ring of the Piper Attention kernel: kStages tile records, block t + kLead copied at
+// iteration t, one workgroup barrier per two iterations (see attention.hip's pipeline_step
+// for the argument that every stage is published before it is read and read before it is
+// overwritten).
+constexpr int kSageStages = 6;
+constexpr int kSageLead = 4;
+
+template <int D, int NW, bool kCausal, bool kBarrier>
+__device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
+                                          int wave, int lane, const v4i (&qf)[D / 32], float cq, int q0, int n,
+                                          int h, int krow, const v16i& bias, const v16i (&s_cur)[2],
+                                          v16i (&s_next)[2], v16f (&acc)[D / 32], float& den, float& mrun) {
+  using L = SageLayout<D, NW>;
+  copy_block<L>(p, smem + ((t + kSageLead) % kSageStages) * L::kStageBytes, bh, min(t + kSageLead, tiles - 1), wave,
+                lane);
+  if (t < wave_tiles) {
+    block_scores<D, L>(smem + ((t + 1) % kSageStages) * L::kStageBytes, qf, h, krow, bias, s_next);
+    const char* stage = smem + (t % kSageStages) * L::kStageBytes;
+    const float key_scale = *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
+    sage_block_update<D, NW, kCausal>(stage, s_cur, cq * key_scale, t, q0, n, h, p.key_length, acc, den, mrun);
+  }
+  if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
+}
+
+template <int D, int NW, bool kCausal, int kOut>
+__global__ void __launch_bounds__(NW * 64, 1) sage_attention_kernel(const SageParams p) {
+  using L = SageLayout<D, NW>;
+  constexpr int kChunksD = D / 32;
+  __shared__ __attribute__((aligned(16))) char smem[kSageStages * L::kStageBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5;
+  const int n = lane & 31;
+  const int logical = p.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
+  const int bh = __builtin_amdgcn_readfirstlane(logical / p.query_tiles);
+  const int qtile_fwd = __builtin_amdgcn_readfirstlane(logical - bh * p.query_tiles);
+  const int qtile = kCausal && !p.causal_forward ? p.query_tiles - 1 - qtile_fwd : qtile_fwd;
+  const int q0 = qtile * (NW * 32) + wave * 32;
+  const bool wave_live = q0 < p.query_length;
+
+  int tiles = p.nkb;
+  int wave_tiles = wave_live ? p.nkb : 0;
+  if constexpr (kCausal) {
+    const int last_query = min(p.query_length, (qtile + 1) * NW * 32) - 1;
+    tiles = last_query / kKeyBlock + 1;
+    wave_tiles = wave_live ? (min(p.query_length, q0 + 32) - 1) / kKeyBlock + 1 : 0;
+  }
+
+  // query loads first (untracked), then the prologue copies, then a wait for the query only
+  v4i raw[D / 16];
+  if (wave_live) issue_query_loads<D>(p, bh, q0, n, h, raw);
+#pragma unroll
+  for (int b = 0; b < kSageLead; ++b) copy_block<L>(p, smem + b * L::kStageBytes, bh, min(b, tiles - 1), wave, lane);
+  v4i qf[kChunksD];
+  float cq = 0.0f;
+  if (wave_live) {
+    if (wave < L::kFullWaves)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kSageLead * L::kRounds) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kSageLead * (L::kRounds - 1)) : "memory");
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
+    cq = quantize_query_block<D>(p, q0, n, raw, qf) * p.scale_log2e;
+  } else {
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
+  }
+
+  v16f acc[kChunksD];
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  float den = 0.0f;
+  float mrun = -__builtin_inff();
+  const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+
+  stage_barrier<0>();  // all prologue copies landed
+
+  v16i bias = {kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias,
+               kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias};
+  asm volatile("" : "+v"(bias));
+  v16i s_a[2], s_b[2];
+  if (wave_tiles > 0) block_scores<D, L>(smem, qf, h, krow, bias, s_a);
+
+  int t = 0;
+  for (; t + 1 < tiles; t += 2) {
+    sage_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
+                                     s_a, s_b, acc, den, mrun);
+    sage_step<D, NW, kCausal, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
+                                    s_b, s_a, acc, den, mrun);
+  }
+  if (t < tiles)
+    sage_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
+                                     s_a, s_b, acc, den, mrun);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may outlive the waves
+
+  // ---- epilogue: acc * scale_v / max(den, 1e-30); lane (n, h) holds rows d = 32j + 8g + 4h + i ----
+  const float total = cross_half_sum(den);
+  const int query = q0 + n;
+  if (!wave_live || query >= p.query_length) return;
+  const float rden = 1.0f / fmaxf(total, 1e-30f);
+  const float* vscale = p.value_scale + static_cast<long>(bh) * D;
+  const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * j + 8 * g + 4 * h;
+      const float4 vs = *reinterpret_cast<const float4*>(vscale + d0);
+      store4<kOut>(p.output, out_row + d0, (acc[j][4 * g + 0] * vs.x) * rden, (acc[j][4 * g + 1] * vs.y) * rden,
+                   (acc[j][4 * g + 2] * vs.z) * rden, (acc[j][4 * g + 3] * vs.w) * rden);
+    }
+  }
+}
+
+template <int D, int NW, bool kCausal>
+static hipError_t sage_launch_out(int out_dtype, const SageParams& sp, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(sp.query_tiles * sp.batch_heads));
+  const dim3 block(NW * 64);
+  switch (out_dtype) {
+    case 0: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 0>), grid, block, 0, stream, sp); break;
+    case 1: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 1>), grid, block, 0, stream, sp); break;
+    default: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 2>), grid, block, 0, stream, sp); break;
+  }
+  return hipGetLastError();
+}
+
+template <int D, int NW>
+static hipError_t sage_launch_causal(bool causal, int out_dtype, const SageParams& sp, hipStream_t stream) {
+  return causal ? sage_launch_out<D, NW, true>(out_dtype, sp, stream)
+                : sage_launch_out<D, NW, false>(out_dtype, sp, stream);
+}
+
+hipError_t launch_sage_attention(int head_dim, bool causal, int out_dtype, int waves, const SageParams& sp,
+                                 hipStream_t stream) {
+  if (head_dim == 128) {
+    return waves == 4 ? sage_launch_causal<128, 4>(causal, out_dtype, sp, stream)
+                      : sage_launch_causal<128, 8>(causal, out_dtype, sp, stream);
+  }
+  return waves == 4 ? sage_launch_causal<64, 4>(causal, out_dtype, sp, stream)
+                    : sage_launch_causal<64, 8>(causal, out_dtype, sp, stream);
+}
+
+}  // namespace piper

@@ -1,0 +1,204 @@
+// Streaming machinery shared by the gfx950 attention kernels (Piper Attention and
+// SageAttention2++): tile records copied straight from HBM into a ring of LDS stages, the
+// workgroup barriers that keep those copies in flight, the in-prologue query quantisation,
+// the INT8 score MFMAs and the output stores.
+//
+// A tile layout type L provides kWaves (waves per workgroup), kKStride (bytes per K row in a
+// stage), kStageBytes (one tile record = one stage, a KiB multiple), kPieces (1 KiB pieces per
+// stage), kRounds (pieces per wave, rounded up) and kFullWaves (waves that copy kRounds
+// pieces).  Parameter structs provide kv_tiles and nkb (tile records of a batch-head), and
+// for the query quantisation query, heads, query_length and query_bf16.
+#pragma once
+
+#include "common.h"
+#include "quant.h"
+
+namespace piper {
+
+// Pieces of a stage of kStageBytes copied by NW waves.
+template <int kStageBytes_, int NW>
+struct StagePieces {
+  static constexpr int kWaves = NW;
+  static constexpr int kStageBytes = kStageBytes_;
+  static constexpr int kPieces = kStageBytes / 1024;  // 1 KiB per wave-wide 16-byte load
+  static constexpr int kRounds = (kPieces + NW - 1) / NW;
+  static constexpr int kFullWaves = kPieces % NW == 0 ? NW : kPieces % NW;  // waves with kRounds pieces
+  static_assert(kStageBytes % 1024 == 0, "a stage is a whole number of KiB");
+};
+
+// One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from its global address to
+// LDS byte lds + 16 * i.  Issued as inline assembly so that the compiler's wait insertion does
+// not treat every later LDS read as dependent on it: the waits are explicit (stage_barrier,
+// and a drain before the waves end).
+__device__ __forceinline__ void copy_piece(const void* src, uint32_t lds) {
+  // s_nop: one wait state between the SALU write of M0 and the LDS DMA that reads it
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// Direct global -> LDS copy of the tile record of block t into one LDS stage: wave w copies
+// 1 KiB pieces w, w + NW, ... (each lane 16 bytes), so the per-lane addresses are loop
+// invariant and no VGPRs hold staged data.  Completion is tracked by this wave's vmcnt.
+template <class L, class Params>
+__device__ __forceinline__ void copy_block(const Params& p, char* stage, int bh, int t, int wave, int lane) {
+  constexpr int NW = L::kWaves;
+  const char* tile = reinterpret_cast<const char*>(p.kv_tiles) + (static_cast<long>(bh) * p.nkb + t) * L::kStageBytes;
+  const uint32_t base = lds_address(stage);
+#pragma unroll
+  for (int r = 0; r < L::kRounds; ++r) {
+    const int piece = wave + r * NW;  // wave-uniform: a scalar branch
+    if (piece < L::kPieces) copy_piece(tile + piece * 1024 + lane * 16, base + piece * 1024);
+  }
+}
+
+// Workgroup barrier that lets this wave's newest kInFlight direct loads stay in flight.
+// (__syncthreads would drain every outstanding load.)  LDS reads are waited for as well, so
+// a stage is never overwritten under a pending read.
+template <int kInFlight>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kInFlight) : "memory");
+}
+
+template <class L>
+__device__ __forceinline__ void stage_barrier_keep_last(int wave) {
+  if (wave < L::kFullWaves)
+    stage_barrier<L::kRounds>();
+  else
+    stage_barrier<L::kRounds - 1>();
+}
+
+// Balanced max over 32 values (depth 4 instead of a 16-long v_max3 chain).
+__device__ __forceinline__ float max32(const float (&x)[32]) {
+  float t[11];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) t[i] = fmaxf(fmaxf(x[3 * i], x[3 * i + 1]), x[3 * i + 2]);
+  t[10] = fmaxf(x[30], x[31]);
+  const float u0 = fmaxf(fmaxf(t[0], t[1]), t[2]);
+  const float u1 = fmaxf(fmaxf(t[3], t[4]), t[5]);
+  const float u2 = fmaxf(fmaxf(t[6], t[7]), t[8]);
+  const float u3 = fmaxf(t[9], t[10]);
+  return fmaxf(fmaxf(u0, u1), fmaxf(u2, u3));
+}
+
+// Keep x as a materialised FP32 value: narrowing must round the FP32 result (as the
+// reference casts its FP32 output), not a fused multiply-add to f16 (v_fma_mix).
+__device__ __forceinline__ float materialize(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+template <int kOut>
+__device__ __forceinline__ void store4(void* out, long index, float a, float b, float c, float d) {
+  if constexpr (kOut != 2) {
+    a = materialize(a);
+    b = materialize(b);
+    c = materialize(c);
+    d = materialize(d);
+  }
+  if constexpr (kOut == 2) {
+    *reinterpret_cast<float4*>(static_cast<float*>(out) + index) = make_float4(a, b, c, d);
+  } else if constexpr (kOut == 1) {
+    const uint2 v = make_uint2(float_to_bf16_bits(a) | (float_to_bf16_bits(b) << 16),
+                               float_to_bf16_bits(c) | (float_to_bf16_bits(d) << 16));
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + index) = v;
+  } else {
+    const uint2 v = make_uint2(float_to_half_bits(a) | (float_to_half_bits(b) << 16),
+                               float_to_half_bits(c) | (float_to_half_bits(d) << 16));
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + index) = v;
+  }
+}
+
+// Value of an integer accumulator that started from kAccBias: one exact FP32 subtraction.
+// (The element arrives as a scalar: this clang's __builtin_bit_cast of an ext_vector
+// subscript reads element 0.)
+__device__ __forceinline__ float unbias(int bits) { return __builtin_bit_cast(float, bits) - kAccBiasValue; }
+
+// A 16-byte global load the compiler does not track: the caller waits for it with an explicit
+// s_waitcnt, which lets later direct LDS copies stay in flight.  (A tracked load would get a
+// compiler wait that also drains every copy issued after it: vmcnt completes in order.)
+__device__ __forceinline__ v4i load_untracked(const void* src) {
+  v4i r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=&v"(r) : "v"(src) : "memory");
+  return r;
+}
+
+// Fused query quantisation, part 1: lane (n, h) issues the loads of elements [32c + 16h, +16)
+// of query row q0 + n (row q0 for rows past the end: their values are replaced by zeros).
+template <int D, class Params>
+__device__ __forceinline__ void issue_query_loads(const Params& p, int bh, int q0, int n, int h,
+                                                  v4i (&raw)[D / 16]) {
+  const int b = bh / p.heads;
+  const int head = bh - b * p.heads;
+  const int row = min(q0 + n, p.query_length - 1);
+  const uint16_t* src = static_cast<const uint16_t*>(p.query.data) + b * p.query.stride_batch +
+                        head * p.query.stride_head + static_cast<long>(row) * p.query.stride_seq + 16 * h;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+    raw[2 * c] = load_untracked(src + 32 * c);
+    raw[2 * c + 1] = load_untracked(src + 32 * c + 8);
+  }
+}
+
+// Part 2, after the wait: the wave's 32-row query block quantised in registers exactly as the
+// prep kernel does it (sage/reference.py:61-77: one scale amax / 127 + 1e-7 over the
+// zero-padded 32 x D block, codes round-half-even(x / scale) clamped to +-127).  The block amax
+// is a wave-wide max; the 16 codes of each chunk are packed in element order, the layout of
+// the prepared code rows.  Returns the scale.
+template <int D, class Params>
+__device__ __forceinline__ float quantize_query_block(const Params& p, int q0, int n, const v4i (&raw)[D / 16],
+                                                     v4i (&qf)[D / 32]) {
+  constexpr int kChunksD = D / 32;
+  const bool valid = q0 + n < p.query_length;
+  float f[2 * kChunksD][8];
+#pragma unroll
+  for (int i = 0; i < 2 * kChunksD; ++i) {
+    const uint4 bits = valid ? make_uint4(raw[i].x, raw[i].y, raw[i].z, raw[i].w) : make_uint4(0, 0, 0, 0);
+    if (p.query_bf16) widen8<true>(bits, f[i]);
+    else widen8<false>(bits, f[i]);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2 * kChunksD; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[i][e]));
+  amax = wave_max(amax);
+  const float scale = scale_from_amax(amax);
+  const Divisor divisor(scale);
+#pragma unroll
+  for (int c = 0; c < kChunksD; ++c) {
+    uint32_t w[4];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t code[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) code[e] = code_word(f[2 * c + half][e], divisor);
+      w[2 * half] = pack_low_bytes(code[0], code[1], code[2], code[3]);
+      w[2 * half + 1] = pack_low_bytes(code[4], code[5], code[6], code[7]);
+    }
+    qf[c] = v4i{static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]), static_cast<int>(w[3])};
+  }
+  return scale;
+}
+
+// Integer scores S^T = K Q^T of one 64-key block: s[0] keys 0..31, s[1] keys 32..63 (each
+// lane: its query column, keys 16h + r after the K-row permutation).
+template <int D, class L>
+__device__ __forceinline__ void block_scores(const char* stage, const v4i (&qf)[D / 32], int h, int krow,
+                                             const v16i& bias, v16i (&s)[2]) {
+  // accumulators start from the bias: |K Q^T| <= D * 128 * 128 < 2^22, so each result reads as
+  // FP32 1.5 * 2^23 + score exactly
+  s[0] = s[1] = bias;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+    const char* kb = stage + 32 * c + 16 * h;
+    const v4i a0 = *reinterpret_cast<const v4i*>(kb + krow * L::kKStride);
+    const v4i a1 = *reinterpret_cast<const v4i*>(kb + (32 + krow) * L::kKStride);
+    s[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qf[c], s[0], 0, 0, 0);
+    s[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qf[c], s[1], 0, 0, 0);
+  }
+}
+
+}  // namespace piper

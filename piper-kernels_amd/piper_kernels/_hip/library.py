@@ -31,6 +31,9 @@ EXPORTED_SYMBOLS = (
     "piper_prepare",
     "piper_attention_forward",
     "piper_attention_forward_fused",
+    "piper_sage_prepared_layout",
+    "piper_sage_prepare",
+    "piper_sage_attention_forward",
     "piper_last_error",
 )
 
@@ -145,6 +148,55 @@ class PiperAttentionFusedArgs(ctypes.Structure):
     ]
 
 
+def sage_tile_bytes(head_dim: int) -> int:
+    """Bytes of one SageAttention2++ tile record (PIPER_SAGE_TILE_BYTES): K rows, FP8 V^T rows."""
+    return (64 * kv_k_stride(head_dim) + head_dim * KV_V_STRIDE + 1023) // 1024 * 1024
+
+
+class PiperSagePrepared(ctypes.Structure):
+    _fields_ = [("key_scale", _ptr), ("key_mean", _ptr), ("value_scale", _ptr), ("kv_tiles", _ptr)]
+
+
+class PiperSageLayout(ctypes.Structure):
+    _fields_ = [
+        ("key_scale_bytes", _i64),
+        ("mean_bytes", _i64),
+        ("kv_tile_bytes", _i64),
+        ("kv_tiles_bytes", _i64),
+        ("workspace_bytes", _i64),
+    ]
+
+
+class PiperSagePrepareArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("dtype", _i32),
+        ("reserved0", _i32),
+        ("reserved1", _i32),
+        ("shape", PiperShape),
+        ("key", PiperTensor),
+        ("value", PiperTensor),
+        ("prepared", PiperSagePrepared),
+        ("workspace", _ptr),
+        ("workspace_bytes", _i64),
+    ]
+
+
+class PiperSageAttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("dtype", _i32),
+        ("output_dtype", _i32),
+        ("is_causal", _i32),
+        ("plan", _i32),
+        ("scale", ctypes.c_float),
+        ("shape", PiperShape),
+        ("query", PiperTensor),
+        ("prepared", PiperSagePrepared),
+        ("output", _ptr),
+    ]
+
+
 class LibraryUnavailableError(RuntimeError):
     """The gfx950 HIP library is not built or cannot be opened."""
 
@@ -168,6 +220,12 @@ class NativeLibrary:
         lib.piper_attention_forward.restype = ctypes.c_int
         lib.piper_attention_forward_fused.argtypes = [ctypes.POINTER(PiperAttentionFusedArgs), _ptr]
         lib.piper_attention_forward_fused.restype = ctypes.c_int
+        lib.piper_sage_prepared_layout.argtypes = [ctypes.POINTER(PiperShape), ctypes.POINTER(PiperSageLayout)]
+        lib.piper_sage_prepared_layout.restype = ctypes.c_int
+        lib.piper_sage_prepare.argtypes = [ctypes.POINTER(PiperSagePrepareArgs), _ptr]
+        lib.piper_sage_prepare.restype = ctypes.c_int
+        lib.piper_sage_attention_forward.argtypes = [ctypes.POINTER(PiperSageAttentionArgs), _ptr]
+        lib.piper_sage_attention_forward.restype = ctypes.c_int
         version = lib.piper_abi_version()
         if version != ABI_VERSION:
             raise LibraryUnavailableError(
@@ -201,6 +259,21 @@ class NativeLibrary:
     def attention_forward_fused(self, args: PiperAttentionFusedArgs, stream: int) -> None:
         self._check(
             self._lib.piper_attention_forward_fused(ctypes.byref(args), _ptr(stream)), "piper_attention_forward_fused"
+        )
+
+    def sage_prepared_layout(self, shape: PiperShape) -> PiperSageLayout:
+        layout = PiperSageLayout()
+        self._check(
+            self._lib.piper_sage_prepared_layout(ctypes.byref(shape), ctypes.byref(layout)), "piper_sage_prepared_layout"
+        )
+        return layout
+
+    def sage_prepare(self, args: PiperSagePrepareArgs, stream: int) -> None:
+        self._check(self._lib.piper_sage_prepare(ctypes.byref(args), _ptr(stream)), "piper_sage_prepare")
+
+    def sage_attention_forward(self, args: PiperSageAttentionArgs, stream: int) -> None:
+        self._check(
+            self._lib.piper_sage_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_sage_attention_forward"
         )
 
 

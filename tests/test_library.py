@@ -47,6 +47,10 @@ def test_ctypes_structures_match_the_c_header(tmp_path) -> None:
         "piper_prepare_args": native.PiperPrepareArgs,
         "piper_attention_args": native.PiperAttentionArgs,
         "piper_attention_fused_args": native.PiperAttentionFusedArgs,
+        "piper_sage_prepared": native.PiperSagePrepared,
+        "piper_sage_layout": native.PiperSageLayout,
+        "piper_sage_prepare_args": native.PiperSagePrepareArgs,
+        "piper_sage_attention_args": native.PiperSageAttentionArgs,
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "piper_mi355x.h"', "int main(void) {"]
     for cname, cls in structs.items():
@@ -191,3 +195,65 @@ def test_fused_attention_validates_before_launching(lib) -> None:
     args.plan, args.abi_version = 0, 2
     with pytest.raises(RuntimeError, match="ABI version mismatch"):
         lib.attention_forward_fused(args, 0)
+
+
+@pytest.mark.parametrize("shape", [(1, 24, 16384, 16384, 128), (2, 3, 35, 67, 64), (1, 1, 1, 1, 64)])
+def test_sage_prepared_layout_sizes(lib, shape) -> None:
+    b, h, sq, sk, d = shape
+    layout = lib.sage_prepared_layout(native.PiperShape(*shape))
+    nkb = -(-sk // 64)
+    # K rows of D + 16 bytes, FP8 V^T rows of 80 bytes: 19 KiB (D = 128) and 10 KiB (D = 64)
+    assert layout.kv_tile_bytes == native.sage_tile_bytes(d) == {128: 19 * 1024, 64: 10 * 1024}[d]
+    assert layout.kv_tiles_bytes == b * h * nkb * layout.kv_tile_bytes
+    assert layout.key_scale_bytes == b * h * nkb * 4
+    assert layout.mean_bytes == b * h * d * 4
+    assert layout.workspace_bytes == 2 * b * h * (-(-sk // 64)) * d * 8
+
+
+def test_sage_prepare_validates_before_launching(lib) -> None:
+    fake = 0x1000
+    args = native.PiperSagePrepareArgs(abi_version=native.ABI_VERSION, dtype=native.FLOAT32,
+                                       shape=native.PiperShape(1, 1, 8, 8, 64))
+    with pytest.raises(RuntimeError, match="float16 or bfloat16"):
+        lib.sage_prepare(args, 0)
+    args.dtype = native.FLOAT16
+    with pytest.raises(RuntimeError, match="key pointer is NULL"):
+        lib.sage_prepare(args, 0)
+    args.key = native.PiperTensor(fake, 512, 512, 64)
+    args.value = native.PiperTensor(fake + 8, 512, 512, 64)
+    with pytest.raises(RuntimeError, match="value must be 16-byte aligned"):
+        lib.sage_prepare(args, 0)
+    args.value = native.PiperTensor(fake, 512, 512, 64)
+    with pytest.raises(RuntimeError, match="prepared output pointer is NULL"):
+        lib.sage_prepare(args, 0)
+    args.prepared = native.PiperSagePrepared(fake, fake, fake + 4, fake)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        lib.sage_prepare(args, 0)
+    args.prepared = native.PiperSagePrepared(fake, fake, fake, fake)
+    with pytest.raises(RuntimeError, match="workspace"):
+        lib.sage_prepare(args, 0)
+
+
+def test_sage_attention_validates_before_launching(lib) -> None:
+    fake = 0x1000
+    args = native.PiperSageAttentionArgs(
+        abi_version=native.ABI_VERSION, dtype=native.FLOAT16, output_dtype=native.FLOAT16,
+        shape=native.PiperShape(1, 1, 8, 8, 64), scale=0.0,
+        query=native.PiperTensor(fake, 512, 512, 64), prepared=native.PiperSagePrepared(fake, fake, fake, fake),
+    )
+    with pytest.raises(RuntimeError, match="scale must be finite and positive"):
+        lib.sage_attention_forward(args, 0)
+    args.scale = 0.125
+    args.plan = 8
+    with pytest.raises(RuntimeError, match="unknown plan"):
+        lib.sage_attention_forward(args, 0)
+    args.plan = 0
+    with pytest.raises(RuntimeError, match="output pointer is NULL"):
+        lib.sage_attention_forward(args, 0)
+    args.is_causal = 1
+    args.shape = native.PiperShape(1, 1, 8, 9, 64)
+    with pytest.raises(RuntimeError, match="equal query and key lengths"):
+        lib.sage_attention_forward(args, 0)
+    args.is_causal, args.shape = 0, native.PiperShape(1, 1, 8, 8, 32)
+    with pytest.raises(RuntimeError, match="head_dim must be 64 or 128"):
+        lib.sage_attention_forward(args, 0)
