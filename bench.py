@@ -49,6 +49,12 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument(
         "--two-step", action="store_true", help="time the prep of Q, K, V + attention on prepared query codes"
     )
+    parser.add_argument(
+        "--operator",
+        choices=["piper_attention", "sage_attention_2pp"],
+        default="piper_attention",
+        help="the operator whose complete call is a step (default: Piper Attention, the headline)",
+    )
     return parser.parse_args()
 
 
@@ -118,7 +124,7 @@ def main() -> int:
     import torch
 
     from piper_kernels.attention.piper_attention.hip import _launch_piper_attention, _prepare_piper_attention
-    from piper_kernels.measure import attention_operations, prep_algorithmic_bytes
+    from piper_kernels.measure import attention_operations, prep_algorithmic_bytes, sage_prep_algorithmic_bytes
     from piper_kernels.workloads import WORKLOADS, make_inputs
 
     workload = WORKLOADS[args.workload]
@@ -129,13 +135,27 @@ def main() -> int:
     b, h, sq, sk, d = workload.shape
     ops = attention_operations(b, h, sq, sk, d, workload.is_causal)
 
+    sage = args.operator == "sage_attention_2pp"
+    if sage:
+        from piper_kernels.attention.sage_attention_2pp.hip import _launch_sage_attention_2pp as launch
+        from piper_kernels.attention.sage_attention_2pp.hip import _prepare_sage_attention_2pp
+
+        def prepare():
+            return _prepare_sage_attention_2pp(q, k, v, scale, workload.is_causal)
+
+    else:
+        launch = _launch_piper_attention
+
+        def prepare():
+            return _prepare_piper_attention(q, k, v, scale, workload.is_causal, quantize_query=args.two_step)
+
     def step(events=None):
         if events is not None:
             events[0].record()
-        prepared = _prepare_piper_attention(q, k, v, scale, workload.is_causal, quantize_query=args.two_step)
+        prepared = prepare()
         if events is not None:
             events[1].record()
-        out = _launch_piper_attention(prepared)
+        out = launch(prepared)
         if events is not None:
             events[2].record()
         return out
@@ -160,13 +180,21 @@ def main() -> int:
     attn_mean = sum(attn_ms) / len(attn_ms)
     prep_mean = sum(prep_ms) / len(prep_ms)
     attn_tops = ops / (attn_mean * 1e-3) / 1e12
-    prep_bytes = prep_algorithmic_bytes(b, h, sq, sk, d, workload.is_causal, quantize_query=args.two_step)
+    prep_bytes = (
+        sage_prep_algorithmic_bytes(b, h, sk, d)
+        if sage
+        else prep_algorithmic_bytes(b, h, sq, sk, d, workload.is_causal, quantize_query=args.two_step)
+    )
     value = ops / (ms_per_step * 1e-3) / 1e12
     log(f"[bench] step {ms_per_step:.4f} ms ({value:.1f} TOPS); attention {attn_mean:.4f} ms "
         f"({attn_tops:.1f} TOPS, {100 * attn_tops / INT8_PEAK_TOPS:.1f}% of INT8 peak); prep {prep_mean:.4f} ms")
 
     result = {
-        "metric": "attention TOPS + % INT8 MFMA peak, B1 H24 S16k D128 fp16, 1 MI355X",
+        "metric": (
+            "SageAttention2++ TOPS + % dense INT8/FP8 MFMA peak, 1 MI355X"
+            if sage
+            else "attention TOPS + % INT8 MFMA peak, B1 H24 S16k D128 fp16, 1 MI355X"
+        ),
         "value": round(value, 2),
         "unit": "TOPS",
         "n_gpus": 1,
@@ -180,9 +208,10 @@ def main() -> int:
         "data": "synthetic (seeded numpy PCG64 per head, fp16 inputs resident in HBM)",
         "config": {
             **workload.as_dict(),
+            "operator": args.operator,
             "step": (
                 "complete operator call: HIP prep of Q, K, V + fused attention kernel"
-                if args.two_step
+                if args.two_step and not sage
                 else "complete operator call: HIP prep of K, V + fused attention kernel quantising Q in its prologue"
             ),
             "plan": None,
@@ -212,8 +241,15 @@ def main() -> int:
     }
     from piper_kernels.attention.piper_attention._plan import select_plan
 
-    result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
-    if not args.no_cpu_baseline:
+    if sage:
+        from piper_kernels.attention.piper_attention._plan import heuristic_plan
+
+        result["config"]["plan"] = heuristic_plan(b, h, sq).as_dict()
+        result["roofline"]["traffic"] = None
+        result["dtype"] = "int8 QK, fp8 e4m3 PV"
+    else:
+        result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
+    if not args.no_cpu_baseline and not sage:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(workload, args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -91,12 +91,7 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
   const int bh = rem / head_dim;
   const int d = rem - bh * head_dim;
   const double* src = p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks * head_dim + d;
-  if (tensor == 1 && p.value_absmax) {
-    double amax = 0.0;
-    for (int c = 0; c < p.chunks; ++c) amax = fmax(amax, src[static_cast<long>(c) * head_dim]);
-    p.value_scale[rem] = __fadd_rn(static_cast<float>(amax) / 2.25f, 1e-7f);
-    return;
-  }
+  const bool absmax = tensor == 1 && p.value_absmax;
   // 16 loads in flight per step; the additions stay in chunk order
   constexpr int kBatch = 16;
   double total = 0.0;
@@ -106,9 +101,16 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) part[i] = src[static_cast<long>(c + i) * head_dim];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) total += part[i];
+    for (int i = 0; i < kBatch; ++i) total = absmax ? fmax(total, part[i]) : total + part[i];
   }
-  for (; c < p.chunks; ++c) total += src[static_cast<long>(c) * head_dim];
+  for (; c < p.chunks; ++c) {
+    const double part = src[static_cast<long>(c) * head_dim];
+    total = absmax ? fmax(total, part) : total + part;
+  }
+  if (absmax) {
+    p.value_scale[rem] = __fadd_rn(static_cast<float>(total) / 2.25f, 1e-7f);
+    return;
+  }
   dst[rem] = static_cast<float>(total / static_cast<double>(p.length));
 }
 

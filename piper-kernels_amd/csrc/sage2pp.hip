@@ -47,24 +47,26 @@ __device__ __forceinline__ uint32_t pack_fp8(float a, float b, float c, float d)
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
 }
 
-// Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave.
-// ct = query scale * key scale * softmax scale * log2 e; mrun is the running maximum (log2
-// units, per query), den this lane half's share of the denominator.
-template <int D, int NW, bool kCausal>
-__device__ __forceinline__ void sage_block_update(const char* stage, const v16i (&s)[2], float ct, int t, int q0,
-                                                  int n, int h, int key_length, v16f (&acc)[D / 32], float& den,
-                                                  float& mrun) {
-  using L = SageLayout<D, NW>;
+// Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave,
+// in two parts.  Head: raw scores, masks, block maximum and the frame move (rescale of the
+// accumulators when the running maximum grows; exact, otherwise the weight is 1).  Tail:
+// probabilities, denominator share, FP8 codes and the PV MFMAs.  ct = query scale * key scale
+// * softmax scale * log2 e; mrun is the running maximum (log2 units, per query), den this lane
+// half's share of the denominator; x carries the raw scores from head to tail.
+template <int D, bool kCausal>
+__device__ __forceinline__ void sage_block_head(const v16i (&s)[2], float ct, int t, int q0, int n, int h,
+                                                int key_length, float (&x)[32], v16f (&acc)[D / 32], float& den,
+                                                float& mrun) {
   constexpr int kChunksD = D / 32;
-
-  // ---- raw scores (exact integers as FP32) and their block maximum ----
-  float x[32];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     x[r] = unbias(s[0][r]);
     x[16 + r] = unbias(s[1][r]);
   }
+  // Both masks are scalar branches taken by one tile (and the diagonal tiles); the empty asm
+  // keeps the compiler from speculating them into per-element compares in every block.
   if (t * kKeyBlock + kKeyBlock > key_length) {  // the last tile: its padding keys score -inf
+    asm volatile("");
     const int key_base = t * kKeyBlock + 16 * h;
 #pragma unroll
     for (int r = 0; r < 32; ++r) {
@@ -74,6 +76,7 @@ __device__ __forceinline__ void sage_block_update(const char* stage, const v16i 
   }
   if constexpr (kCausal) {
     if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // block crosses this wave's diagonal
+      asm volatile("");
       const int query = q0 + n;
       const int key_base = t * kKeyBlock + 16 * h;
 #pragma unroll
@@ -87,8 +90,6 @@ __device__ __forceinline__ void sage_block_update(const char* stage, const v16i 
   const float raw_max = cross_half_max(max32(x));
   const float block_max = raw_max * ct - kLog2Of448;
   const float next = fmaxf(mrun, block_max);
-
-  // ---- move the frame when the running maximum grows (exact: otherwise the weight is 1) ----
   const bool grow = next > mrun;
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
     const float w = grow ? __builtin_amdgcn_exp2f(mrun - next) : 1.0f;  // exp2(-inf) = 0 at the start
@@ -99,7 +100,13 @@ __device__ __forceinline__ void sage_block_update(const char* stage, const v16i 
     den *= w;
     mrun = next;
   }
+}
 
+template <int D, int NW>
+__device__ __forceinline__ void sage_block_tail(const char* stage, const float (&x)[32], float ct, int n, int h,
+                                                v16f (&acc)[D / 32], float& den, float mrun) {
+  using L = SageLayout<D, NW>;
+  constexpr int kChunksD = D / 32;
   // ---- p = exp2(s ct - m') in [0, 448], the denominator share and the FP8 codes ----
   float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   uint32_t pw[8];
@@ -146,10 +153,14 @@ __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t
   copy_block<L>(p, smem + ((t + kSageLead) % kSageStages) * L::kStageBytes, bh, min(t + kSageLead, tiles - 1), wave,
                 lane);
   if (t < wave_tiles) {
-    block_scores<D, L>(smem + ((t + 1) % kSageStages) * L::kStageBytes, qf, h, krow, bias, s_next);
     const char* stage = smem + (t % kSageStages) * L::kStageBytes;
-    const float key_scale = *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
-    sage_block_update<D, NW, kCausal>(stage, s_cur, cq * key_scale, t, q0, n, h, p.key_length, acc, den, mrun);
+    const float ct = cq * *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
+    float x[32];
+    // the next block's QK MFMAs first: they run under this block's softmax (issuing them after
+    // the frame move, or interleaving them with the softmax, measured 1-5% slower)
+    block_scores<D, L>(smem + ((t + 1) % kSageStages) * L::kStageBytes, qf, h, krow, bias, s_next);
+    sage_block_head<D, kCausal>(s_cur, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
+    sage_block_tail<D, NW>(stage, x, ct, n, h, acc, den, mrun);
   }
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }

@@ -127,3 +127,11 @@ def prep_algorithmic_bytes(
     scales = 4 * batch * heads * (q_scales + -(-key_length // 64) + key_length)
     means = (4 if is_causal else 8) * batch * heads * head_dim
     return 2 * (eq + 2 * ekv) + (eq + 2 * ekv) + scales + means
+
+
+def sage_prep_algorithmic_bytes(batch: int, heads: int, key_length: int, head_dim: int) -> int:
+    """Minimum HBM bytes of the SageAttention2++ prep: fp16/bf16 reads of K and V, INT8 K and
+    FP8 V code writes, FP32 K scales (per 64 rows), K means and per-channel V scales."""
+    ekv = batch * heads * key_length * head_dim
+    scales = 4 * batch * heads * (-(-key_length // 64) + 2 * head_dim)
+    return 2 * 2 * ekv + 2 * ekv + scales

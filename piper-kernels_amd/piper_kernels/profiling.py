@@ -6,6 +6,8 @@
     python -m piper_kernels.profiling prep --workload c3 --launches 3
         run only the prep pipeline (mean partials, mean finalisation, quantisation; K and V
         only unless --two-step)
+    python -m piper_kernels.profiling attention --operator sage_attention_2pp --workload c3
+        the same for SageAttention2++ (its K/V prep, then only its attention kernel)
     python -m piper_kernels.profiling copy --bytes 1073741824 --launches 3
         a plain device-to-device copy of a known size: the calibration that turns
         FETCH_SIZE / WRITE_SIZE counter readings into bytes
@@ -33,6 +35,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--launches", type=int, default=3)
     parser.add_argument("--bytes", type=int, default=1 << 30)
     parser.add_argument("--two-step", action="store_true", help="quantise the query in the prep, not the kernel")
+    parser.add_argument("--operator", choices=["piper_attention", "sage_attention_2pp"], default="piper_attention")
     args = parser.parse_args(argv)
 
     import torch
@@ -53,6 +56,22 @@ def main(argv: list[str] | None = None) -> int:
     q, k, v = make_inputs(w, device)
     scale = w.head_dim**-0.5
     fused = not args.two_step
+    if args.operator == "sage_attention_2pp":
+        from piper_kernels.attention.sage_attention_2pp.hip import (
+            _launch_sage_attention_2pp,
+            _prepare_sage_attention_2pp,
+        )
+
+        with torch.no_grad():
+            prepared = _prepare_sage_attention_2pp(q, k, v, scale, w.is_causal)
+            for _ in range(args.launches):
+                if args.what == "attention":
+                    _launch_sage_attention_2pp(prepared)
+                else:
+                    _prepare_sage_attention_2pp(q, k, v, scale, w.is_causal)
+        torch.cuda.synchronize()
+        print(f"{args.operator} {args.what} {args.workload} x {args.launches} done", flush=True)
+        return 0
     with torch.no_grad():
         prepared = _prepare_piper_attention(q, k, v, scale, w.is_causal, quantize_query=not fused)
         for _ in range(args.launches):

@@ -21,7 +21,12 @@ from piper_kernels._hip import library as native
 from piper_kernels._hip.targets import AcceleratorTarget
 from piper_kernels.attention.piper_attention import dispatch
 from piper_kernels.attention.piper_attention._plan import MI355XPlan, select_plan
-from piper_kernels.measure import attention_operations, measure_quality, prep_algorithmic_bytes
+from piper_kernels.measure import (
+    attention_operations,
+    measure_quality,
+    prep_algorithmic_bytes,
+    sage_prep_algorithmic_bytes,
+)
 from piper_kernels.workloads import WORKLOADS, make_inputs
 
 REPO = Path(__file__).resolve().parents[1]
@@ -270,6 +275,8 @@ def test_prep_algorithmic_bytes_for_headline_shape() -> None:
     # without the query: fp16 read (2 B), code write (1 B) and one scale per 32 rows of Q drop out
     q_bytes = 3 * 24 * 16384 * 128 + 4 * 24 * 512
     assert prep_algorithmic_bytes(1, 24, 16384, 16384, 128, False, quantize_query=False) == 454_656_000 - q_bytes
+    # SageAttention2++: K and V read (2 B) and written (1 B each), K scales per 64 rows, K mean and V scales
+    assert sage_prep_algorithmic_bytes(1, 24, 16384, 128) == 6 * 24 * 16384 * 128 + 4 * 24 * (256 + 256)
 
 
 def test_workload_inputs_are_reproducible_per_head() -> None:
