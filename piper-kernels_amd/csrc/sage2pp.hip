@@ -42,8 +42,12 @@ struct SageLayout : StagePieces<sage_tile_bytes(D), NW> {  // the tile record is
   static constexpr int kVOffset = sage_v_offset(D);
 };
 
+// Four FP8 E4M3 codes in one word, a in byte 0.  Both 16-bit halves are written, so the word
+// starts from an undefined register (no clearing move).
 __device__ __forceinline__ uint32_t pack_fp8(float a, float b, float c, float d) {
-  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+  int undef;
+  asm volatile("" : "=v"(undef));
+  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, undef, false));
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
 }
 
@@ -157,7 +161,9 @@ __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t
     const float ct = cq * *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
     float x[32];
     // the next block's QK MFMAs first: they run under this block's softmax (issuing them after
-    // the frame move, or interleaving them with the softmax, measured 1-5% slower)
+    // the frame move, or interleaving them with the softmax, measured 1-5% slower; feeding the
+    // biased accumulator bits to the exp FMA with a folded constant saves the 32 subtractions
+    // but costs register copies and measured 3% slower)
     block_scores<D, L>(smem + ((t + 1) % kSageStages) * L::kStageBytes, qf, h, krow, bias, s_next);
     sage_block_head<D, kCausal>(s_cur, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
     sage_block_tail<D, NW>(stage, x, ct, n, h, acc, den, mrun);

@@ -7,9 +7,11 @@
   The remaining differences are exp2 versus exp, summation order and the rare FP8 probability
   that rounds the other way from within an ulp of a rounding midpoint (one such flip moves a
   probability by up to 1/16 of itself).  Gates: mean |err| <= 1e-4, cosine >= 0.99999 and
-  max |err| <= 5e-3 against the FP32-accumulation oracle; mean <= 2e-4 against the reference
-  mode; and the reference's own Triton-versus-reference gate (mean < 0.003, max < 0.12,
-  tests/attention/sage_attention_2pp/test_triton.py:71-98) on its shapes.
+  max |err| <= 5e-3 against the FP32-accumulation oracle; against the reference mode, a mean no
+  larger than the oracle's own distance between its two modes plus 1e-4 (that distance is the
+  reference's FP16 rounding of each 64-key partial: up to 2e-4 on short sequences, where the
+  partials are large); and the reference's own Triton-versus-reference gate (mean < 0.003,
+  max < 0.12, tests/attention/sage_attention_2pp/test_triton.py:71-98) on its shapes.
 * Invariants: every launch plan and a rerun give identical bits; strided views equal contiguous
   inputs; 16-bit outputs are the RNE rounding of the FP32 result; torch.compile(fullgraph=True).
 """
@@ -20,7 +22,7 @@ import numpy as np
 import pytest
 import torch
 
-from _parity import log
+from _parity import GOLDEN, load_golden, log
 from oracle import piper_oracle
 from oracle import sage2pp_oracle as oracle
 from piper_kernels.attention.piper_attention._plan import MI355XPlan
@@ -126,7 +128,7 @@ def test_output_against_oracle(gfx950_device, case) -> None:
         f"vs reference mode: mean {np.abs(actual - reference).mean():.2e} max {np.abs(actual - reference).max():.2e}")
     assert np.isfinite(actual).all()
     assert err.mean() <= MEAN_ABS and err.max() <= MAX_ABS and _cosine(actual, fp32) >= COSINE
-    assert np.abs(actual - reference).mean() <= 2 * MEAN_ABS
+    assert np.abs(actual - reference).mean() <= np.abs(fp32 - reference).mean() + MEAN_ABS
     # 16-bit outputs are the RNE rounding of the FP32 result
     out16 = _launch(prepared, dtype)
     assert torch.equal(out16.cpu(), torch.from_numpy(actual).to(dtype))
@@ -210,3 +212,27 @@ def test_quality_against_fp64_sdpa(gfx950_device) -> None:
     assert err.mean() < 0.01 and err.max() < 0.2
     assert err.max() <= ref_err.max() + 2e-3
     assert _cosine(actual, sdpa) >= _cosine(reference, sdpa) - 1e-5
+
+
+GOLDEN_FIXTURES = sorted((GOLDEN / "sage2pp").glob("*.npz"))
+
+
+@pytest.mark.parametrize("waves", [8, 4])
+@pytest.mark.parametrize("fixture", GOLDEN_FIXTURES, ids=[p.stem for p in GOLDEN_FIXTURES])
+def test_golden_fixture(gfx950_device, fixture, waves) -> None:
+    """Prep bit for bit and the output within the gates of the committed oracle fixtures."""
+    g = load_golden(fixture)
+    log(f"[sage golden] {fixture.stem} waves={waves}")
+    q, k, v = g["query"], g["key"], g["value"]
+    sk, d = k.shape[2], k.shape[3]
+    prepared = _prepare(q, k, v, g["scale"], g["is_causal"], gfx950_device, plan=MI355XPlan(waves=waves))
+    assert _bits_equal(prepared.key_mean.cpu().numpy(), g["key_mean"])
+    assert _bits_equal(prepared.key_scale.cpu().numpy(), g["key_block_scale"])
+    assert _bits_equal(prepared.value_scale.cpu().numpy(), g["value_scale"])
+    assert np.array_equal(prepared.key_code().cpu().numpy()[:, :, :sk], g["key_code"])
+    assert np.array_equal(prepared.value_code().cpu().numpy()[:, :, :sk], g["value_code"])
+    actual = _launch(prepared).cpu().numpy()
+    err = np.abs(actual - g["output_fp32_accumulation"])
+    assert err.mean() <= MEAN_ABS and err.max() <= MAX_ABS
+    modes = np.abs(g["output_fp32_accumulation"] - g["output_reference"]).mean()
+    assert np.abs(actual - g["output_reference"]).mean() <= modes + MEAN_ABS
