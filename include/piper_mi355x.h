@@ -166,7 +166,10 @@ typedef struct piper_prepare_args {
 #define PIPER_PLAN_FOUR_WAVES 1     /* 4 query waves per workgroup (for grids below the CU count) */
 #define PIPER_PLAN_CAUSAL_FORWARD 2 /* causal: query tiles in forward order */
 #define PIPER_PLAN_NO_XCD_REMAP 4   /* hardware workgroup order */
-#define PIPER_PLAN_MASK 7
+#define PIPER_PLAN_CAUSAL_INTERLEAVE 8 /* causal, longest first: query tiles dispatched longest first
+                                          across the heads of each XCD (across all heads with
+                                          PIPER_PLAN_NO_XCD_REMAP) instead of head by head */
+#define PIPER_PLAN_MASK 15
 
 typedef struct piper_attention_args {
   int32_t abi_version;  /* PIPER_ABI_VERSION */

@@ -114,6 +114,7 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   ap.scale_log2e = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   ap.causal_forward = (plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
   ap.xcd_remap = (plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
+  ap.causal_interleave = (plan & PIPER_PLAN_CAUSAL_INTERLEAVE) ? 1 : 0;
   ap.heads = static_cast<int>(s.heads);
   if (query != nullptr) {
     ap.fused_query = 1;
@@ -362,6 +363,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   sp.scale_log2e = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
   sp.causal_forward = (a->plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
   sp.xcd_remap = (a->plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
+  sp.causal_interleave = (a->plan & PIPER_PLAN_CAUSAL_INTERLEAVE) ? 1 : 0;
   if (static_cast<int64_t>(sp.query_tiles) * sp.batch_heads > 0x7fffffff)
     return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
 

@@ -197,13 +197,11 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5;  // lane half
   const int n = lane & 31;  // query column within the wave
-  const int logical = p.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
-  // causal: the longest query tiles (most key blocks) are dispatched first
   // wave-uniform in SGPRs (the runtime division is VALU code): per-block key scales then come
   // from scalar loads, which do not share the vmcnt counter with the direct LDS copies
-  const int bh = __builtin_amdgcn_readfirstlane(logical / p.query_tiles);
-  const int qtile_fwd = __builtin_amdgcn_readfirstlane(logical - bh * p.query_tiles);
-  const int qtile = kCausal && !p.causal_forward ? p.query_tiles - 1 - qtile_fwd : qtile_fwd;
+  const TileCoord tc = workgroup_tile<kCausal>(p);
+  const int bh = __builtin_amdgcn_readfirstlane(tc.bh);
+  const int qtile = __builtin_amdgcn_readfirstlane(tc.qtile);
   const int q0 = qtile * (NW * 32) + wave * 32;  // first query of this wave
   const bool wave_live = q0 < p.query_length;
 

@@ -94,6 +94,7 @@ struct AttnParams {
   float scale_log2e;
   int causal_forward;  // causal grids: 1 = query tiles in forward order, 0 = longest first
   int xcd_remap;       // 1 = consecutive workgroups of a head share an XCD, 0 = hardware order
+  int causal_interleave;  // causal, longest first: 1 = across the heads of an XCD, 0 = head by head
   // Fused query quantisation: each wave quantises its own 32-row query block from `query`
   // (query_code and query_scale are then unused).
   int fused_query;
@@ -134,6 +135,7 @@ struct SageParams {
   float scale_log2e;
   int causal_forward;
   int xcd_remap;
+  int causal_interleave;
 };
 
 hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream);

@@ -26,6 +26,42 @@ struct StagePieces {
   static_assert(kStageBytes % 1024 == 0, "a stage is a whole number of KiB");
 };
 
+// Workgroup -> (batch-head, query tile) of both attention kernels.  With the XCD remap the
+// logical ids of one XCD are contiguous (xcd_remap).  Non-causal grids and causal grids in
+// forward order walk the query tiles of one head after another; causal grids in longest-first
+// order (the work of a query tile grows with its index) walk each head's tiles longest first.
+// With causal_interleave they instead go in longest-processing-time order across the heads
+// that share an L2: when the batch-heads split evenly over the 8 XCDs, each XCD's range covers
+// its own batch-heads and walks the query tiles longest first across all of them (without the
+// remap the whole grid does).  That shortens the tail of short and medium sequences; for long
+// sequences with many heads the head-by-head order keeps more of the K/V reuse in L2.
+struct TileCoord {
+  int bh;
+  int qtile;
+};
+
+template <bool kCausal, class Params>
+__device__ __forceinline__ TileCoord workgroup_tile(const Params& p) {
+  const int logical = p.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
+  const int qt = p.query_tiles;
+  if (kCausal && !p.causal_forward && p.causal_interleave && !(p.xcd_remap && (p.batch_heads & 7) != 0)) {
+    int heads = p.batch_heads;
+    int base_bh = 0;
+    int r = logical;
+    if (p.xcd_remap) {  // batch_heads % 8 == 0: one group of heads per XCD
+      heads = p.batch_heads >> 3;
+      const int group = logical / (heads * qt);
+      base_bh = group * heads;
+      r = logical - group * heads * qt;
+    }
+    const int rank = r / heads;
+    return {base_bh + (r - rank * heads), qt - 1 - rank};
+  }
+  const int bh = logical / qt;
+  const int qtile = logical - bh * qt;
+  return {bh, kCausal && !p.causal_forward ? qt - 1 - qtile : qtile};
+}
+
 // One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from its global address to
 // LDS byte lds + 16 * i.  Issued as inline assembly so that the compiler's wait insertion does
 // not treat every later LDS read as dependent on it: the waits are explicit (stage_barrier,

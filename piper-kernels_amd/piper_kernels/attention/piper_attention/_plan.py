@@ -25,6 +25,8 @@ PLAN_TABLE = Path(__file__).with_name("mi355x_plans.json")
 PLAN_FOUR_WAVES = 1
 PLAN_CAUSAL_FORWARD = 2
 PLAN_NO_XCD_REMAP = 4
+PLAN_CAUSAL_INTERLEAVE = 8
+PLAN_MASK = 15
 
 
 @dataclass(frozen=True)
@@ -35,11 +37,14 @@ class MI355XPlan:
     per workgroup, one workgroup per CU; 4: 128 queries). ``causal_longest_first``: causal
     grids dispatch the query tiles with the most key blocks first. ``xcd_remap``: consecutive
     workgroups of one head run on one XCD (its L2 then serves the head's K/V tiles).
+    ``causal_interleave``: causal, longest first, across the heads of an XCD rather than head
+    by head (a shorter tail for short and medium sequences; less L2 reuse for long ones).
     """
 
     waves: int = 8
     causal_longest_first: bool = True
     xcd_remap: bool = True
+    causal_interleave: bool = False
 
     def __post_init__(self) -> None:
         if self.waves not in (4, 8):
@@ -56,16 +61,18 @@ class MI355XPlan:
             (PLAN_FOUR_WAVES if self.waves == 4 else 0)
             | (0 if self.causal_longest_first else PLAN_CAUSAL_FORWARD)
             | (0 if self.xcd_remap else PLAN_NO_XCD_REMAP)
+            | (PLAN_CAUSAL_INTERLEAVE if self.causal_interleave else 0)
         )
 
     @classmethod
     def from_id(cls, plan_id: int) -> "MI355XPlan":
-        if not 0 <= plan_id <= PLAN_FOUR_WAVES | PLAN_CAUSAL_FORWARD | PLAN_NO_XCD_REMAP:
+        if not 0 <= plan_id <= PLAN_MASK:
             raise ValueError(f"unknown plan id {plan_id}")
         return cls(
             waves=4 if plan_id & PLAN_FOUR_WAVES else 8,
             causal_longest_first=not plan_id & PLAN_CAUSAL_FORWARD,
             xcd_remap=not plan_id & PLAN_NO_XCD_REMAP,
+            causal_interleave=bool(plan_id & PLAN_CAUSAL_INTERLEAVE),
         )
 
     def workgroups(self, batch: int, heads: int, query_length: int) -> int:

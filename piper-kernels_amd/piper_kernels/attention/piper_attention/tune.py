@@ -2,7 +2,8 @@
 
 Counterpart of the reference's ``benchmarks/tune_piper_attention.py:53-221``: a bounded
 search over the plan axes the gfx950 kernel exposes (query waves per workgroup, causal
-query-tile order, XCD-aware workgroup order), quality-gated, whose result is frozen into
+query-tile order -- forward, longest first head by head, or longest first across the heads of
+an XCD -- and XCD-aware workgroup order), quality-gated, whose result is frozen into
 ``mi355x_plans.json`` for ``select_plan``.
 
     python -m piper_kernels.attention.piper_attention.tune --workloads c1 c2 c3 c4 c5 --write
@@ -36,8 +37,12 @@ if __package__ in (None, ""):
 def candidate_plans(is_causal: bool):
     from piper_kernels.attention.piper_attention._plan import MI355XPlan
 
-    orders = (True, False) if is_causal else (True,)
-    return [MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x) for w, o, x in product((8, 4), orders, (True, False))]
+    # causal orders: (longest first, interleaved across heads); both flags only matter when causal
+    orders = ((True, False), (True, True), (False, False)) if is_causal else ((True, False),)
+    return [
+        MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x, causal_interleave=i)
+        for w, (o, i), x in product((8, 4), orders, (True, False))
+    ]
 
 
 def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launches: int, margin: float) -> dict:
@@ -92,7 +97,8 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
     batch_heads, ql, kl, hd, causal = shape_key(b, h, sq, sk, d, is_causal)
     return {
         "key": {"batch_heads": batch_heads, "query_length": ql, "key_length": kl, "head_dim": hd, "is_causal": causal},
-        "plan": {"waves": best.waves, "causal_longest_first": best.causal_longest_first, "xcd_remap": best.xcd_remap},
+        "plan": {"waves": best.waves, "causal_longest_first": best.causal_longest_first, "xcd_remap": best.xcd_remap,
+                 "causal_interleave": best.causal_interleave},
         "candidates": [
             {"plan_id": p.plan_id, **p.as_dict(), "median_ms": round(medians[p], 5), "bitwise_equal_to_default": passed[p]}
             for p in plans

@@ -179,26 +179,28 @@ def test_plan_selection() -> None:
     assert _plan.heuristic_plan(1, 2, 193) == MI355XPlan(waves=4)
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
-                                        "block_m": 256, "block_n": 64}
+                                        "causal_interleave": False, "block_m": 256, "block_n": 64}
     with pytest.raises(ValueError):
         MI355XPlan(waves=2)
     with pytest.raises(ValueError):
-        MI355XPlan.from_id(8)
+        MI355XPlan.from_id(16)
 
 
 def test_plan_ids_round_trip_and_match_the_header() -> None:
     from piper_kernels.attention.piper_attention import _plan
 
     header = (REPO / "include" / "piper_mi355x.h").read_text()
-    for name, value in (("FOUR_WAVES", 1), ("CAUSAL_FORWARD", 2), ("NO_XCD_REMAP", 4), ("MASK", 7)):
+    for name, value in (("FOUR_WAVES", 1), ("CAUSAL_FORWARD", 2), ("NO_XCD_REMAP", 4), ("CAUSAL_INTERLEAVE", 8),
+                        ("MASK", 15)):
         assert f"#define PIPER_PLAN_{name} {value}" in header
-    assert _plan.PLAN_FOUR_WAVES == 1 and _plan.PLAN_CAUSAL_FORWARD == 2 and _plan.PLAN_NO_XCD_REMAP == 4
+    assert (_plan.PLAN_FOUR_WAVES, _plan.PLAN_CAUSAL_FORWARD, _plan.PLAN_NO_XCD_REMAP) == (1, 2, 4)
+    assert (_plan.PLAN_CAUSAL_INTERLEAVE, _plan.PLAN_MASK) == (8, 15)
     ids = set()
-    for plan_id in range(8):
+    for plan_id in range(16):
         plan = MI355XPlan.from_id(plan_id)
         assert plan.plan_id == plan_id
         ids.add(plan)
-    assert len(ids) == 8
+    assert len(ids) == 16
 
 
 def test_frozen_plan_table_lookup_and_fallback(tmp_path, monkeypatch) -> None:

@@ -131,7 +131,7 @@ def test_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 8
+    args.plan = 16
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward(args, 0)
     args.plan = 0
@@ -189,7 +189,7 @@ def test_fused_attention_validates_before_launching(lib) -> None:
     args.query = native.PiperTensor(fake, 512, 512, 64)
     with pytest.raises(RuntimeError, match="output pointer is NULL"):
         lib.attention_forward_fused(args, 0)
-    args.plan = 8
+    args.plan = 16
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward_fused(args, 0)
     args.plan, args.abi_version = 0, 2
@@ -244,7 +244,7 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.sage_attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 8
+    args.plan = 16
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.sage_attention_forward(args, 0)
     args.plan = 0
