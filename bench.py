@@ -12,8 +12,11 @@ Prints ONE JSON line.  ``value`` = whole-call TOPS (reference op count 4*B*H*Sq*
 call, benchmarks/benchmark_attention.py:184-193).  ``roofline`` prices the dominant
 kernel (the fused attention kernel) against MI355X's dense INT8 MFMA peak, with its
 average duration measured by HIP events recorded on the launch stream inside the timed
-region.  ``cpu_baseline`` times the CPU oracle (a numpy restatement of the reference's
-portable path) on a bounded slice of the same workload, on one host thread.
+region.  ``mfma_peak_measured`` is the sustained dense INT8 and FP8 MFMA rate of the same GPU
+(the library's back-to-back MFMA probe, results checked), and ``attention_kernel`` also
+reports the kernel's fraction of that measured INT8 rate.  ``cpu_baseline`` times the CPU
+oracle (a numpy restatement of the reference's portable path) on a bounded slice of the same
+workload, on one host thread.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline] [--two-step]
 """
@@ -249,6 +252,17 @@ def main() -> int:
         result["dtype"] = "int8 QK, fp8 e4m3 PV"
     else:
         result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
+    # the sustained dense MFMA rate of this GPU (library probe, after the timed region)
+    from piper_kernels._hip import library as native
+    from piper_kernels.measure import measure_mfma_peak
+
+    log("[bench] MFMA probe")
+    measured = {
+        "int8": measure_mfma_peak(native.MFMA_PROBE_I8, device),
+        "fp8": measure_mfma_peak(native.MFMA_PROBE_F8, device),
+    }
+    result["mfma_peak_measured"] = measured
+    result["attention_kernel"]["percent_of_measured_int8_peak"] = round(100 * attn_tops / measured["int8"]["tops"], 2)
     if not args.no_cpu_baseline and not sage:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(workload, args.cpu_seconds)

@@ -278,6 +278,20 @@ int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layo
 int piper_sage_prepare(const piper_sage_prepare_args* args, void* stream);
 int piper_sage_attention_forward(const piper_sage_attention_args* args, void* stream);
 
+/* Roofline calibration; no counterpart in the reference (whose benchmarks price kernels
+ * against published peaks only).  Runs `workgroups` x 512 threads of back-to-back dense MFMAs
+ * of one kind on `stream`: each wave issues 4 * `iterations` MFMAs with all-ones operands
+ * (INT8 1, FP8 E4M3 1.0), so that events around the launch give the sustained matrix-core rate
+ * at the running clock.  Per wave: 4 * iterations * PIPER_MFMA_PROBE_OPS(kind) operations.
+ * `sink` receives one 32-bit word per thread (workgroups * 512 words): the sum of the thread's
+ * 64 accumulator registers, iterations * 2048 modulo 2^32 for PIPER_MFMA_PROBE_I8 and the FP32
+ * bits of iterations * 4096 for PIPER_MFMA_PROBE_F8 (exact for iterations <= 4096). */
+#define PIPER_MFMA_PROBE_I8 0 /* v_mfma_i32_32x32x32_i8 */
+#define PIPER_MFMA_PROBE_F8 1 /* v_mfma_f32_32x32x64_f8f6f4 on FP8 E4M3 */
+#define PIPER_MFMA_PROBE_THREADS 512
+#define PIPER_MFMA_PROBE_OPS(kind) ((kind) == PIPER_MFMA_PROBE_I8 ? 65536 : 131072)
+int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream);
+
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* piper_last_error(void);
 

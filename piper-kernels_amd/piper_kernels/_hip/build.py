@@ -19,7 +19,7 @@ CSRC = PACKAGE_ROOT / "csrc"
 INCLUDE = PACKAGE_ROOT.parent / "include"
 BUILD_DIR = PACKAGE_ROOT / "_build"
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpiper_mi355x.so"
-SOURCES = ("abi.hip", "prep.hip", "attention.hip", "sage2pp.hip")
+SOURCES = ("abi.hip", "prep.hip", "attention.hip", "sage2pp.hip", "probe.hip")
 OFFLOAD_ARCH = "gfx950"
 
 COMPILE_FLAGS = (

@@ -34,10 +34,17 @@ EXPORTED_SYMBOLS = (
     "piper_sage_prepared_layout",
     "piper_sage_prepare",
     "piper_sage_attention_forward",
+    "piper_mfma_probe",
     "piper_last_error",
 )
 
 PREPARE_SKIP_QUERY = 1  # piper_prepare_args.flags
+
+# piper_mfma_probe kinds, workgroup size and operations per MFMA (PIPER_MFMA_PROBE_* in the header)
+MFMA_PROBE_I8 = 0
+MFMA_PROBE_F8 = 1
+MFMA_PROBE_THREADS = 512
+MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -226,6 +233,8 @@ class NativeLibrary:
         lib.piper_sage_prepare.restype = ctypes.c_int
         lib.piper_sage_attention_forward.argtypes = [ctypes.POINTER(PiperSageAttentionArgs), _ptr]
         lib.piper_sage_attention_forward.restype = ctypes.c_int
+        lib.piper_mfma_probe.argtypes = [_i32, _i32, _i32, _ptr, _ptr]
+        lib.piper_mfma_probe.restype = ctypes.c_int
         version = lib.piper_abi_version()
         if version != ABI_VERSION:
             raise LibraryUnavailableError(
@@ -275,6 +284,9 @@ class NativeLibrary:
         self._check(
             self._lib.piper_sage_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_sage_attention_forward"
         )
+
+    def mfma_probe(self, kind: int, workgroups: int, iterations: int, sink: int, stream: int) -> None:
+        self._check(self._lib.piper_mfma_probe(kind, workgroups, iterations, _ptr(sink), _ptr(stream)), "piper_mfma_probe")
 
 
 _lock = threading.Lock()

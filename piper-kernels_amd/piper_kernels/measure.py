@@ -6,6 +6,11 @@
 * ``measure_quality`` -- the metric definitions of ``benchmarks/lib/quality.py:88-252``:
   mean/max absolute error, relative L1/L2 error, SQNR in dB and cosine similarity over the
   finite pairs, with non-finite values counted separately.
+
+``measure_mfma_peak`` has no counterpart in the reference (whose benchmarks quote published
+peaks only): it times the library's back-to-back MFMA probe to give the sustained dense
+matrix-core rate of the GPU at hand, which the attention kernels are priced against next to
+the published 5.0 P/s.
 """
 
 from __future__ import annotations
@@ -135,3 +140,55 @@ def sage_prep_algorithmic_bytes(batch: int, heads: int, key_length: int, head_di
     ekv = batch * heads * key_length * head_dim
     scales = 4 * batch * heads * (-(-key_length // 64) + 2 * head_dim)
     return 2 * 2 * ekv + 2 * ekv + scales
+
+
+def mfma_probe_expected(kind: int, iterations: int) -> int:
+    """The 32-bit word every probe thread stores: the sum of its 64 accumulators, each
+    ``iterations * K`` with all-ones operands (K = 32 INT8, 64 FP8); FP8 as FP32 bits."""
+    from ._hip import library as native
+
+    if kind == native.MFMA_PROBE_I8:
+        return (iterations * 2048) % (1 << 32)
+    import struct
+
+    return struct.unpack("<I", struct.pack("<f", float(iterations * 4096)))[0]
+
+
+def measure_mfma_peak(kind: int, device: torch.device, *, iterations: int = 4096, launches: int = 5) -> dict:
+    """Sustained dense MFMA rate (tera-ops/s) of the library's probe on ``device``.
+
+    Four workgroups of 8 waves per compute unit, four independent accumulator chains per wave;
+    the median of ``launches`` timed launches (HIP events on the launch stream) after two
+    warm-up launches.  Every thread's result word is checked against its exact value, so a
+    time cannot come from elided work.  ``iterations <= 4096`` keeps the FP8 check exact.
+    """
+    from ._hip import library as native
+
+    lib = native.load_library()
+    workgroups = 4 * torch.cuda.get_device_properties(device).multi_processor_count
+    sink = torch.zeros(workgroups * native.MFMA_PROBE_THREADS, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device)
+    with torch.cuda.device(device):
+        for _ in range(2):
+            lib.mfma_probe(kind, workgroups, iterations, sink.data_ptr(), stream.cuda_stream)
+        times = []
+        for _ in range(launches):
+            begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            begin.record(stream)
+            lib.mfma_probe(kind, workgroups, iterations, sink.data_ptr(), stream.cuda_stream)
+            end.record(stream)
+            end.synchronize()
+            times.append(begin.elapsed_time(end))
+    expected = mfma_probe_expected(kind, iterations)
+    words = sink.cpu().numpy().view("uint32")
+    if not (words == expected).all():
+        raise RuntimeError(f"MFMA probe kind {kind} returned wrong results ({int((words != expected).sum())} threads)")
+    ms = sorted(times)[len(times) // 2]
+    ops = workgroups * (native.MFMA_PROBE_THREADS // 64) * 4 * iterations * native.MFMA_PROBE_OPS[kind]
+    return {
+        "instruction": "v_mfma_i32_32x32x32_i8" if kind == native.MFMA_PROBE_I8 else "v_mfma_f32_32x32x64_f8f6f4",
+        "tops": round(ops / (ms * 1e-3) / 1e12, 1),
+        "ms_per_launch": round(ms, 4),
+        "workgroups": workgroups,
+        "iterations": iterations,
+    }

@@ -257,3 +257,39 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     args.is_causal, args.shape = 0, native.PiperShape(1, 1, 8, 8, 32)
     with pytest.raises(RuntimeError, match="head_dim must be 64 or 128"):
         lib.sage_attention_forward(args, 0)
+
+
+def test_mfma_probe_constants_match_the_header(tmp_path) -> None:
+    source = tmp_path / "probe.c"
+    source.write_text('#include <stdio.h>\n#include "piper_mi355x.h"\nint main(void) {\n'
+                      '  printf("%d %d %d %d %d\\n", PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8, PIPER_MFMA_PROBE_THREADS,\n'
+                      '         PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8));\n'
+                      '  return 0; }\n')
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", f"-I{REPO / 'include'}", str(source), "-o", str(exe)], check=True)
+    values = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
+    assert values == [native.MFMA_PROBE_I8, native.MFMA_PROBE_F8, native.MFMA_PROBE_THREADS,
+                      native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8]]
+    # 32x32x32 INT8 and 32x32x64 FP8: two operations per multiply-add
+    assert native.MFMA_PROBE_OPS == {native.MFMA_PROBE_I8: 2 * 32 * 32 * 32, native.MFMA_PROBE_F8: 2 * 32 * 32 * 64}
+
+
+def test_mfma_probe_validates_before_launching(lib) -> None:
+    with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
+        lib.mfma_probe(2, 1, 1, 0x1000, 0)
+    with pytest.raises(RuntimeError, match="workgroups and"):
+        lib.mfma_probe(native.MFMA_PROBE_I8, 0, 1, 0x1000, 0)
+    with pytest.raises(RuntimeError, match="workgroups and"):
+        lib.mfma_probe(native.MFMA_PROBE_F8, 1, 0, 0x1000, 0)
+    with pytest.raises(RuntimeError, match="sink must be"):
+        lib.mfma_probe(native.MFMA_PROBE_I8, 1, 1, 0, 0)
+    with pytest.raises(RuntimeError, match="sink must be"):
+        lib.mfma_probe(native.MFMA_PROBE_I8, 1, 1, 0x1002, 0)
+
+
+def test_mfma_probe_expected_words() -> None:
+    from piper_kernels.measure import mfma_probe_expected
+
+    assert mfma_probe_expected(native.MFMA_PROBE_I8, 4096) == 4096 * 64 * 32
+    assert mfma_probe_expected(native.MFMA_PROBE_I8, 1 << 21) == (64 * 32 << 21) % (1 << 32)
+    assert mfma_probe_expected(native.MFMA_PROBE_F8, 4096) == 0x4B800000  # 2^24 as FP32
