@@ -45,13 +45,14 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
   // the V statistic of SageAttention2++ is max |v| (exact in any order); otherwise a sum
   const bool absmax = tensor == 1 && p.value_absmax;
   int row = row0;
-  for (; row + 8 <= row1; row += 8) {  // 8 loads in flight, adds still in row order
-    uint4 raw[8];
+  constexpr int kInFlight = 16;
+  for (; row + kInFlight <= row1; row += kInFlight) {  // 16 loads in flight, adds still in row order
+    uint4 raw[kInFlight];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kInFlight; ++u)
       raw[u] = *reinterpret_cast<const uint4*>(base + static_cast<long>(row + u) * t.stride_seq);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kInFlight; ++u) {
       float f[8];
       widen8<kBf16>(raw[u], f);
 #pragma unroll
@@ -92,8 +93,8 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
   const int d = rem - bh * head_dim;
   const double* src = p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks * head_dim + d;
   const bool absmax = tensor == 1 && p.value_absmax;
-  // 16 loads in flight per step; the additions stay in chunk order
-  constexpr int kBatch = 16;
+  // 64 loads in flight per step; the additions stay in chunk order
+  constexpr int kBatch = 64;
   double total = 0.0;
   int c = 0;
   for (; c + kBatch <= p.chunks; c += kBatch) {
@@ -116,8 +117,8 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
 
 // ---------------------------------------------------------------------------------------
 // Quantisation.  Each wave owns one unit: a 32-row Q block, a 64-row K block or a 64-key V
-// tile.  A workgroup (4 waves) holds units of one kind only, so V workgroups can use
-// workgroup barriers around their LDS transpose.
+// tile (a workgroup of 4 waves holds units of one kind only).  No LDS: V tiles are written
+// transposed straight from registers.
 // ---------------------------------------------------------------------------------------
 // Q or K block of kRows rows: one scale over kRows x D values.
 // Codes go to rows of kStride bytes (D for query codes, the padded tile stride for keys).
@@ -183,9 +184,6 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
 
 template <bool kBf16, int D>
 __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
-  constexpr int kVStride = kKeyBlock + 16;  // LDS row stride of a V^T tile (bytes)
-  __shared__ __attribute__((aligned(16))) int8_t vt_lds[4][D * kVStride];
-
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int block = blockIdx.x;
@@ -215,34 +213,48 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
     return;
   }
 
-  // ---- V tile: per-key scales, codes transposed through LDS, tile column sums ----
+  // ---- V tile: per-key scales, codes written transposed from registers, tile column sums ----
   const int unit = (block - p.q_blocks_wg - p.k_blocks_wg) * 4 + wave;
-  const bool active = unit < p.batch_heads * p.nkb;
-  int8_t* lds = vt_lds[wave];
-  if (active) {
-    const int bh = unit / p.nkb;
-    const int kb = unit - bh * p.nkb;
-    const int b = bh / p.heads;
-    const int h = bh - b * p.heads;
-    constexpr int kGroups = D / 8;
-    constexpr int kRowsPerIter = kWave / kGroups;
-    constexpr int kIters = kKeyBlock / kRowsPerIter;
-    const int group = lane % kGroups;
-    const int sub = lane / kGroups;
-    const uint16_t* base = static_cast<const uint16_t*>(p.value.data) + b * p.value.stride_batch +
-                           h * p.value.stride_head + group * 8;
-    float mu[8];
+  if (unit >= p.batch_heads * p.nkb) return;
+  const int bh = unit / p.nkb;
+  const int kb = unit - bh * p.nkb;
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  // lane (group, sub) owns columns [8 group, +8) of the kKeys consecutive keys
+  // [kKeys sub, +kKeys): its codes, packed four keys to a word, are the 16-byte (D = 128) or
+  // 8-byte (D = 64) pieces of its eight V^T rows -- no transpose through LDS.
+  constexpr int kGroups = D / 8;
+  constexpr int kSubs = kWave / kGroups;
+  constexpr int kKeys = kKeyBlock / kSubs;
+  const int group = lane % kGroups;
+  const int sub = lane / kGroups;
+  const int key0 = sub * kKeys;  // first key of this lane in the tile
+  const uint16_t* base = static_cast<const uint16_t*>(p.value.data) + b * p.value.stride_batch +
+                         h * p.value.stride_head + group * 8;
+  uint4 raw[kKeys];  // every row in flight before any arithmetic
 #pragma unroll
-    for (int i = 0; i < 8; ++i) mu[i] = p.center_value ? p.value_mean[static_cast<long>(bh) * D + group * 8 + i] : 0.0f;
-#pragma unroll 4
-    for (int it = 0; it < kIters; ++it) {
-      const int key_in_tile = it * kRowsPerIter + sub;
-      const int row = kb * kKeyBlock + key_in_tile;
+  for (int j = 0; j < kKeys; ++j) {
+    const int row = kb * kKeyBlock + key0 + j;
+    raw[j] = row < p.key_length ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
+                                : make_uint4(0, 0, 0, 0);
+  }
+  float mu[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mu[i] = p.center_value ? p.value_mean[static_cast<long>(bh) * D + group * 8 + i] : 0.0f;
+  uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D);
+  float* meta = reinterpret_cast<float*>(tile + kv_log_offset(D));
+  uint32_t packed[8][kKeys / 4];  // [column][four keys]
+  int colsum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int j4 = 0; j4 < kKeys / 4; ++j4) {
+    uint32_t word[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = 4 * j4 + u;
+      const int row = kb * kKeyBlock + key0 + j;
       const bool valid = row < p.key_length;
-      const uint4 raw = valid ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
-                              : make_uint4(0, 0, 0, 0);
       float f[8];
-      widen8<kBf16>(raw, f);
+      widen8<kBf16>(raw[j], f);
       float amax = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -253,36 +265,37 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
       const float scale = scale_from_amax(amax);
       const Divisor divisor(scale);
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<int8_t>(code_of(f[i], divisor));
+      for (int i = 0; i < 8; ++i) word[u][i] = code_word(f[i], divisor);
       if (group == 0) {
-        float* meta = reinterpret_cast<float*>(p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D) + kv_log_offset(D));
         p.value_scale[static_cast<long>(bh) * p.sk64 + row] = valid ? scale : 0.0f;
-        meta[key_in_tile] = valid ? log2f(scale) : -__builtin_inff();
-        meta[kKeyBlock + key_in_tile] = valid ? 1.0f / (255.0f * scale) : 0.0f;
+        meta[key0 + j] = valid ? log2f(scale) : -__builtin_inff();
+        meta[kKeyBlock + key0 + j] = valid ? 1.0f / (255.0f * scale) : 0.0f;
       }
     }
-  }
-  __syncthreads();
-  if (!active) return;
-  // transposed rows: lane owns features d = lane, lane + 64, ...
-  uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D);
-  int32_t* correction = reinterpret_cast<int32_t*>(tile + kv_corr_offset(D));
-  for (int d = lane; d < D; d += kWave) {
-    const uint4* src = reinterpret_cast<const uint4*>(lds + d * kVStride);
-    uint4* dst = reinterpret_cast<uint4*>(tile + kv_v_offset(D) + d * kv_v_stride());
-    int sum = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4 w = src[j];
-      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.x), 0x01010101, sum, false);
-      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.y), 0x01010101, sum, false);
-      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.z), 0x01010101, sum, false);
-      sum = __builtin_amdgcn_sdot4(static_cast<int>(w.w), 0x01010101, sum, false);
-      dst[j] = w;
+    for (int i = 0; i < 8; ++i) {
+      packed[i][j4] = pack_low_bytes(word[0][i], word[1][i], word[2][i], word[3][i]);
+      colsum[i] = __builtin_amdgcn_sdot4(static_cast<int>(packed[i][j4]), 0x01010101, colsum[i], false);
     }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint8_t* dst = tile + kv_v_offset(D) + (group * 8 + i) * kv_v_stride() + key0;
+    if constexpr (kKeys == 16)
+      *reinterpret_cast<uint4*>(dst) = make_uint4(packed[i][0], packed[i][1], packed[i][2], packed[i][3]);
+    else
+      *reinterpret_cast<uint2*>(dst) = make_uint2(packed[i][0], packed[i][1]);
+  }
+  // column sums over the tile's 64 keys: the kSubs lanes sharing a group hold disjoint keys
+#pragma unroll
+  for (int m = kGroups; m < kWave; m <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) colsum[i] += __shfl_xor(colsum[i], m, kWave);
+  if (sub == 0) {
     // |PV| <= 64 * 255 * 127 < 2^22, so the biased accumulator stays exact (common.h)
-    correction[d] = 128 * sum + kAccBias;
+    int32_t* correction = reinterpret_cast<int32_t*>(tile + kv_corr_offset(D)) + group * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) correction[i] = 128 * colsum[i] + kAccBias;
   }
 }
 
@@ -291,12 +304,10 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
 // owns a 64-row K block (the Piper K path, into the SageAttention2++ tile record) or a
 // 64-key V tile: FP8 E4M3 codes of v / scale[channel] (the correctly rounded FP32 quotient,
 // then v_cvt_pk_fp8_f32: round to nearest even, bit-identical to torch's float8_e4m3fn
-// cast), transposed through LDS into the record's V^T rows.  Keys past the end get code 0.
+// cast), written transposed into the record's V^T rows.  Keys past the end get code 0.
 // ---------------------------------------------------------------------------------------
 template <bool kBf16, int D>
 __global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParams p) {
-  constexpr int kVStride = kKeyBlock + 16;  // LDS row stride of a V^T tile (bytes)
-  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[4][D * kVStride];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -315,51 +326,58 @@ __global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParam
     return;
   }
 
+  // V tile: lane (group, sub) owns columns [8 group, +8) of the kKeys consecutive keys
+  // [kKeys sub, +kKeys), converts them with the per-channel divisors and packs four keys of a
+  // column per word: the 16-byte (D = 128) or 8-byte (D = 64) pieces of its eight V^T rows.
   const int unit = (block - p.k_blocks_wg) * 4 + wave;
-  const bool active = unit < p.batch_heads * p.nkb;
-  uint8_t* lds = vt_lds[wave];
-  if (active) {
-    const int bh = unit / p.nkb;
-    const int kb = unit - bh * p.nkb;
-    const int b = bh / p.heads;
-    const int h = bh - b * p.heads;
-    constexpr int kGroups = D / 8;
-    constexpr int kRowsPerIter = kWave / kGroups;
-    constexpr int kIters = kKeyBlock / kRowsPerIter;
-    const int group = lane % kGroups;
-    const int sub = lane / kGroups;
-    const uint16_t* base = static_cast<const uint16_t*>(p.value.data) + b * p.value.stride_batch +
-                           h * p.value.stride_head + group * 8;
-    Divisor divisor[8];  // this lane's 8 channels
+  if (unit >= p.batch_heads * p.nkb) return;
+  const int bh = unit / p.nkb;
+  const int kb = unit - bh * p.nkb;
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  constexpr int kGroups = D / 8;
+  constexpr int kSubs = kWave / kGroups;
+  constexpr int kKeys = kKeyBlock / kSubs;
+  const int group = lane % kGroups;
+  const int sub = lane / kGroups;
+  const int key0 = sub * kKeys;
+  const uint16_t* base = static_cast<const uint16_t*>(p.value.data) + b * p.value.stride_batch +
+                         h * p.value.stride_head + group * 8;
+  uint4 raw[kKeys];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) divisor[i] = Divisor(p.value_scale[static_cast<long>(bh) * D + group * 8 + i]);
-#pragma unroll 4
-    for (int it = 0; it < kIters; ++it) {
-      const int key_in_tile = it * kRowsPerIter + sub;
-      const int row = kb * kKeyBlock + key_in_tile;
-      const bool valid = row < p.key_length;
-      const uint4 raw = valid ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
-                              : make_uint4(0, 0, 0, 0);
+  for (int j = 0; j < kKeys; ++j) {
+    const int row = kb * kKeyBlock + key0 + j;
+    raw[j] = row < p.key_length ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
+                                : make_uint4(0, 0, 0, 0);
+  }
+  Divisor divisor[8];  // this lane's 8 channels
+#pragma unroll
+  for (int i = 0; i < 8; ++i) divisor[i] = Divisor(p.value_scale[static_cast<long>(bh) * D + group * 8 + i]);
+  uint32_t packed[8][kKeys / 4];  // [column][four keys]
+#pragma unroll
+  for (int j4 = 0; j4 < kKeys / 4; ++j4) {
+    float q[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
       float f[8];
-      widen8<kBf16>(raw, f);
+      widen8<kBf16>(raw[4 * j4 + u], f);
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        const uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(
-            divisor[i].quotient(f[i]), divisor[i + 1].quotient(f[i + 1]), 0, false));
-        lds[(group * 8 + i) * kVStride + key_in_tile] = static_cast<uint8_t>(w);
-        lds[(group * 8 + i + 1) * kVStride + key_in_tile] = static_cast<uint8_t>(w >> 8);
-      }
+      for (int i = 0; i < 8; ++i) q[u][i] = divisor[i].quotient(f[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0][i], q[1][i], 0, false);
+      packed[i][j4] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(q[2][i], q[3][i], lo, true));
     }
   }
-  __syncthreads();
-  if (!active) return;
-  // transposed rows: lane owns features d = lane, lane + 64, ...
   uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * sage_tile_bytes(D);
-  for (int d = lane; d < D; d += kWave) {
-    const uint4* src = reinterpret_cast<const uint4*>(lds + d * kVStride);
-    uint4* dst = reinterpret_cast<uint4*>(tile + sage_v_offset(D) + d * kv_v_stride());
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[j] = src[j];
+  for (int i = 0; i < 8; ++i) {
+    uint8_t* dst = tile + sage_v_offset(D) + (group * 8 + i) * kv_v_stride() + key0;
+    if constexpr (kKeys == 16)
+      *reinterpret_cast<uint4*>(dst) = make_uint4(packed[i][0], packed[i][1], packed[i][2], packed[i][3]);
+    else
+      *reinterpret_cast<uint2*>(dst) = make_uint2(packed[i][0], packed[i][1]);
   }
 }
 
