@@ -45,8 +45,8 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
   // the V statistic of SageAttention2++ is max |v| (exact in any order); otherwise a sum
   const bool absmax = tensor == 1 && p.value_absmax;
   int row = row0;
-  constexpr int kInFlight = 16;
-  for (; row + kInFlight <= row1; row += kInFlight) {  // 16 loads in flight, adds still in row order
+  constexpr int kInFlight = 8;
+  for (; row + kInFlight <= row1; row += kInFlight) {  // 8 loads in flight, adds still in row order
     uint4 raw[kInFlight];
 #pragma unroll
     for (int u = 0; u < kInFlight; ++u)
@@ -245,6 +245,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
   float* meta = reinterpret_cast<float*>(tile + kv_log_offset(D));
   uint32_t packed[8][kKeys / 4];  // [column][four keys]
   int colsum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float own_scale = 0.0f;  // the scale of key key0 + group (lane group < kKeys), for the metadata
 #pragma unroll
   for (int j4 = 0; j4 < kKeys / 4; ++j4) {
     uint32_t word[4][8];
@@ -266,11 +267,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
       const Divisor divisor(scale);
 #pragma unroll
       for (int i = 0; i < 8; ++i) word[u][i] = code_word(f[i], divisor);
-      if (group == 0) {
-        p.value_scale[static_cast<long>(bh) * p.sk64 + row] = valid ? scale : 0.0f;
-        meta[key0 + j] = valid ? log2f(scale) : -__builtin_inff();
-        meta[kKeyBlock + key0 + j] = valid ? 1.0f / (255.0f * scale) : 0.0f;
-      }
+      if (group == j) own_scale = scale;
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -285,6 +282,14 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
       *reinterpret_cast<uint4*>(dst) = make_uint4(packed[i][0], packed[i][1], packed[i][2], packed[i][3]);
     else
       *reinterpret_cast<uint2*>(dst) = make_uint2(packed[i][0], packed[i][1]);
+  }
+  // per-key metadata, one key per lane: lane (group, sub) with group < kKeys owns key key0 + group
+  if (group < kKeys) {
+    const int row = kb * kKeyBlock + key0 + group;
+    const bool valid = row < p.key_length;
+    p.value_scale[static_cast<long>(bh) * p.sk64 + row] = valid ? own_scale : 0.0f;
+    meta[key0 + group] = valid ? log2f(own_scale) : -__builtin_inff();
+    meta[kKeyBlock + key0 + group] = valid ? 1.0f / (255.0f * own_scale) : 0.0f;
   }
   // column sums over the tile's 64 keys: the kSubs lanes sharing a group hold disjoint keys
 #pragma unroll
