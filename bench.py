@@ -14,7 +14,9 @@ kernel (the fused attention kernel) against MI355X's dense INT8 MFMA peak, with 
 average duration measured by HIP events recorded on the launch stream inside the timed
 region.  ``mfma_peak_measured`` is the sustained dense INT8 and FP8 MFMA rate of the same GPU
 (the library's back-to-back MFMA probe, results checked), and ``attention_kernel`` also
-reports the kernel's fraction of that measured INT8 rate.  ``cpu_baseline`` times the CPU
+reports the kernel's fraction of that measured INT8 rate.  ``mfma_valu_sharing`` times the same
+probe's MFMA-only, FP32-FMA-only and interleaved kinds at the kernel's occupancy (two waves per
+SIMD): how much MFMA execution and VALU issue overlap on this GPU.  ``cpu_baseline`` times the CPU
 oracle (a numpy restatement of the reference's portable path) on a bounded slice of the same
 workload, on one host thread.
 
@@ -262,6 +264,11 @@ def main() -> int:
         "fp8": measure_mfma_peak(native.MFMA_PROBE_F8, device),
     }
     result["mfma_peak_measured"] = measured
+    # how MFMA execution and VALU issue share a SIMD at the attention kernels' occupancy
+    from piper_kernels.measure import measure_mfma_valu_sharing
+
+    log("[bench] MFMA/VALU sharing probe")
+    result["mfma_valu_sharing"] = measure_mfma_valu_sharing(device)
     result["attention_kernel"]["percent_of_measured_int8_peak"] = round(100 * attn_tops / measured["int8"]["tops"], 2)
     if not args.no_cpu_baseline and not sage:
         log("[bench] cpu baseline")

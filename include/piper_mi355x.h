@@ -288,8 +288,21 @@ int piper_sage_attention_forward(const piper_sage_attention_args* args, void* st
  * bits of iterations * 4096 for PIPER_MFMA_PROBE_F8 (exact for iterations <= 4096). */
 #define PIPER_MFMA_PROBE_I8 0 /* v_mfma_i32_32x32x32_i8 */
 #define PIPER_MFMA_PROBE_F8 1 /* v_mfma_f32_32x32x64_f8f6f4 on FP8 E4M3 */
+/* How MFMA execution and VALU issue share a SIMD: kind VALU issues 64 FP32 FMAs per round
+ * (16 chains f = f * 1 + 1) and no MFMA, storing the FP32 bits of 64 * iterations (exact for
+ * iterations <= 2^18); kind I8_VALU issues the INT8 kind's 4 MFMAs per round with 16 of those
+ * FMAs after each, storing iterations * 2112 modulo 2^32.  Launched with one workgroup per
+ * compute unit (two waves per SIMD, like the attention kernels), t(I8_VALU) lies between
+ * max(t(I8), t(VALU)) (full overlap) and t(I8) + t(VALU) (serialised). */
+#define PIPER_MFMA_PROBE_VALU 2
+#define PIPER_MFMA_PROBE_I8_VALU 3
+/* Issue rates of two more VALU classes, 64 per round on 16 chains and no MFMA: v_max3_f32
+ * (f = max(f, 1, 0) from 1; stores the FP32 bits of 16.0) and v_exp_f32 (f = 2^-f from 0,
+ * which converges to 0.641186; stores the FP32 bits of the 16-chain sum). */
+#define PIPER_MFMA_PROBE_MAX3 4
+#define PIPER_MFMA_PROBE_EXP 5
 #define PIPER_MFMA_PROBE_THREADS 512
-#define PIPER_MFMA_PROBE_OPS(kind) ((kind) == PIPER_MFMA_PROBE_I8 ? 65536 : 131072)
+#define PIPER_MFMA_PROBE_OPS(kind) ((kind) == PIPER_MFMA_PROBE_F8 ? 131072 : 65536)
 int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream);
 
 /* Thread-local description of the last failure on this thread ("" if none). */

@@ -9,6 +9,18 @@
 // then stores the 32-bit sum of its 64 accumulator registers to sink[global thread index]:
 // iterations * 2048 (INT8, modulo 2^32) or iterations * 4096 (FP8, as FP32 bits), a value a
 // caller can check so that a fast time cannot come from work the compiler removed.
+//
+// Two more kinds measure how MFMA execution and VALU issue share a SIMD.  Kind 2 runs 64
+// FP32 FMAs per round (16 independent chains f = f * 1 + 1, every result an exact integer)
+// and no MFMA; kind 3 runs the INT8 kind's four MFMAs per round with 16 of those FMAs issued
+// after each one (scheduling barriers keep the interleave).  Launched like the attention
+// kernel (one 8-wave workgroup per compute unit, two waves per SIMD), the three times give
+// t(MFMA), t(VALU) and t(both): t(both) = max of the two if the units overlap, their sum if
+// they serialise.  Kind 2 stores the FP32 bits of 64 * iterations; kind 3 stores
+// iterations * 2048 + 64 * iterations modulo 2^32.  Kinds 4 and 5 time two other instruction
+// classes the same way (64 per round on 16 chains): v_max3_f32 (f = max(f, 1, 0), which stays 1;
+// stores the bits of 16.0) and v_exp_f32 (f = 2^-f from 0, which converges to the root of
+// x = 2^-x, 0.641186; stores the bits of the 16-chain sum).
 #include "common.h"
 #include "kernels.h"
 
@@ -34,6 +46,60 @@ __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* 
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) total += static_cast<uint32_t>(acc[c][r]);
+  } else if constexpr (kKind == 4 || kKind == 5) {
+    // instruction-class issue rates: 64 v_max3_f32 (kind 4) or v_exp_f32 (kind 5) per round
+    float one = 1.0f, zero = 0.0f;
+    asm volatile("" : "+v"(one), "+v"(zero));
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] = kKind == 4 ? 1.0f : 0.0f;
+    for (int it = 0; it < iterations; ++it) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if constexpr (kKind == 4) f[i] = fmaxf(fmaxf(f[i], one), zero);  // stays 1
+          else f[i] = __builtin_amdgcn_exp2f(-f[i]);  // converges to the root of x = 2^-x
+        }
+      }
+    }
+    float fsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) fsum += f[i];
+    total = __builtin_bit_cast(uint32_t, fsum);
+  } else if constexpr (kKind == 2 || kKind == 3) {
+    v4i a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    asm volatile("" : "+v"(a));
+    float one = 1.0f, addend = 1.0f;  // two registers: an FMA reading one VGPR twice issues slower
+    asm volatile("" : "+v"(one), "+v"(addend));  // opaque: the FMAs cannot be folded
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] = 0.0f;
+    v16i acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = v16i{};
+    for (int it = 0; it < iterations; ++it) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if constexpr (kKind == 3) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, acc[c], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) f[i] = fmaf(f[i], one, addend);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    float fsum = 0.0f;  // 16 chains of 4 * iterations: exact while 64 * iterations < 2^24
+#pragma unroll
+    for (int i = 0; i < 16; ++i) fsum += f[i];
+    if constexpr (kKind == 2) {
+      total = __builtin_bit_cast(uint32_t, fsum);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) total += static_cast<uint32_t>(acc[c][r]);
+      total += static_cast<uint32_t>(fsum);
+    }
   } else {
     v8i a = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
     asm volatile("" : "+v"(a));
@@ -58,10 +124,14 @@ __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* 
 hipError_t launch_mfma_probe(int kind, int workgroups, int iterations, uint32_t* sink, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(workgroups));
   const dim3 block(kProbeThreads);
-  if (kind == 0)
-    hipLaunchKernelGGL(mfma_probe_kernel<0>, grid, block, 0, stream, sink, iterations);
-  else
-    hipLaunchKernelGGL(mfma_probe_kernel<1>, grid, block, 0, stream, sink, iterations);
+  switch (kind) {
+    case 0: hipLaunchKernelGGL(mfma_probe_kernel<0>, grid, block, 0, stream, sink, iterations); break;
+    case 1: hipLaunchKernelGGL(mfma_probe_kernel<1>, grid, block, 0, stream, sink, iterations); break;
+    case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, grid, block, 0, stream, sink, iterations); break;
+    case 3: hipLaunchKernelGGL(mfma_probe_kernel<3>, grid, block, 0, stream, sink, iterations); break;
+    case 4: hipLaunchKernelGGL(mfma_probe_kernel<4>, grid, block, 0, stream, sink, iterations); break;
+    default: hipLaunchKernelGGL(mfma_probe_kernel<5>, grid, block, 0, stream, sink, iterations); break;
+  }
   return hipGetLastError();
 }
 

@@ -10,7 +10,9 @@
 ``measure_mfma_peak`` has no counterpart in the reference (whose benchmarks quote published
 peaks only): it times the library's back-to-back MFMA probe to give the sustained dense
 matrix-core rate of the GPU at hand, which the attention kernels are priced against next to
-the published 5.0 P/s.
+the published 5.0 P/s.  ``measure_mfma_valu_sharing`` (no counterpart either) times the
+same probe's MFMA-only, FMA-only and interleaved kinds at the attention kernels' occupancy, to
+show how much MFMA execution and VALU issue overlap on a SIMD.
 """
 
 from __future__ import annotations
@@ -147,11 +149,60 @@ def mfma_probe_expected(kind: int, iterations: int) -> int:
     ``iterations * K`` with all-ones operands (K = 32 INT8, 64 FP8); FP8 as FP32 bits."""
     from ._hip import library as native
 
-    if kind == native.MFMA_PROBE_I8:
-        return (iterations * 2048) % (1 << 32)
     import struct
 
+    if kind == native.MFMA_PROBE_I8:
+        return (iterations * 2048) % (1 << 32)
+    if kind == native.MFMA_PROBE_VALU:  # 16 FMA chains of 4 * iterations increments of 1.0
+        return struct.unpack("<I", struct.pack("<f", float(iterations * 64)))[0]
+    if kind == native.MFMA_PROBE_I8_VALU:
+        return (iterations * 2048 + iterations * 64) % (1 << 32)
+    if kind == native.MFMA_PROBE_MAX3:  # 16 chains that stay at 1.0
+        return struct.unpack("<I", struct.pack("<f", 16.0))[0]
+    if kind == native.MFMA_PROBE_EXP:
+        raise ValueError("the exp probe converges to an irrational value: check it with exp_probe_ok")
     return struct.unpack("<I", struct.pack("<f", float(iterations * 4096)))[0]
+
+
+EXP_PROBE_FIXED_POINT = 0.6411857445049859  # the root of x = 2^-x
+
+
+def exp_probe_ok(words) -> bool:
+    """Every thread of the exp probe converged to the same 16-chain sum, 16 * the root of
+    x = 2^-x to within v_exp_f32's accuracy."""
+    import numpy as np
+
+    values = np.asarray(words, dtype=np.uint32).view(np.float32)
+    return bool((values == values[0]).all() and abs(float(values[0]) - 16 * EXP_PROBE_FIXED_POINT) < 1e-4)
+
+
+def _time_probe(lib, kind: int, workgroups: int, iterations: int, launches: int, device: torch.device) -> float:
+    """Median milliseconds of ``launches`` probe launches (after two warm-ups); the result
+    words are checked against their exact value."""
+    from ._hip import library as native
+
+    sink = torch.zeros(workgroups * native.MFMA_PROBE_THREADS, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device)
+    with torch.cuda.device(device):
+        for _ in range(2):
+            lib.mfma_probe(kind, workgroups, iterations, sink.data_ptr(), stream.cuda_stream)
+        times = []
+        for _ in range(launches):
+            begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            begin.record(stream)
+            lib.mfma_probe(kind, workgroups, iterations, sink.data_ptr(), stream.cuda_stream)
+            end.record(stream)
+            end.synchronize()
+            times.append(begin.elapsed_time(end))
+    words = sink.cpu().numpy().view("uint32")
+    if kind == native.MFMA_PROBE_EXP:
+        if not exp_probe_ok(words):
+            raise RuntimeError("MFMA probe kind exp returned wrong results")
+    else:
+        expected = mfma_probe_expected(kind, iterations)
+        if not (words == expected).all():
+            raise RuntimeError(f"MFMA probe kind {kind} returned wrong results ({int((words != expected).sum())} threads)")
+    return sorted(times)[len(times) // 2]
 
 
 def measure_mfma_peak(kind: int, device: torch.device, *, iterations: int = 4096, launches: int = 5) -> dict:
@@ -166,24 +217,7 @@ def measure_mfma_peak(kind: int, device: torch.device, *, iterations: int = 4096
 
     lib = native.load_library()
     workgroups = 4 * torch.cuda.get_device_properties(device).multi_processor_count
-    sink = torch.zeros(workgroups * native.MFMA_PROBE_THREADS, dtype=torch.int32, device=device)
-    stream = torch.cuda.current_stream(device)
-    with torch.cuda.device(device):
-        for _ in range(2):
-            lib.mfma_probe(kind, workgroups, iterations, sink.data_ptr(), stream.cuda_stream)
-        times = []
-        for _ in range(launches):
-            begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            begin.record(stream)
-            lib.mfma_probe(kind, workgroups, iterations, sink.data_ptr(), stream.cuda_stream)
-            end.record(stream)
-            end.synchronize()
-            times.append(begin.elapsed_time(end))
-    expected = mfma_probe_expected(kind, iterations)
-    words = sink.cpu().numpy().view("uint32")
-    if not (words == expected).all():
-        raise RuntimeError(f"MFMA probe kind {kind} returned wrong results ({int((words != expected).sum())} threads)")
-    ms = sorted(times)[len(times) // 2]
+    ms = _time_probe(lib, kind, workgroups, iterations, launches, device)
     ops = workgroups * (native.MFMA_PROBE_THREADS // 64) * 4 * iterations * native.MFMA_PROBE_OPS[kind]
     return {
         "instruction": "v_mfma_i32_32x32x32_i8" if kind == native.MFMA_PROBE_I8 else "v_mfma_f32_32x32x64_f8f6f4",
@@ -191,4 +225,44 @@ def measure_mfma_peak(kind: int, device: torch.device, *, iterations: int = 4096
         "ms_per_launch": round(ms, 4),
         "workgroups": workgroups,
         "iterations": iterations,
+    }
+
+
+def measure_mfma_valu_sharing(device: torch.device, *, iterations: int = 2048, launches: int = 5) -> dict:
+    """How INT8 MFMA execution and FP32 VALU issue share a SIMD at the attention kernels'
+    occupancy (one 8-wave workgroup per compute unit: two waves per SIMD).
+
+    Times the probe's MFMA-only, FMA-only and interleaved kinds (4 MFMAs and 64 FMAs per
+    wave-round).  ``overlap`` = (t_mfma + t_valu - t_both) / min(t_mfma, t_valu): 1 when the
+    units run concurrently, 0 when MFMA execution and VALU issue serialise.  The cycle figures
+    convert per-SIMD time at the 2.4 GHz peak clock: per MFMA, per FMA (two waves issuing), and
+    the VALU cycles one interleaved MFMA costs (its share of t_both - t_valu); and, from the
+    max3 and exp kinds, the per-SIMD cycles of a v_max3_f32 and a v_exp_f32 issued by two waves.
+    """
+    from ._hip import library as native
+
+    if iterations > 1 << 18:
+        raise ValueError("iterations must be <= 2^18 for the exact FMA check")
+    lib = native.load_library()
+    workgroups = torch.cuda.get_device_properties(device).multi_processor_count
+    kinds = (native.MFMA_PROBE_I8, native.MFMA_PROBE_VALU, native.MFMA_PROBE_I8_VALU, native.MFMA_PROBE_MAX3,
+             native.MFMA_PROBE_EXP)
+    t = {k: _time_probe(lib, k, workgroups, iterations, launches, device) for k in kinds}
+    t_m, t_v, t_b = t[native.MFMA_PROBE_I8], t[native.MFMA_PROBE_VALU], t[native.MFMA_PROBE_I8_VALU]
+    cycles = 2.4e9 * 1e-3  # cycles per millisecond at the peak clock
+    waves_per_simd = native.MFMA_PROBE_THREADS // 64 // 4
+    mfmas = waves_per_simd * 4 * iterations  # per SIMD
+    fmas = waves_per_simd * 64 * iterations
+    return {
+        "workgroups": workgroups,
+        "iterations": iterations,
+        "mfma_ms": round(t_m, 4),
+        "valu_ms": round(t_v, 4),
+        "both_ms": round(t_b, 4),
+        "overlap": round((t_m + t_v - t_b) / min(t_m, t_v), 3),
+        "cycles_per_mfma": round(t_m * cycles / mfmas, 1),
+        "cycles_per_fma": round(t_v * cycles / fmas, 2),
+        "cycles_per_max3": round(t[native.MFMA_PROBE_MAX3] * cycles / fmas, 2),
+        "cycles_per_exp": round(t[native.MFMA_PROBE_EXP] * cycles / fmas, 2),
+        "valu_cycles_per_interleaved_mfma": round((t_b - t_v) * cycles / mfmas, 1),
     }

@@ -262,21 +262,27 @@ def test_sage_attention_validates_before_launching(lib) -> None:
 def test_mfma_probe_constants_match_the_header(tmp_path) -> None:
     source = tmp_path / "probe.c"
     source.write_text('#include <stdio.h>\n#include "piper_mi355x.h"\nint main(void) {\n'
-                      '  printf("%d %d %d %d %d\\n", PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8, PIPER_MFMA_PROBE_THREADS,\n'
-                      '         PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8));\n'
+                      '  printf("%d %d %d %d %d %d %d\\n", PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8, PIPER_MFMA_PROBE_THREADS,\n'
+                      '         PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8),\n'
+                      '         PIPER_MFMA_PROBE_VALU, PIPER_MFMA_PROBE_I8_VALU);\n'
+                      '  printf("%d %d\\n", PIPER_MFMA_PROBE_MAX3, PIPER_MFMA_PROBE_EXP);\n'
                       '  return 0; }\n')
     exe = tmp_path / "probe"
     subprocess.run(["gcc", f"-I{REPO / 'include'}", str(source), "-o", str(exe)], check=True)
     values = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
     assert values == [native.MFMA_PROBE_I8, native.MFMA_PROBE_F8, native.MFMA_PROBE_THREADS,
-                      native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8]]
+                      native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8],
+                      native.MFMA_PROBE_VALU, native.MFMA_PROBE_I8_VALU, native.MFMA_PROBE_MAX3,
+                      native.MFMA_PROBE_EXP]
     # 32x32x32 INT8 and 32x32x64 FP8: two operations per multiply-add
     assert native.MFMA_PROBE_OPS == {native.MFMA_PROBE_I8: 2 * 32 * 32 * 32, native.MFMA_PROBE_F8: 2 * 32 * 32 * 64}
 
 
 def test_mfma_probe_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
-        lib.mfma_probe(2, 1, 1, 0x1000, 0)
+        lib.mfma_probe(6, 1, 1, 0x1000, 0)
+    with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
+        lib.mfma_probe(-1, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="workgroups and"):
         lib.mfma_probe(native.MFMA_PROBE_I8, 0, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="workgroups and"):
@@ -293,3 +299,25 @@ def test_mfma_probe_expected_words() -> None:
     assert mfma_probe_expected(native.MFMA_PROBE_I8, 4096) == 4096 * 64 * 32
     assert mfma_probe_expected(native.MFMA_PROBE_I8, 1 << 21) == (64 * 32 << 21) % (1 << 32)
     assert mfma_probe_expected(native.MFMA_PROBE_F8, 4096) == 0x4B800000  # 2^24 as FP32
+    # 16 FMA chains, each 4 * iterations increments of 1.0: 64 * 2048 = 2^17 as FP32
+    assert mfma_probe_expected(native.MFMA_PROBE_VALU, 2048) == 0x48000000
+    assert mfma_probe_expected(native.MFMA_PROBE_I8_VALU, 2048) == 2048 * 2048 + 64 * 2048
+    assert mfma_probe_expected(native.MFMA_PROBE_MAX3, 7) == 0x41800000  # 16.0
+
+
+def test_exp_probe_check() -> None:
+    import math
+
+    import numpy as np
+    from piper_kernels.measure import EXP_PROBE_FIXED_POINT, exp_probe_ok
+
+    assert abs(EXP_PROBE_FIXED_POINT - 2.0 ** -EXP_PROBE_FIXED_POINT) < 1e-15
+    x = 0.0  # the chain the probe runs, in float32 with a correctly rounded 2^-x
+    for _ in range(64):
+        x = float(np.float32(math.pow(2.0, -x)))
+    good = np.full(8, np.float32(16 * x)).view(np.uint32)
+    assert exp_probe_ok(good)
+    bad = good.copy()
+    bad[3] ^= 1
+    assert not exp_probe_ok(bad)
+    assert not exp_probe_ok(np.full(8, np.float32(16.0)).view(np.uint32))
