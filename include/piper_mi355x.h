@@ -53,8 +53,6 @@ extern "C" {
 /* Rows per quantisation group (sage/reference.py:6-7) and keys per P block (reference.py:16). */
 #define PIPER_QUERY_BLOCK 32
 #define PIPER_KEY_BLOCK 64
-/* Rows per FP64 partial sum of the order-defined K/V sequence mean. */
-#define PIPER_MEAN_CHUNK 64
 
 typedef enum piper_dtype {
   PIPER_FLOAT16 = 0,
@@ -139,7 +137,9 @@ typedef struct piper_layout {
   int64_t mean_bytes; /* each of key_mean, value_mean */
   int64_t kv_tile_bytes; /* one tile record */
   int64_t kv_tiles_bytes; /* all tile records */
-  int64_t workspace_bytes; /* scratch for piper_prepare (FP64 mean partials) */
+  int64_t workspace_bytes; /* scratch for piper_prepare: FP32 partial sums of the K/V means
+                              (torch's CPU summation order, so the means and every K/V code
+                              equal the reference's torch.mean(dim=2) path bit for bit) */
 } piper_layout;
 
 /* piper_prepare_args.flags */

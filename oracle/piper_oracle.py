@@ -13,19 +13,16 @@ It restates, in numpy, the portable PyTorch reference of
 * ``src/piper_kernels/attention/kernels/qk_quantization/int8/sage/reference.py:13-108``
   (K smoothing and INT8 Q/K quantisation, ``per_thread`` and ``per_warp``).
 
-One deliberate, documented deviation: the sequence means of K and V.  The
-reference uses ``torch.mean`` in FP32 (``reference.py:50``,
-``sage/reference.py:89``) whose summation order is internal to torch and not
-reproducible on a GPU.  This oracle pins an order-defined mean instead
-(:func:`sequence_mean`), which the HIP prep kernel reproduces bit for bit.
-For FP16 inputs this definition equals the correctly rounded exact mean
-whenever ``S * max|x| < 2**29`` (every FP16 value is a multiple of 2**-24, so
-every FP64 partial sum is exact).
+The sequence means of K and V (``reference.py:50``, ``sage/reference.py:89``:
+FP32 ``torch.mean(dim=2)`` on CPU) are restated with torch's own summation
+order (:func:`sequence_mean`): the FP32 cascade sum of torch's CPU reduction
+kernel, then one FP32 division by S.  The HIP prep kernels compute the same
+order, so K and V codes are bit-exact with the reference's portable path.
 
 Parity status of each function (how it is pinned; see tests/test_oracle.py):
 
-* ``sequence_mean`` -- pinned against exact rational arithmetic
-  (``fractions.Fraction``) on FP16 inputs.
+* ``sequence_mean`` -- pinned bit for bit against ``torch.mean(dim=2)`` on
+  CPU (the reference's own call) over lengths, layouts and thread counts.
 * ``quantize_per_group`` / ``quantize_*_per_thread`` / ``quantize_value_per_key``
   -- pinned by a pure-Python IEEE re-derivation on small inputs, the
   reference's own dequantisation bound (``tests/attention/test_qk_quantization.py:26-33``)
@@ -45,7 +42,7 @@ import numpy as np
 QUERY_BLOCK = 32  # sage/reference.py:6
 KEY_BLOCK = 64  # sage/reference.py:7
 PV_BLOCK = 64  # reference.py:16
-MEAN_CHUNK = 64  # rows per FP64 partial sum in the pinned mean definition
+MEAN_LEVELS = 4  # cascade levels of torch's CPU sum
 INT8_RANGE = np.float32(127.0)  # sage/reference.py quantization_range / reference.py:18
 P_UINT8_RANGE = np.float32(255.0)  # reference.py:17
 SCALE_EPSILON = np.float32(1e-7)  # reference.py:19, sage/reference.py:8
@@ -91,29 +88,56 @@ def cast_output(out32: np.ndarray, dtype: str) -> np.ndarray:
 
 
 # --------------------------------------------------------------------------------------
-# sequence mean (pinned definition)
+# sequence mean (torch's CPU FP32 order)
 # --------------------------------------------------------------------------------------
-def sequence_mean(x32: np.ndarray, chunk: int = MEAN_CHUNK) -> np.ndarray:
-    """Mean over the sequence axis of ``[B, H, S, D]`` float32 data, order-defined.
+def cascade_block_rows(length: int) -> int:
+    """Rows per first-level block of torch's cascade sum over ``length`` rows: 2**p with
+    p = max(4, ceil(log2(length)) // 4) (16 for every length up to 2**19)."""
+    ceil_log2 = (length - 1).bit_length() if length > 1 else 0
+    return 1 << max(4, ceil_log2 // MEAN_LEVELS)
 
-    Definition (the HIP prep kernel computes exactly this):
 
-    1. the S rows are cut into chunks of ``chunk`` consecutive rows (the last may be short);
-    2. each chunk's FP64 partial starts at +0.0 and adds its rows in increasing order;
-    3. the total starts at +0.0 and adds the chunk partials in increasing chunk order;
-    4. ``mean = float32(total / S)`` with the division in FP64 (both roundings are to
-       nearest even).
+def cascade_sum(x32: np.ndarray) -> np.ndarray:
+    """FP32 sum over axis 2 of ``[B, H, S, D]`` data in the order of torch's CPU reduction.
 
-    Replaces the FP32 ``mean(dim=2)`` of ``reference.py:50`` and ``sage/reference.py:89``.
+    Four accumulators start at +0.0.  Rows are added in order to level 0; after every block
+    of L rows (L = :func:`cascade_block_rows`) level 0 is added to level 1 and cleared, and
+    the carry continues upward -- level 1 into level 2 when the row count is a multiple of
+    L**2, level 2 into level 3 when it is a multiple of L**3.  Trailing rows stay in level 0,
+    and the result is ((level0 + level1) + level2) + level3.  Every addition rounds to FP32.
     """
     batch, heads, length, width = x32.shape
-    total = np.zeros((batch, heads, width), dtype=np.float64)
-    for start in range(0, length, chunk):
-        partial = np.zeros((batch, heads, width), dtype=np.float64)
-        for row in range(start, min(start + chunk, length)):
-            partial += x32[:, :, row, :].astype(np.float64)
-        total += partial
-    return (total / np.float64(length)).astype(np.float32)
+    step = cascade_block_rows(length)
+    power = step.bit_length() - 1
+    mask = step - 1
+    acc = [np.zeros((batch, heads, width), dtype=np.float32) for _ in range(MEAN_LEVELS)]
+    i = 0
+    while i + step <= length:
+        for _ in range(step):
+            acc[0] = acc[0] + x32[:, :, i, :]
+            i += 1
+        for j in range(1, MEAN_LEVELS):
+            acc[j] = acc[j] + acc[j - 1]
+            acc[j - 1] = np.zeros_like(acc[j - 1])
+            if i & (mask << (j * power)):
+                break
+    while i < length:
+        acc[0] = acc[0] + x32[:, :, i, :]
+        i += 1
+    for j in range(1, MEAN_LEVELS):
+        acc[0] = acc[0] + acc[j]
+    return acc[0]
+
+
+def sequence_mean(x32: np.ndarray) -> np.ndarray:
+    """Mean over the sequence axis of ``[B, H, S, D]`` float32 data: :func:`cascade_sum`
+    divided by S in FP32 (round to nearest even), which is what ``torch.mean(dim=2)`` returns
+    on CPU for float32 input (``reference.py:50``, ``sage/reference.py:89``) when D is a
+    multiple of 32 -- every head dim the operator accepts.  (torch's vectorised kernel takes
+    columns in groups of 32 or 64 floats; a narrower remainder of columns is summed in another
+    order, which this restatement does not model.)"""
+    x32 = np.asarray(x32, dtype=np.float32)
+    return (cascade_sum(x32) / np.float32(x32.shape[2])).astype(np.float32)
 
 
 # --------------------------------------------------------------------------------------

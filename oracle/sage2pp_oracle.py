@@ -18,8 +18,8 @@ It restates the portable PyTorch reference of ``jumbledpoophj/piper-kernels`` 0.
   in FP8's range, FP8 probabilities, and 64-key partial products rounded to FP16
   (``reference.py:58-104``).
 
-The K mean uses the order-defined definition of :func:`oracle.piper_oracle.sequence_mean`
-(the one documented deviation, shared with Piper Attention).
+The K mean is :func:`oracle.piper_oracle.sequence_mean`, torch's CPU FP32 summation order
+(the reference's ``key_float.mean(dim=2)``), shared with Piper Attention.
 
 ``accumulate="fp32"`` restates the MI355X kernel's arithmetic instead of the reference's
 FP16 partials: gfx950's FP8 MFMA accumulates in FP32, so the kernel keeps one FP32

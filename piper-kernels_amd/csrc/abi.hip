@@ -147,7 +147,7 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
   const int64_t d = shape->head_dim;
   const int64_t sq32 = ceil_div(shape->query_length, PIPER_QUERY_BLOCK) * PIPER_QUERY_BLOCK;
   const int64_t sk64 = ceil_div(shape->key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK;
-  const int64_t chunks = ceil_div(shape->key_length, PIPER_MEAN_CHUNK);
+  const int64_t chunks = piper::cascade_chunks(static_cast<int>(shape->key_length));
   layout->query_code_bytes = bh * sq32 * d;
   layout->query_scale_bytes = bh * (sq32 / PIPER_QUERY_BLOCK) * 4;
   layout->key_scale_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * 4;
@@ -155,7 +155,7 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
   layout->mean_bytes = bh * d * 4;
   layout->kv_tile_bytes = PIPER_KV_TILE_BYTES(d);
   layout->kv_tiles_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * PIPER_KV_TILE_BYTES(d);
-  layout->workspace_bytes = 2 * bh * chunks * d * 8;
+  layout->workspace_bytes = 2 * bh * (chunks + 1) * d * 4;
   g_last_error[0] = '\0';
   return PIPER_OK;
 }
@@ -197,13 +197,14 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   piper::MeanParams mp{};
   mp.key = to_input(a->key);
   mp.value = to_input(a->value);
-  mp.partials = static_cast<double*>(a->workspace);
+  mp.partials = static_cast<float*>(a->workspace);
   mp.key_mean = o.key_mean;
   mp.value_mean = o.value_mean;
   mp.batch_heads = bh;
   mp.heads = static_cast<int>(s.heads);
   mp.length = static_cast<int>(s.key_length);
-  mp.chunks = static_cast<int>(ceil_div(s.key_length, PIPER_MEAN_CHUNK));
+  mp.block_rows = piper::cascade_block_rows(static_cast<int>(s.key_length));
+  mp.chunks = piper::cascade_chunks(static_cast<int>(s.key_length));
   mp.tensors = a->is_causal ? 1 : 2;
 
   piper::QuantParams qp{};
@@ -254,12 +255,12 @@ int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layo
   const int64_t bh = shape->batch * shape->heads;
   const int64_t d = shape->head_dim;
   const int64_t nkb = ceil_div(shape->key_length, PIPER_KEY_BLOCK);
-  const int64_t chunks = ceil_div(shape->key_length, PIPER_MEAN_CHUNK);
+  const int64_t chunks = piper::cascade_chunks(static_cast<int>(shape->key_length));
   layout->key_scale_bytes = bh * nkb * 4;
   layout->mean_bytes = bh * d * 4;
   layout->kv_tile_bytes = PIPER_SAGE_TILE_BYTES(d);
   layout->kv_tiles_bytes = bh * nkb * PIPER_SAGE_TILE_BYTES(d);
-  layout->workspace_bytes = 2 * bh * chunks * d * 8;
+  layout->workspace_bytes = 2 * bh * (chunks + 1) * d * 4;
   g_last_error[0] = '\0';
   return PIPER_OK;
 }
@@ -289,17 +290,18 @@ int piper_sage_prepare(const piper_sage_prepare_args* a, void* stream) {
   const int bh = static_cast<int>(s.batch * s.heads);
   const int nkb = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK));
 
-  // statistics: the K sum (the order-defined mean) and the per-column max |v|
+  // statistics: the K sum (torch's CPU order) and the per-column max |v|
   piper::MeanParams mp{};
   mp.key = to_input(a->key);
   mp.value = to_input(a->value);
-  mp.partials = static_cast<double*>(a->workspace);
+  mp.partials = static_cast<float*>(a->workspace);
   mp.key_mean = o.key_mean;
   mp.value_mean = nullptr;
   mp.batch_heads = bh;
   mp.heads = static_cast<int>(s.heads);
   mp.length = static_cast<int>(s.key_length);
-  mp.chunks = static_cast<int>(ceil_div(s.key_length, PIPER_MEAN_CHUNK));
+  mp.block_rows = piper::cascade_block_rows(static_cast<int>(s.key_length));
+  mp.chunks = piper::cascade_chunks(static_cast<int>(s.key_length));
   mp.tensors = 2;
   mp.value_absmax = 1;
   mp.value_scale = o.value_scale;

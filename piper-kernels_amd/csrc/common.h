@@ -12,7 +12,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kWave = 64;
 constexpr int kQueryBlock = 32;  // rows per Q scale (sage/reference.py:6)
 constexpr int kKeyBlock = 64;    // rows per K scale and keys per P block (reference.py:16)
-constexpr int kMeanChunk = 64;   // rows per FP64 partial of the order-defined mean
 constexpr float kLog2e = 1.4426950408889634f;
 // Integer accumulators that start from kAccBias read, as FP32 bits, 1.5 * 2^23 + value exactly
 // while |value| < 2^22: the FP32 mantissa at [2^23, 2^24) has unit spacing.  Subtracting

@@ -6,6 +6,26 @@
 
 namespace piper {
 
+constexpr int kMeanLevels = 4;  // accumulator levels of torch's CPU cascade sum
+
+// The K/V sequence means follow torch's CPU FP32 reduction order (the reference's
+// torch.mean(dim=2), piper_attention/reference.py:50, sage/reference.py:89): rows are summed in
+// blocks of L = cascade_block_rows(S) rows, L consecutive blocks form a level-1 sum over a
+// chunk of L^2 rows, L consecutive level-1 sums form a level-2 sum, and the level-2 sums are
+// added in order; trailing rows and unfinished levels are combined at the end as
+// ((rows + level 1) + level 2) + level 3.  Every partial starts from +0.0 and every addition
+// is one FP32 rounding; the mean is that sum divided by S in FP32.
+__host__ __device__ inline int cascade_block_rows(int length) {
+  const int ceil_log2 = length > 1 ? 32 - __builtin_clz(static_cast<unsigned>(length - 1)) : 0;
+  const int power = ceil_log2 / kMeanLevels > 4 ? ceil_log2 / kMeanLevels : 4;
+  return 1 << power;
+}
+
+__host__ __device__ inline int cascade_chunks(int length) {  // chunks of L^2 rows, the last may be short
+  const long rows = static_cast<long>(cascade_block_rows(length)) * cascade_block_rows(length);
+  return static_cast<int>((length + rows - 1) / rows);
+}
+
 // One 64-key tile record is byte for byte the attention kernel's LDS stage, so it is copied
 // with direct global -> LDS loads in 1 KiB pieces: K codes [64][D] in rows of D + 16 bytes,
 // V^T codes [D][64] in rows of 80 bytes (the 16 spare bytes per row spread LDS banks), 64
@@ -37,13 +57,17 @@ struct InputTensor {
 struct MeanParams {
   InputTensor key;
   InputTensor value;
-  double* partials;  // [tensors][batch_heads][chunks][D]
+  // [tensors][batch_heads][chunks + 1][D]: the level-1 sum of each chunk of L^2 rows (for a
+  // short last chunk, the sum of its complete L-row blocks), then the sum of the trailing
+  // length % L rows; SageAttention2++'s V slots hold per-chunk max |v| instead
+  float* partials;
   float* key_mean;   // [batch_heads][D]
   float* value_mean; // [batch_heads][D]
   int batch_heads;
   int heads;
   int length;  // key length
-  int chunks;  // ceil(length / 64)
+  int block_rows;  // L = cascade_block_rows(length)
+  int chunks;      // cascade_chunks(length)
   int tensors; // 1 = K only (causal), 2 = K and V
   // 1: the V statistic is the per-column max of |v| (SageAttention2++), finalised into
   // value_scale = amax / 2.25 + 1e-7; 0: the V sum, finalised into value_mean

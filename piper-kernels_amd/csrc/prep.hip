@@ -6,9 +6,8 @@
 //   V centring (non-causal only) and per-key V codes   piper_attention/reference.py:22-59
 // Every code and scale is bit-exact with that arithmetic: scale = amax/127 + 1e-7 in FP32
 // (IEEE division, FP32 add), code = clamp(round_half_even(x / scale), -127, 127) with an IEEE
-// division per element.  The means use the order-defined FP64 definition documented in the
-// C header (chunks of 64 rows summed in order, chunk partials summed in order, FP64 divide,
-// round to FP32).
+// division per element.  The K/V means are the reference's FP32 torch.mean(dim=2) on CPU bit
+// for bit: its cascade summation order (common.h) and one FP32 division.
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"
@@ -16,68 +15,99 @@
 namespace piper {
 
 // ---------------------------------------------------------------------------------------
-// Means, pass 1: one thread owns 8 columns of one 64-row chunk of K (tensor 0) or V
-// (tensor 1) and adds the chunk's rows in order into FP64 accumulators that start at +0.0.
+// Means, pass 1: one thread owns a column pair of one chunk of L^2 rows of K (tensor 0) or V
+// (tensor 1).  It sums each L-row block in row order and the chunk's complete blocks in block
+// order (the first two cascade levels); the thread of the last chunk also sums the trailing
+// length % L rows.  SageAttention2++'s V statistic is the per-column max |v| instead (exact in
+// any order).
 // ---------------------------------------------------------------------------------------
+template <bool kBf16>
+__device__ __forceinline__ float2 widen_pair(uint32_t bits) {
+  if constexpr (kBf16) return make_float2(__uint_as_float(bits << 16), __uint_as_float(bits & 0xffff0000u));
+  return make_float2(half_bits_to_float(bits & 0xffffu), half_bits_to_float(bits >> 16));
+}
+
 template <bool kBf16, int D>
 __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
-  constexpr int kGroups = D / 8;  // 16-byte column groups per row
+  constexpr int kPairs = D / 2;
+  constexpr int kUnroll = 16;  // loads in flight; L is a power of two >= 16
   const long gid = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-  const long per_tensor = static_cast<long>(p.batch_heads) * p.chunks * kGroups;
+  const long per_tensor = static_cast<long>(p.batch_heads) * p.chunks * kPairs;
   if (gid >= per_tensor * p.tensors) return;
   const int tensor = static_cast<int>(gid / per_tensor);
   const long rem = gid - tensor * per_tensor;
-  const int group = static_cast<int>(rem % kGroups);
-  const int chunk = static_cast<int>((rem / kGroups) % p.chunks);
-  const int bh = static_cast<int>(rem / (static_cast<long>(kGroups) * p.chunks));
+  const int pair = static_cast<int>(rem % kPairs);
+  const int chunk = static_cast<int>((rem / kPairs) % p.chunks);
+  const int bh = static_cast<int>(rem / (static_cast<long>(kPairs) * p.chunks));
   const int b = bh / p.heads;
   const int h = bh - b * p.heads;
 
   const InputTensor& t = tensor == 0 ? p.key : p.value;
-  const uint16_t* base = static_cast<const uint16_t*>(t.data) + b * t.stride_batch +
-                         h * t.stride_head + group * 8;
-  const int row0 = chunk * kMeanChunk;
-  const int row1 = min(row0 + kMeanChunk, p.length);
-
-  double acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.0;
-  // the V statistic of SageAttention2++ is max |v| (exact in any order); otherwise a sum
+  // two adjacent 16-bit elements per 4-byte load (rows are 16-byte aligned, so the pair is too)
+  const uint16_t* base = static_cast<const uint16_t*>(t.data) + b * t.stride_batch + h * t.stride_head + 2 * pair;
+  const int block = p.block_rows;
+  const long chunk_rows = static_cast<long>(block) * block;
+  const int row0 = static_cast<int>(chunk * chunk_rows);
+  const int row1 = static_cast<int>(min(row0 + chunk_rows, static_cast<long>(p.length)));
+  const int blocks = (row1 - row0) / block;
   const bool absmax = tensor == 1 && p.value_absmax;
+
+  float s0 = 0.0f, s1 = 0.0f;  // level 1: complete blocks of this chunk, in order
   int row = row0;
-  constexpr int kInFlight = 8;
-  for (; row + kInFlight <= row1; row += kInFlight) {  // 8 loads in flight, adds still in row order
-    uint4 raw[kInFlight];
+  for (int blk = 0; blk < blocks; ++blk) {
+    float b0 = 0.0f, b1 = 0.0f;  // level 0: the block's rows, in order
+    for (int r = 0; r < block; r += kUnroll) {
+      uint32_t raw[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kInFlight; ++u)
-      raw[u] = *reinterpret_cast<const uint4*>(base + static_cast<long>(row + u) * t.stride_seq);
+      for (int u = 0; u < kUnroll; ++u)
+        raw[u] = *reinterpret_cast<const uint32_t*>(base + static_cast<long>(row + u) * t.stride_seq);
 #pragma unroll
-    for (int u = 0; u < kInFlight; ++u) {
-      float f[8];
-      widen8<kBf16>(raw[u], f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        acc[i] = absmax ? fmax(acc[i], static_cast<double>(fabsf(f[i]))) : acc[i] + static_cast<double>(f[i]);
+      for (int u = 0; u < kUnroll; ++u) {
+        const float2 f = widen_pair<kBf16>(raw[u]);
+        if (absmax) {
+          b0 = fmaxf(b0, fabsf(f.x));
+          b1 = fmaxf(b1, fabsf(f.y));
+        } else {
+          b0 += f.x;
+          b1 += f.y;
+        }
+      }
+      row += kUnroll;
+    }
+    if (absmax) {
+      s0 = fmaxf(s0, b0);
+      s1 = fmaxf(s1, b1);
+    } else {
+      s0 += b0;
+      s1 += b1;
     }
   }
-  for (; row < row1; ++row) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * t.stride_seq);
-    float f[8];
-    widen8<kBf16>(raw, f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      acc[i] = absmax ? fmax(acc[i], static_cast<double>(fabsf(f[i]))) : acc[i] + static_cast<double>(f[i]);
+  float* out = p.partials + ((static_cast<long>(tensor) * p.batch_heads + bh) * (p.chunks + 1) + chunk) * D + 2 * pair;
+  out[0] = s0;
+  out[1] = s1;
+  if (chunk == p.chunks - 1) {  // the trailing rows, summed in order from +0.0 (slot `chunks`)
+    float a0 = 0.0f, a1 = 0.0f;
+    for (; row < row1; ++row) {
+      const float2 f = widen_pair<kBf16>(*reinterpret_cast<const uint32_t*>(base + static_cast<long>(row) * t.stride_seq));
+      if (absmax) {
+        a0 = fmaxf(a0, fabsf(f.x));
+        a1 = fmaxf(a1, fabsf(f.y));
+      } else {
+        a0 += f.x;
+        a1 += f.y;
+      }
+    }
+    out[D] = a0;
+    out[D + 1] = a1;
   }
-  double* out = p.partials + ((static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks + chunk) * D +
-                group * 8;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = acc[i];
 }
 
-// Means, pass 2: sum the chunk partials of one (tensor, batch-head, column) in chunk order,
-// divide by the length in FP64 and round to FP32.  Causal calls write a zero V mean.
-// SageAttention2++ (value_absmax): the V column's max |v| over the chunks gives its FP8 scale
-// amax / 2.25 + 1e-7 (sage_attention_2pp/reference.py:22-23: FP32 division, FP32 add).
+// Means, pass 2, one thread per (tensor, batch-head, column): the complete chunks' level-1 sums
+// are added in groups of L (level 2), the group sums in order (level 3); then
+// ((trailing rows + short chunk's blocks) + unfinished level 2) + level 3, divided by the length
+// in FP32.  Causal calls write a zero V mean.  SageAttention2++ (value_absmax): the V column's
+// max |v| over the chunks gives its FP8 scale amax / 2.25 + 1e-7
+// (sage_attention_2pp/reference.py:22-23: FP32 division, FP32 add).
 __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, int head_dim) {
   const int gid = blockIdx.x * 64 + threadIdx.x;
   const int per_tensor = p.batch_heads * head_dim;
@@ -91,28 +121,43 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
   }
   const int bh = rem / head_dim;
   const int d = rem - bh * head_dim;
-  const double* src = p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * p.chunks * head_dim + d;
-  const bool absmax = tensor == 1 && p.value_absmax;
-  // 64 loads in flight per step; the additions stay in chunk order
-  constexpr int kBatch = 64;
-  double total = 0.0;
+  const float* src =
+      p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * (p.chunks + 1) * head_dim + d;
+  if (tensor == 1 && p.value_absmax) {
+    float amax = 0.0f;
+    for (int c = 0; c <= p.chunks; ++c) amax = fmaxf(amax, src[static_cast<long>(c) * head_dim]);
+    p.value_scale[rem] = __fadd_rn(amax / 2.25f, 1e-7f);
+    return;
+  }
+  const int block = p.block_rows;
+  const int full = static_cast<int>(p.length / (static_cast<long>(block) * block));  // complete chunks
+  float level2 = 0.0f, level3 = 0.0f;
+  constexpr int kBatch = 16;  // loads in flight; the additions stay in chunk order
   int c = 0;
-  for (; c + kBatch <= p.chunks; c += kBatch) {
-    double part[kBatch];
+  for (; c + kBatch <= full; c += kBatch) {
+    float part[kBatch];
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) part[i] = src[static_cast<long>(c + i) * head_dim];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) total = absmax ? fmax(total, part[i]) : total + part[i];
+    for (int i = 0; i < kBatch; ++i) {
+      level2 += part[i];
+      if ((c + i + 1) % block == 0) {
+        level3 += level2;
+        level2 = 0.0f;
+      }
+    }
   }
-  for (; c < p.chunks; ++c) {
-    const double part = src[static_cast<long>(c) * head_dim];
-    total = absmax ? fmax(total, part) : total + part;
+  for (; c < full; ++c) {
+    level2 += src[static_cast<long>(c) * head_dim];
+    if ((c + 1) % block == 0) {
+      level3 += level2;
+      level2 = 0.0f;
+    }
   }
-  if (absmax) {
-    p.value_scale[rem] = __fadd_rn(static_cast<float>(total) / 2.25f, 1e-7f);
-    return;
-  }
-  dst[rem] = static_cast<float>(total / static_cast<double>(p.length));
+  const float level1 = full < p.chunks ? src[static_cast<long>(full) * head_dim] : 0.0f;
+  const float level0 = src[static_cast<long>(p.chunks) * head_dim];
+  const float total = ((level0 + level1) + level2) + level3;
+  dst[rem] = total / static_cast<float>(p.length);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -391,7 +436,7 @@ __global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParam
 // ---------------------------------------------------------------------------------------
 template <bool kBf16, int D>
 static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {
-  const long mean_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 8) * mp.tensors;
+  const long mean_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 2) * mp.tensors;
   hipLaunchKernelGGL((mean_partial_kernel<kBf16, D>), dim3(static_cast<unsigned>((mean_threads + 255) / 256)),
                      dim3(256), 0, stream, mp);
   hipError_t err = hipGetLastError();
@@ -407,7 +452,7 @@ static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp,
 
 template <bool kBf16, int D>
 static hipError_t launch_sage_prep_typed(const MeanParams& mp, const SageQuantParams& qp, hipStream_t stream) {
-  const long stat_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 8) * mp.tensors;
+  const long stat_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 2) * mp.tensors;
   hipLaunchKernelGGL((mean_partial_kernel<kBf16, D>), dim3(static_cast<unsigned>((stat_threads + 255) / 256)),
                      dim3(256), 0, stream, mp);
   hipError_t err = hipGetLastError();

@@ -19,7 +19,6 @@ from .build import LIBRARY_PATH
 ABI_VERSION = 1
 QUERY_BLOCK = 32
 KEY_BLOCK = 64
-MEAN_CHUNK = 64
 
 FLOAT16 = 0
 BFLOAT16 = 1

@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 from _parity import GOLDEN, load_golden
 from oracle import piper_oracle as oracle
@@ -27,3 +28,16 @@ def test_oracle_reproduces_fixture(fixture) -> None:
     np.testing.assert_allclose(out, g["output_per_warp"], rtol=1e-6, atol=1e-6)
     out_t = oracle.piper_attention_reference(g["query"], g["key"], g["value"], g["scale"], g["is_causal"], "per_thread")
     np.testing.assert_allclose(out_t, g["output_per_thread"], rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("fixture", FIXTURES, ids=[p.stem for p in FIXTURES])
+def test_fixture_means_are_torch_cpu_means(fixture) -> None:
+    """The K (and, non-causal, V) means of every fixture are bit for bit what the reference's
+    own calls return on CPU: key.float().mean(dim=2) (sage/reference.py:88-89) and
+    value.float().mean(dim=2) (reference.py:47-51)."""
+    g = load_golden(fixture)
+    key = torch.from_numpy(oracle.as_float32(g["key"]))
+    assert np.array_equal(key.mean(dim=2).numpy().view(np.uint32), g["key_mean"].view(np.uint32))
+    if not g["is_causal"]:
+        value = torch.from_numpy(oracle.as_float32(g["value"]))
+        assert np.array_equal(value.mean(dim=2).numpy().view(np.uint32), g["value_mean"].view(np.uint32))

@@ -92,6 +92,37 @@ def test_random_shapes_match_oracle(shape, gfx950_device) -> None:
     assert_attention_close(out32, expected, f"random {shape}", key_length=sk)
 
 
+MEAN_CASES = [
+    # (workload, batches, heads): head subsets of the BASELINE configurations at their full S
+    ("c2", None, [0, 7, 23]),
+    ("c3", None, [0, 23]),
+    ("c4", [0, 3], [0, 31]),
+    ("c5", [1], [0, 39]),
+]
+
+
+@pytest.mark.parametrize("case", MEAN_CASES, ids=[c[0] for c in MEAN_CASES])
+def test_means_are_the_reference_torch_cpu_means(case, gfx950_device) -> None:
+    """The HIP prep's K and V means equal, bit for bit, what the reference itself computes on
+    CPU -- key.float().mean(dim=2) (sage/reference.py:88-89) and value.float().mean(dim=2)
+    (reference.py:47-51) -- at the workloads' full sequence lengths (16 to 32768 keys)."""
+    from piper_kernels.workloads import WORKLOADS, make_inputs
+
+    name, batches, heads = case
+    w = WORKLOADS[name]
+    q, k, v = make_inputs(w, batches=batches, heads=heads)
+    log(f"[case] means {name} batches={batches} heads={heads} S={w.key_length}")
+    prepared = gpu_prepare(q, k, v, w.head_dim**-0.5, w.is_causal, gfx950_device)
+    got = prepared_numpy(prepared)
+    key_mean = k.float().mean(dim=2).numpy()
+    assert np.array_equal(got["key_mean"].view(np.uint32), key_mean.view(np.uint32))
+    if w.is_causal:
+        assert not got["value_mean"].any()
+    else:
+        value_mean = v.float().mean(dim=2).numpy()
+        assert np.array_equal(got["value_mean"].view(np.uint32), value_mean.view(np.uint32))
+
+
 def test_public_operator_runs_custom_op_and_keeps_dtype(gfx950_device) -> None:
     from piper_kernels import piper_attention
 

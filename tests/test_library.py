@@ -69,6 +69,15 @@ def test_ctypes_structures_match_the_c_header(tmp_path) -> None:
             assert int(expected[f"{cname}.{field}"]) == getattr(cls, field).offset, f"{cname}.{field}"
 
 
+def mean_workspace_bytes(batch_heads: int, key_length: int, head_dim: int) -> int:
+    """FP32 partials of the K and V means in torch's cascade order: one level-1 sum per chunk of
+    L^2 rows (L = 16 rows per block up to 2^19 rows) plus one trailing-rows sum, per column."""
+    ceil_log2 = (key_length - 1).bit_length() if key_length > 1 else 0
+    block = 1 << max(4, ceil_log2 // 4)
+    chunks = -(-key_length // (block * block))
+    return 2 * batch_heads * (chunks + 1) * head_dim * 4
+
+
 @pytest.mark.parametrize(
     "shape", [(1, 24, 16384, 16384, 128), (2, 3, 35, 67, 64), (1, 1, 1, 1, 64), (4, 32, 8192, 8192, 128)]
 )
@@ -88,7 +97,7 @@ def test_prepared_layout_sizes(lib, shape) -> None:
     assert layout.kv_tile_bytes == native.kv_tile_bytes(d) == -(-raw // 1024) * 1024
     assert layout.kv_tile_bytes % 1024 == 0 and layout.kv_tile_bytes - raw < 1024
     assert layout.kv_tiles_bytes == b * h * (sk64 // 64) * layout.kv_tile_bytes
-    assert layout.workspace_bytes == 2 * b * h * (-(-sk // 64)) * d * 8
+    assert layout.workspace_bytes == mean_workspace_bytes(b * h, sk, d)
 
 
 @pytest.mark.parametrize("bad", [(1, 1, 8, 8, 32), (0, 1, 8, 8, 64), (1, 1, 0, 8, 64)])
@@ -207,7 +216,7 @@ def test_sage_prepared_layout_sizes(lib, shape) -> None:
     assert layout.kv_tiles_bytes == b * h * nkb * layout.kv_tile_bytes
     assert layout.key_scale_bytes == b * h * nkb * 4
     assert layout.mean_bytes == b * h * d * 4
-    assert layout.workspace_bytes == 2 * b * h * (-(-sk // 64)) * d * 8
+    assert layout.workspace_bytes == mean_workspace_bytes(b * h, sk, d)
 
 
 def test_sage_prepare_validates_before_launching(lib) -> None:

@@ -57,40 +57,62 @@ def exact_code(x: float, scale: float) -> int:
 # --------------------------------------------------------------------------------------
 # sequence mean
 # --------------------------------------------------------------------------------------
-@pytest.mark.parametrize("length", [1, 5, 64, 65, 200])
-def test_sequence_mean_equals_exact_rational_mean_for_fp16(length: int) -> None:
+def _torch_mean_bits(x: torch.Tensor, threads: int) -> np.ndarray:
+    """The reference's call (reference.py:50, sage/reference.py:89) on CPU, as FP32 bits."""
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        return x.float().mean(dim=2).numpy().view(np.uint32)
+    finally:
+        torch.set_num_threads(previous)
+
+
+@pytest.mark.parametrize("length", [1, 5, 15, 16, 17, 64, 255, 256, 257, 1000, 4095, 4096, 4097, 8192, 12289])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_sequence_mean_is_torch_cpu_mean_bit_for_bit(length: int, dtype: torch.dtype) -> None:
     g = torch.Generator().manual_seed(length)
-    x = (torch.randn((2, 3, length, 16), generator=g) * 3 + 1).to(torch.float16)
-    got = oracle.sequence_mean(oracle.as_float32(x))
-    x64 = x.double().numpy()
-    for b in range(2):
-        for h in range(3):
-            for d in range(16):
-                total = sum(Fraction(float(v)) for v in x64[b, h, :, d])
-                # float(Fraction) is correctly rounded to FP64; then FP64 -> FP32 rounds to even
-                expected = np.float32(float(total / length))
-                assert got[b, h, d].view(np.uint32) == expected.view(np.uint32)
+    # head dims are multiples of 32 (the operator accepts 64 and 128): torch's CPU kernel runs
+    # its vectorised cascade on every column of such widths
+    x = (torch.randn((1, 2, length, 64), generator=g) * 3 + torch.randn((1, 2, 1, 64), generator=g) * 5).to(dtype)
+    got = oracle.sequence_mean(oracle.as_float32(x)).view(np.uint32)
+    for threads in (1, 4):
+        assert np.array_equal(got, _torch_mean_bits(x, threads))
+
+
+def test_sequence_mean_is_torch_cpu_mean_on_a_permuted_view() -> None:
+    # [B, S, H, D] memory viewed as [B, H, S, D]: torch reduces the same rows in the same order
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn((2, 3000, 3, 64), generator=g) * 2 + 0.5).to(torch.float16).permute(0, 2, 1, 3)
+    assert np.array_equal(oracle.sequence_mean(oracle.as_float32(x)).view(np.uint32), _torch_mean_bits(x, 4))
+
+
+def test_sequence_mean_is_torch_cpu_mean_where_the_order_matters() -> None:
+    # huge and tiny values (bf16 range): every regrouping of the additions changes the result
+    x = np.ones((1, 1, 9000, 32), dtype=np.float32)
+    x[0, 0, 0, 0] = 2.0**100
+    x[0, 0, 4095, 1] = -(2.0**100)
+    x[0, 0, 300:310, 2] = 2.0**30
+    x[0, 0, 8191, 2] = -(2.0**31)
+    x[0, 0, 0, 5] = 2.0**30  # absorbs the ones of its first blocks, not of the exact sum
+    t = torch.from_numpy(x).to(torch.bfloat16)
+    got = oracle.sequence_mean(oracle.as_float32(t)).view(np.uint32)
+    assert np.array_equal(got, _torch_mean_bits(t, 1))
+    exact = (oracle.as_float32(t).astype(np.float64).sum(axis=2) / 9000).astype(np.float32).view(np.uint32)
+    assert not np.array_equal(got, exact)  # the case really distinguishes the orders
+
+
+def test_sequence_mean_uses_longer_blocks_past_2_pow_19_rows() -> None:
+    assert [oracle.cascade_block_rows(n) for n in (1, 16, 2**16, 2**19, 2**19 + 1, 2**24)] == [16] * 4 + [32, 64]
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn((1, 1, 2**19 + 37, 32), generator=g) * 4).to(torch.float16)
+    assert np.array_equal(oracle.sequence_mean(oracle.as_float32(x)).view(np.uint32), _torch_mean_bits(x, 1))
 
 
 def test_sequence_mean_of_negative_zeros_is_positive_zero() -> None:
-    x = np.full((1, 1, 70, 4), -0.0, dtype=np.float32)
+    x = np.full((1, 1, 70, 32), -0.0, dtype=np.float32)
     mean = oracle.sequence_mean(x)
     assert not np.signbit(mean).any()
-
-
-def test_sequence_mean_is_order_defined_for_wide_bf16_ranges() -> None:
-    # 2^100 + tiny values: inexact in FP64, so the result depends on the defined order
-    x = np.zeros((1, 1, 130, 1), dtype=np.float32)
-    x[0, 0, 0, 0] = 2.0**100
-    x[0, 0, 1:, 0] = 1.0
-    x[0, 0, 100, 0] = -(2.0**100)
-    total = 0.0
-    for start in range(0, 130, oracle.MEAN_CHUNK):
-        partial = 0.0
-        for row in range(start, min(start + oracle.MEAN_CHUNK, 130)):
-            partial += float(x[0, 0, row, 0])
-        total += partial
-    assert oracle.sequence_mean(x)[0, 0, 0] == np.float32(total / 130)
+    assert np.array_equal(mean.view(np.uint32), _torch_mean_bits(torch.from_numpy(x), 1))
 
 
 # --------------------------------------------------------------------------------------
