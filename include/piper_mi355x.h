@@ -301,6 +301,9 @@ int piper_sage_attention_forward(const piper_sage_attention_args* args, void* st
  * which converges to 0.641186; stores the FP32 bits of the 16-chain sum). */
 #define PIPER_MFMA_PROBE_MAX3 4
 #define PIPER_MFMA_PROBE_EXP 5
+/* Kind VALU with one wave-wide ds_read_b128 (of zeros) after every 8 FMAs: stores the same word
+ * as kind VALU; t(VALU_LDS) - t(VALU) is the issue cost of 8 * iterations LDS reads. */
+#define PIPER_MFMA_PROBE_VALU_LDS 6
 #define PIPER_MFMA_PROBE_THREADS 512
 #define PIPER_MFMA_PROBE_OPS(kind) ((kind) == PIPER_MFMA_PROBE_F8 ? 131072 : 65536)
 int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream);

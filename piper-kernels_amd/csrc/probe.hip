@@ -20,7 +20,9 @@
 // iterations * 2048 + 64 * iterations modulo 2^32.  Kinds 4 and 5 time two other instruction
 // classes the same way (64 per round on 16 chains): v_max3_f32 (f = max(f, 1, 0), which stays 1;
 // stores the bits of 16.0) and v_exp_f32 (f = 2^-f from 0, which converges to the root of
-// x = 2^-x, 0.641186; stores the bits of the 16-chain sum).
+// x = 2^-x, 0.641186; stores the bits of the 16-chain sum).  Kind 6 is kind 2 with a wave-wide
+// ds_read_b128 of zeros after every 8 FMAs (the FMA result word, 64 * iterations, is unchanged):
+// t(6) - t(2) is what 8 * iterations LDS reads add to a VALU-bound wave.
 #include "common.h"
 #include "kernels.h"
 
@@ -67,6 +69,38 @@ __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* 
 #pragma unroll
     for (int i = 0; i < 16; ++i) fsum += f[i];
     total = __builtin_bit_cast(uint32_t, fsum);
+  } else if constexpr (kKind == 6) {
+    // kind 2's FMAs with one wave-wide ds_read_b128 after every 8 of them (8 per round, the
+    // attention kernel's ratio of LDS reads to VALU work); the LDS words are zero
+    __shared__ __attribute__((aligned(16))) float lds[4 * kProbeThreads];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lds[4 * threadIdx.x + i] = 0.0f;
+    __syncthreads();
+    const uint32_t address = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) float*)(lds + 4 * (threadIdx.x & 63))));
+    float one = 1.0f, addend = 1.0f;
+    asm volatile("" : "+v"(one), "+v"(addend));
+    float f[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) f[i] = 0.0f;
+    v4i word = {0, 0, 0, 0};
+    for (int it = 0; it < iterations; ++it) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        // explicit reads (the compiler would hoist or merge loop-invariant loads); their words
+        // are waited for once after the loop
+        asm volatile("ds_read_b128 %0, %1" : "=v"(word) : "v"(address) : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[(8 * c + i) & 15] = fmaf(f[(8 * c + i) & 15], one, addend);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(word) : : "memory");
+    float fsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) fsum += f[i];
+    total = __builtin_bit_cast(uint32_t, fsum) + static_cast<uint32_t>(word[0] | word[1] | word[2] | word[3]);
   } else if constexpr (kKind == 2 || kKind == 3) {
     v4i a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     asm volatile("" : "+v"(a));
@@ -130,7 +164,8 @@ hipError_t launch_mfma_probe(int kind, int workgroups, int iterations, uint32_t*
     case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, grid, block, 0, stream, sink, iterations); break;
     case 3: hipLaunchKernelGGL(mfma_probe_kernel<3>, grid, block, 0, stream, sink, iterations); break;
     case 4: hipLaunchKernelGGL(mfma_probe_kernel<4>, grid, block, 0, stream, sink, iterations); break;
-    default: hipLaunchKernelGGL(mfma_probe_kernel<5>, grid, block, 0, stream, sink, iterations); break;
+    case 5: hipLaunchKernelGGL(mfma_probe_kernel<5>, grid, block, 0, stream, sink, iterations); break;
+    default: hipLaunchKernelGGL(mfma_probe_kernel<6>, grid, block, 0, stream, sink, iterations); break;
   }
   return hipGetLastError();
 }

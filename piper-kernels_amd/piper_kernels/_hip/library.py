@@ -46,6 +46,7 @@ MFMA_PROBE_VALU = 2  # FP32 FMAs only
 MFMA_PROBE_I8_VALU = 3  # the INT8 MFMAs interleaved with the FP32 FMAs
 MFMA_PROBE_MAX3 = 4  # v_max3_f32 only
 MFMA_PROBE_EXP = 5  # v_exp_f32 only
+MFMA_PROBE_VALU_LDS = 6  # the FP32 FMAs with a ds_read_b128 after every 8
 MFMA_PROBE_THREADS = 512
 MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 

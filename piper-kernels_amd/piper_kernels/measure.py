@@ -153,7 +153,7 @@ def mfma_probe_expected(kind: int, iterations: int) -> int:
 
     if kind == native.MFMA_PROBE_I8:
         return (iterations * 2048) % (1 << 32)
-    if kind == native.MFMA_PROBE_VALU:  # 16 FMA chains of 4 * iterations increments of 1.0
+    if kind in (native.MFMA_PROBE_VALU, native.MFMA_PROBE_VALU_LDS):  # 16 chains of 4 * iterations + 1.0
         return struct.unpack("<I", struct.pack("<f", float(iterations * 64)))[0]
     if kind == native.MFMA_PROBE_I8_VALU:
         return (iterations * 2048 + iterations * 64) % (1 << 32)
@@ -237,7 +237,8 @@ def measure_mfma_valu_sharing(device: torch.device, *, iterations: int = 2048, l
     units run concurrently, 0 when MFMA execution and VALU issue serialise.  The cycle figures
     convert per-SIMD time at the 2.4 GHz peak clock: per MFMA, per FMA (two waves issuing), and
     the VALU cycles one interleaved MFMA costs (its share of t_both - t_valu); and, from the
-    max3 and exp kinds, the per-SIMD cycles of a v_max3_f32 and a v_exp_f32 issued by two waves.
+    max3 and exp kinds, the per-SIMD cycles of a v_max3_f32 and a v_exp_f32 issued by two waves;
+    and, from the LDS kind, the VALU cycles one interleaved wave-wide ds_read_b128 costs.
     """
     from ._hip import library as native
 
@@ -246,7 +247,7 @@ def measure_mfma_valu_sharing(device: torch.device, *, iterations: int = 2048, l
     lib = native.load_library()
     workgroups = torch.cuda.get_device_properties(device).multi_processor_count
     kinds = (native.MFMA_PROBE_I8, native.MFMA_PROBE_VALU, native.MFMA_PROBE_I8_VALU, native.MFMA_PROBE_MAX3,
-             native.MFMA_PROBE_EXP)
+             native.MFMA_PROBE_EXP, native.MFMA_PROBE_VALU_LDS)
     t = {k: _time_probe(lib, k, workgroups, iterations, launches, device) for k in kinds}
     t_m, t_v, t_b = t[native.MFMA_PROBE_I8], t[native.MFMA_PROBE_VALU], t[native.MFMA_PROBE_I8_VALU]
     cycles = 2.4e9 * 1e-3  # cycles per millisecond at the peak clock
@@ -264,5 +265,6 @@ def measure_mfma_valu_sharing(device: torch.device, *, iterations: int = 2048, l
         "cycles_per_fma": round(t_v * cycles / fmas, 2),
         "cycles_per_max3": round(t[native.MFMA_PROBE_MAX3] * cycles / fmas, 2),
         "cycles_per_exp": round(t[native.MFMA_PROBE_EXP] * cycles / fmas, 2),
+        "valu_cycles_per_lds_read": round((t[native.MFMA_PROBE_VALU_LDS] - t_v) * cycles / (fmas / 8), 1),
         "valu_cycles_per_interleaved_mfma": round((t_b - t_v) * cycles / mfmas, 1),
     }

@@ -274,7 +274,7 @@ def test_mfma_probe_constants_match_the_header(tmp_path) -> None:
                       '  printf("%d %d %d %d %d %d %d\\n", PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8, PIPER_MFMA_PROBE_THREADS,\n'
                       '         PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8),\n'
                       '         PIPER_MFMA_PROBE_VALU, PIPER_MFMA_PROBE_I8_VALU);\n'
-                      '  printf("%d %d\\n", PIPER_MFMA_PROBE_MAX3, PIPER_MFMA_PROBE_EXP);\n'
+                      '  printf("%d %d %d\\n", PIPER_MFMA_PROBE_MAX3, PIPER_MFMA_PROBE_EXP, PIPER_MFMA_PROBE_VALU_LDS);\n'
                       '  return 0; }\n')
     exe = tmp_path / "probe"
     subprocess.run(["gcc", f"-I{REPO / 'include'}", str(source), "-o", str(exe)], check=True)
@@ -282,14 +282,14 @@ def test_mfma_probe_constants_match_the_header(tmp_path) -> None:
     assert values == [native.MFMA_PROBE_I8, native.MFMA_PROBE_F8, native.MFMA_PROBE_THREADS,
                       native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8],
                       native.MFMA_PROBE_VALU, native.MFMA_PROBE_I8_VALU, native.MFMA_PROBE_MAX3,
-                      native.MFMA_PROBE_EXP]
+                      native.MFMA_PROBE_EXP, native.MFMA_PROBE_VALU_LDS]
     # 32x32x32 INT8 and 32x32x64 FP8: two operations per multiply-add
     assert native.MFMA_PROBE_OPS == {native.MFMA_PROBE_I8: 2 * 32 * 32 * 32, native.MFMA_PROBE_F8: 2 * 32 * 32 * 64}
 
 
 def test_mfma_probe_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
-        lib.mfma_probe(6, 1, 1, 0x1000, 0)
+        lib.mfma_probe(7, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
         lib.mfma_probe(-1, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="workgroups and"):
