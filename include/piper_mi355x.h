@@ -48,11 +48,17 @@
 extern "C" {
 #endif
 
-#define PIPER_ABI_VERSION 1
+#define PIPER_ABI_VERSION 2
 
 /* Rows per quantisation group (sage/reference.py:6-7) and keys per P block (reference.py:16). */
 #define PIPER_QUERY_BLOCK 32
 #define PIPER_KEY_BLOCK 64
+/* Scales stored per quantisation block: one per thread group of the reference's "per_thread"
+ * Q/K granularity (sage/reference.py:23-58) -- query rows {t, t+8, t+16, t+24} of a 32-row
+ * block share slot t, key rows {8a + 2t + c} of a 64-row block share slot t.  With the default
+ * per-block ("per_warp") granularity every slot holds the block's one scale. */
+#define PIPER_QUERY_SCALE_SLOTS 8
+#define PIPER_KEY_SCALE_SLOTS 4
 
 typedef enum piper_dtype {
   PIPER_FLOAT16 = 0,
@@ -90,17 +96,20 @@ typedef struct piper_tensor {
  * nqb = Sq32/32 and nkb = Sk64/64, all arrays are dense and row-major:
  *
  *   query_code     int8    [B, H, Sq32, D]   Q codes, padded rows zero
- *   query_scale    float   [B, H, nqb]       amax/127 + 1e-7 per 32-row block
- *   key_scale      float   [B, H, nkb]       same for K - mean(K), per 64-row block
+ *   query_scale    float   [B, H, nqb, 8]    amax/127 + 1e-7 per 32-row block, or per thread
+ *                                            group of it (PIPER_QUERY_SCALE_SLOTS)
+ *   key_scale      float   [B, H, nkb, 4]    same for K - mean(K), per 64-row block or thread
+ *                                            group (PIPER_KEY_SCALE_SLOTS)
  *   value_scale    float   [B, H, Sk64]      amax_D/127 + 1e-7 per V row (padding 0)
- *   key_mean       float   [B, H, D]         order-defined sequence mean of K
+ *   key_mean       float   [B, H, D]         sequence mean of K: FP32, torch's CPU summation order
  *   value_mean     float   [B, H, D]         same for V; zeros when causal
  *   kv_tiles       bytes   [B, H, nkb, PIPER_KV_TILE_BYTES(D)]: one self-contained record
  *                  per 64-key tile, byte for byte the LDS stage of the attention kernel (it is
  *                  copied with direct global -> LDS loads in 1 KiB pieces):
  *       [0, 64*(D+16))           int8  K codes of K - mean(K), [64 keys][D], rows of D + 16
  *                                      bytes (padding rows of short tiles are zero codes);
- *                                      bytes [D, D+4) of row 0 hold the tile's K scale (FP32)
+ *                                      bytes [D, D+16) of row 0 hold the tile's 4 K scale
+ *                                      slots (FP32, as key_scale)
  *       [PIPER_KV_V_OFFSET(D), +80*D)
  *                                int8  V codes of V - mean(V), transposed: [D][64 keys], rows
  *                                      of 80 bytes
@@ -145,6 +154,8 @@ typedef struct piper_layout {
 /* piper_prepare_args.flags */
 #define PIPER_PREPARE_SKIP_QUERY 1 /* leave query_code / query_scale alone (they may be NULL):
                                       for piper_attention_forward_fused, which quantises Q itself */
+#define PIPER_PREPARE_QK_PER_THREAD 2 /* Q and K scales per thread group (the reference's
+                                         "per_thread"); default: one per block ("per_warp") */
 
 typedef struct piper_prepare_args {
   int32_t abi_version; /* PIPER_ABI_VERSION */
@@ -171,6 +182,11 @@ typedef struct piper_prepare_args {
                                           PIPER_PLAN_NO_XCD_REMAP) instead of head by head */
 #define PIPER_PLAN_MASK 15
 
+/* piper_attention_args.flags / piper_attention_fused_args.flags */
+#define PIPER_ATTENTION_QK_PER_THREAD 1 /* Q/K scales per thread group: read slot (row % 8) of the
+                                           query scales and the tile's four K group scales; the
+                                           fused entry point quantises Q per thread group too */
+
 typedef struct piper_attention_args {
   int32_t abi_version;  /* PIPER_ABI_VERSION */
   int32_t output_dtype; /* PIPER_FLOAT16, PIPER_BFLOAT16 or PIPER_FLOAT32 */
@@ -178,7 +194,7 @@ typedef struct piper_attention_args {
   int32_t plan;         /* launch plan: OR of PIPER_PLAN_* bits; 0 = the default plan */
   piper_shape shape;
   float scale;          /* softmax scale, finite and > 0 */
-  int32_t reserved;
+  int32_t flags;        /* PIPER_ATTENTION_QK_PER_THREAD if the prep ran with PIPER_PREPARE_QK_PER_THREAD */
   piper_prepared prepared; /* inputs, as written by piper_prepare */
   void* output;            /* [B, H, Sq, D] dense row-major, output_dtype */
 } piper_attention_args;
@@ -194,6 +210,8 @@ typedef struct piper_attention_fused_args {
   int32_t is_causal;
   int32_t plan;         /* OR of PIPER_PLAN_* bits */
   float scale;          /* softmax scale, finite and > 0 */
+  int32_t flags;        /* PIPER_ATTENTION_QK_PER_THREAD with a per-thread-group K prep */
+  int32_t reserved;     /* 0 */
   piper_shape shape;
   piper_tensor query;      /* [B, H, Sq, D], the layout rules of piper_prepare_args.query */
   piper_prepared prepared; /* from piper_prepare; query_code and query_scale are not read */
@@ -217,7 +235,7 @@ typedef struct piper_attention_fused_args {
 
 typedef struct piper_sage_prepared {
   float* key_scale;   /* [B, H, Sk64/64] INT8 K scales */
-  float* key_mean;    /* [B, H, D] the K smoothing mean (order-defined, as piper_prepared) */
+  float* key_mean;    /* [B, H, D] the K smoothing mean (torch's CPU order, as piper_prepared) */
   float* value_scale; /* [B, H, D] FP8 V scales, per channel */
   void* kv_tiles;     /* [B, H, Sk64/64] tile records, 16-byte aligned */
 } piper_sage_prepared;

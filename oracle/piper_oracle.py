@@ -215,6 +215,24 @@ def quantize_key_per_thread(k32: np.ndarray, quantization_range=INT8_RANGE):
     return codes[:, :, :length], np.ascontiguousarray(per_row[:, :, :length])
 
 
+def query_group_scales_per_thread(q32: np.ndarray, quantization_range=INT8_RANGE) -> np.ndarray:
+    """The 8 group scales of every zero-padded 32-row Q block under ``per_thread``
+    (group t = rows {t, t+8, t+16, t+24}): ``[B, H, Sq32/32, 8]``, the slots the HIP prep stores."""
+    padded, _ = _pad_rows(np.asarray(q32, dtype=np.float32), QUERY_BLOCK)
+    batch, heads, padded_length, width = padded.shape
+    grouped = padded.reshape(batch, heads, padded_length // QUERY_BLOCK, 4, 8, width)
+    return _scale_from_amax(np.abs(grouped).max(axis=(3, 5)), quantization_range)
+
+
+def key_group_scales_per_thread(k_centered32: np.ndarray, quantization_range=INT8_RANGE) -> np.ndarray:
+    """The 4 group scales of every zero-padded 64-row K block under ``per_thread``
+    (group t = rows {8a + 2t + c}): ``[B, H, Sk64/64, 4]``."""
+    padded, _ = _pad_rows(np.asarray(k_centered32, dtype=np.float32), KEY_BLOCK)
+    batch, heads, padded_length, width = padded.shape
+    grouped = padded.reshape(batch, heads, padded_length // KEY_BLOCK, 8, 4, 2, width)
+    return _scale_from_amax(np.abs(grouped).max(axis=(3, 5, 6)), quantization_range)
+
+
 def center_key(k32: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """``K - mean_S(K)`` in FP32 with the pinned mean (sage/reference.py:88-89)."""
     mean = sequence_mean(k32)
@@ -224,8 +242,10 @@ def center_key(k32: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
 def quantize_query_key(q32: np.ndarray, k32: np.ndarray, granularity: str):
     """Centre K and quantise Q/K (sage/reference.py:80-108).
 
-    Returns a dict with codes, per-row scales (as the reference returns them) and, for
-    ``per_warp``, the per-block scales the HIP prep kernel stores.
+    Returns a dict with codes, per-row scales (as the reference returns them), for
+    ``per_warp`` the per-block scales, and for both the scale slots the HIP prep stores
+    (``query_slot_scale`` [B, H, Sq32/32, 8], ``key_slot_scale`` [B, H, Sk64/64, 4]: one per
+    thread group, or the block scale repeated).
     """
     if granularity not in GRANULARITIES:
         raise ValueError(f"unknown Q/K quantization granularity: {granularity}")
@@ -241,11 +261,20 @@ def quantize_query_key(q32: np.ndarray, k32: np.ndarray, granularity: str):
             key_block_scale=k_block_scale,
             query_scale=np.repeat(q_block_scale, QUERY_BLOCK, axis=2)[:, :, : q32.shape[2]],
             key_scale=np.repeat(k_block_scale, KEY_BLOCK, axis=2)[:, :, : k32.shape[2]],
+            query_slot_scale=np.repeat(q_block_scale[..., None], 8, axis=3),
+            key_slot_scale=np.repeat(k_block_scale[..., None], 4, axis=3),
         )
     else:
         q_codes, q_scale = quantize_query_per_thread(q32)
         k_codes, k_scale = quantize_key_per_thread(key_centered)
-        result.update(query_code=q_codes, key_code=k_codes, query_scale=q_scale, key_scale=k_scale)
+        result.update(
+            query_code=q_codes,
+            key_code=k_codes,
+            query_scale=q_scale,
+            key_scale=k_scale,
+            query_slot_scale=query_group_scales_per_thread(q32),
+            key_slot_scale=key_group_scales_per_thread(key_centered),
+        )
     return result
 
 

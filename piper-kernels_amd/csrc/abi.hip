@@ -20,6 +20,8 @@ static_assert(PIPER_SAGE_TILE_BYTES(64) == piper::sage_tile_bytes(64), "SageAtte
 static_assert(PIPER_SAGE_TILE_BYTES(128) == piper::sage_tile_bytes(128), "SageAttention2++ record size (D = 128)");
 static_assert(PIPER_SAGE_V_OFFSET(128) == piper::sage_v_offset(128), "SageAttention2++ V^T offset");
 static_assert(PIPER_MFMA_PROBE_THREADS == piper::kProbeThreads, "probe workgroup size");
+static_assert(PIPER_QUERY_SCALE_SLOTS == piper::kQueryScaleSlots && PIPER_KEY_SCALE_SLOTS == piper::kKeyScaleSlots,
+              "scale slots per block");
 
 namespace {
 
@@ -68,7 +70,7 @@ piper::InputTensor to_input(const piper_tensor& t) {
 
 // Validation and launch shared by piper_attention_forward (prepared query codes) and
 // piper_attention_forward_fused (query != NULL: the kernel quantises the query itself).
-int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_causal, int32_t plan,
+int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_causal, int32_t plan, int32_t flags,
                           const piper_shape& s, float scale, const piper_prepared& o, void* output,
                           const piper_tensor* query, int32_t query_dtype, void* stream) {
   if (abi_version != PIPER_ABI_VERSION)
@@ -82,6 +84,7 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   if (!(std::isfinite(scale) && scale > 0.0f))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
   if (plan < 0 || plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", plan);
+  if ((flags & ~PIPER_ATTENTION_QK_PER_THREAD) != 0) return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", flags);
   if (query != nullptr) {
     if (query_dtype != PIPER_FLOAT16 && query_dtype != PIPER_BFLOAT16)
       return fail(PIPER_ERROR_UNSUPPORTED, "query dtype must be float16 or bfloat16");
@@ -117,6 +120,7 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   ap.xcd_remap = (plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
   ap.causal_interleave = (plan & PIPER_PLAN_CAUSAL_INTERLEAVE) ? 1 : 0;
   ap.heads = static_cast<int>(s.heads);
+  ap.per_thread = (flags & PIPER_ATTENTION_QK_PER_THREAD) ? 1 : 0;
   if (query != nullptr) {
     ap.fused_query = 1;
     ap.query_bf16 = query_dtype == PIPER_BFLOAT16 ? 1 : 0;
@@ -149,8 +153,8 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
   const int64_t sk64 = ceil_div(shape->key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK;
   const int64_t chunks = piper::cascade_chunks(static_cast<int>(shape->key_length));
   layout->query_code_bytes = bh * sq32 * d;
-  layout->query_scale_bytes = bh * (sq32 / PIPER_QUERY_BLOCK) * 4;
-  layout->key_scale_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * 4;
+  layout->query_scale_bytes = bh * (sq32 / PIPER_QUERY_BLOCK) * PIPER_QUERY_SCALE_SLOTS * 4;
+  layout->key_scale_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * PIPER_KEY_SCALE_SLOTS * 4;
   layout->value_scale_bytes = bh * sk64 * 4;
   layout->mean_bytes = bh * d * 4;
   layout->kv_tile_bytes = PIPER_KV_TILE_BYTES(d);
@@ -170,7 +174,8 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   if (int st = check_shape(&a->shape)) return st;
   if (a->is_causal && a->shape.query_length != a->shape.key_length)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
-  if ((a->flags & ~PIPER_PREPARE_SKIP_QUERY) != 0) return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
+  if ((a->flags & ~(PIPER_PREPARE_SKIP_QUERY | PIPER_PREPARE_QK_PER_THREAD)) != 0)
+    return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   const bool with_query = (a->flags & PIPER_PREPARE_SKIP_QUERY) == 0;
   if (with_query)
     if (int st = check_input("query", a->query)) return st;
@@ -223,6 +228,7 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   qp.k_blocks_wg = static_cast<int>(ceil_div(static_cast<int64_t>(bh) * qp.nkb, 4));
   qp.v_blocks_wg = qp.k_blocks_wg;
   qp.center_value = a->is_causal ? 0 : 1;
+  qp.per_thread = (a->flags & PIPER_PREPARE_QK_PER_THREAD) ? 1 : 0;
   qp.key_mean = o.key_mean;
   qp.value_mean = o.value_mean;
   qp.query_code = o.query_code;
@@ -239,14 +245,14 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
 
 int piper_attention_forward(const piper_attention_args* a, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
-  return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->shape, a->scale,
-                               a->prepared, a->output, nullptr, 0, stream);
+  return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->flags, a->shape,
+                               a->scale, a->prepared, a->output, nullptr, 0, stream);
 }
 
 int piper_attention_forward_fused(const piper_attention_fused_args* a, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
-  return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->shape, a->scale,
-                               a->prepared, a->output, &a->query, a->dtype, stream);
+  return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->flags, a->shape,
+                               a->scale, a->prepared, a->output, &a->query, a->dtype, stream);
 }
 
 int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layout) {

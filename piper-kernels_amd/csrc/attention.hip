@@ -50,9 +50,14 @@ __device__ __forceinline__ uint32_t pack_codes(float e0, float e1, float e2, flo
 }
 
 // Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave.
+// ct[g]: the score multiplier q_scale * k_scale * softmax_scale * log2(e) of key thread group g
+// (keys k with (k % 8) / 2 == g; all four equal for per-block K scales).  Output register r of
+// lane half h holds key 16h + r (and 32 + 16h + r), so register 4q + i belongs to group
+// 2 (q % 2) + i / 2.
 template <int D, int NW, bool kCausal>
-__device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[2], float ct, int t, int q0, int n,
-                                             int h, float (&num)[D / 32][16], float& den, float& mref) {
+__device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[2], const float (&ct)[4], int t,
+                                             int q0, int n, int h, float (&num)[D / 32][16], float& den,
+                                             float& mref) {
   using L = TileLayout<D, NW>;
   constexpr int kChunksD = D / 32;
 
@@ -63,14 +68,15 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   for (int q = 0; q < 4; ++q) {
     const float4 la = lk4[4 * h + q];
     const float4 lb = lk4[8 + 4 * h + q];
-    x[4 * q + 0] = fmaf(unbias(s[0][4 * q + 0]), ct, la.x);
-    x[4 * q + 1] = fmaf(unbias(s[0][4 * q + 1]), ct, la.y);
-    x[4 * q + 2] = fmaf(unbias(s[0][4 * q + 2]), ct, la.z);
-    x[4 * q + 3] = fmaf(unbias(s[0][4 * q + 3]), ct, la.w);
-    x[16 + 4 * q + 0] = fmaf(unbias(s[1][4 * q + 0]), ct, lb.x);
-    x[16 + 4 * q + 1] = fmaf(unbias(s[1][4 * q + 1]), ct, lb.y);
-    x[16 + 4 * q + 2] = fmaf(unbias(s[1][4 * q + 2]), ct, lb.z);
-    x[16 + 4 * q + 3] = fmaf(unbias(s[1][4 * q + 3]), ct, lb.w);
+    const float c01 = ct[2 * (q & 1)], c23 = ct[2 * (q & 1) + 1];
+    x[4 * q + 0] = fmaf(unbias(s[0][4 * q + 0]), c01, la.x);
+    x[4 * q + 1] = fmaf(unbias(s[0][4 * q + 1]), c01, la.y);
+    x[4 * q + 2] = fmaf(unbias(s[0][4 * q + 2]), c23, la.z);
+    x[4 * q + 3] = fmaf(unbias(s[0][4 * q + 3]), c23, la.w);
+    x[16 + 4 * q + 0] = fmaf(unbias(s[1][4 * q + 0]), c01, lb.x);
+    x[16 + 4 * q + 1] = fmaf(unbias(s[1][4 * q + 1]), c01, lb.y);
+    x[16 + 4 * q + 2] = fmaf(unbias(s[1][4 * q + 2]), c23, lb.z);
+    x[16 + 4 * q + 3] = fmaf(unbias(s[1][4 * q + 3]), c23, lb.w);
   }
   if constexpr (kCausal) {
     if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // block crosses this wave's diagonal
@@ -168,7 +174,7 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
 constexpr int kStages = 6;
 constexpr int kLead = 4;
 
-template <int D, int NW, bool kCausal, bool kBarrier>
+template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                               int wave, int lane, const v4i (&qf)[D / 32], float cq,
                                               int q0, int n, int h, int krow, const v16i& bias,
@@ -181,13 +187,23 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
   if (t < wave_tiles) {
     block_scores<D, L>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, bias, s_next);  // unused past the end
     const char* stage = smem + (t % kStages) * L::kStageBytes;
-    const float key_scale = *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
-    block_update<D, NW, kCausal>(stage, s_cur, cq * key_scale, t, q0, n, h, num, den, mref);
+    // the K scales of the tile's four thread groups sit in the padding of K row 0
+    float ct[4];
+    if constexpr (kPerThread) {
+      const float4 ks = *reinterpret_cast<const float4*>(stage + D);
+      ct[0] = cq * ks.x;
+      ct[1] = cq * ks.y;
+      ct[2] = cq * ks.z;
+      ct[3] = cq * ks.w;
+    } else {  // per-block scales: the four slots hold the same value
+      ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
+    }
+    block_update<D, NW, kCausal>(stage, s_cur, ct, t, q0, n, h, num, den, mref);
   }
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }
 
-template <int D, int NW, bool kCausal, int kOut>
+template <int D, int NW, bool kCausal, int kOut, bool kPerThread>
 __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams p) {
   using L = TileLayout<D, NW>;
   constexpr int kChunksD = D / 32;
@@ -223,7 +239,9 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
     const int8_t* qrow = p.query_code + (static_cast<long>(bh) * p.sq32 + q0 + n) * D + 16 * h;
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) qf[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
-    cq = p.query_scale[static_cast<long>(bh) * p.nqb + (q0 >> 5)] * p.scale_log2e;
+    // the scale of this lane's query row: slot n % 8 of its block (every slot, per block)
+    cq = p.query_scale[(static_cast<long>(bh) * p.nqb + (q0 >> 5)) * kQueryScaleSlots + (kPerThread ? (n & 7) : 0)] *
+         p.scale_log2e;
     // Settle the prepared Q loads inside this branch: a load the compiler still counts as
     // pending at the loop header would get its wait (in-order vmcnt, so a wait for all direct
     // LDS copies in flight) inside every iteration, and a wait at the join would also drain
@@ -249,7 +267,7 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLead * (L::kRounds - 1)) : "memory");
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
-    cq = quantize_query_block<D>(p, q0, n, raw, qf) * p.scale_log2e;
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * p.scale_log2e;
   }
 
   float num[kChunksD][16];
@@ -276,13 +294,13 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   // unrolled by two so both score sets keep static names; one barrier per pair
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
+    pipeline_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
                                          krow, bias, s_a, s_b, num, den, mref);
-    pipeline_step<D, NW, kCausal, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
+    pipeline_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
                                         h, krow, bias, s_b, s_a, num, den, mref);
   }
   if (t < tiles)
-    pipeline_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
+    pipeline_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
                                          krow, bias, s_a, s_b, num, den, mref);
   // no direct copy may still be writing this workgroup's LDS when its waves end
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -307,21 +325,28 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   }
 }
 
-template <int D, int NW, bool kCausal>
+template <int D, int NW, bool kCausal, bool kPerThread>
 static hipError_t launch_out(int out_dtype, const AttnParams& ap, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(ap.query_tiles * ap.batch_heads));
   const dim3 block(NW * 64);
   switch (out_dtype) {
-    case 0: hipLaunchKernelGGL((attention_kernel<D, NW, kCausal, 0>), grid, block, 0, stream, ap); break;
-    case 1: hipLaunchKernelGGL((attention_kernel<D, NW, kCausal, 1>), grid, block, 0, stream, ap); break;
-    default: hipLaunchKernelGGL((attention_kernel<D, NW, kCausal, 2>), grid, block, 0, stream, ap); break;
+    case 0: hipLaunchKernelGGL((attention_kernel<D, NW, kCausal, 0, kPerThread>), grid, block, 0, stream, ap); break;
+    case 1: hipLaunchKernelGGL((attention_kernel<D, NW, kCausal, 1, kPerThread>), grid, block, 0, stream, ap); break;
+    default: hipLaunchKernelGGL((attention_kernel<D, NW, kCausal, 2, kPerThread>), grid, block, 0, stream, ap); break;
   }
   return hipGetLastError();
 }
 
+template <int D, int NW, bool kCausal>
+static hipError_t launch_granularity(int out_dtype, const AttnParams& ap, hipStream_t stream) {
+  return ap.per_thread ? launch_out<D, NW, kCausal, true>(out_dtype, ap, stream)
+                       : launch_out<D, NW, kCausal, false>(out_dtype, ap, stream);
+}
+
 template <int D, int NW>
 static hipError_t launch_causal(bool causal, int out_dtype, const AttnParams& ap, hipStream_t stream) {
-  return causal ? launch_out<D, NW, true>(out_dtype, ap, stream) : launch_out<D, NW, false>(out_dtype, ap, stream);
+  return causal ? launch_granularity<D, NW, true>(out_dtype, ap, stream)
+                : launch_granularity<D, NW, false>(out_dtype, ap, stream);
 }
 
 hipError_t launch_attention(int head_dim, bool causal, int out_dtype, int waves, const AttnParams& ap,

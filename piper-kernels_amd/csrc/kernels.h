@@ -75,6 +75,12 @@ struct MeanParams {
   float* value_scale;  // [batch_heads][D] (value_absmax only)
 };
 
+// Scales stored per quantisation block: one per thread group of the reference's per_thread
+// granularity (8 per 32-row Q block, 4 per 64-row K block); per-block quantisation repeats its
+// one scale in every slot, so the attention kernel reads both the same way.
+constexpr int kQueryScaleSlots = 8;
+constexpr int kKeyScaleSlots = 4;
+
 struct QuantParams {
   InputTensor query;
   InputTensor key;
@@ -91,6 +97,7 @@ struct QuantParams {
   int k_blocks_wg;
   int v_blocks_wg;
   int center_value;
+  int per_thread;  // 1: Q/K scales per thread group (per_thread); 0: one per block (per_warp)
   const float* key_mean;
   const float* value_mean;
   int8_t* query_code;
@@ -122,6 +129,9 @@ struct AttnParams {
   // Fused query quantisation: each wave quantises its own 32-row query block from `query`
   // (query_code and query_scale are then unused).
   int fused_query;
+  // Q/K scale granularity: 1 = per thread group (query scale slot n % 8 of the row's block, the
+  // tile's four K group scales), 0 = per block (slot 0, one K scale)
+  int per_thread;
   int query_bf16;
   int heads;
   InputTensor query;

@@ -165,15 +165,21 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
 // tile (a workgroup of 4 waves holds units of one kind only).  No LDS: V tiles are written
 // transposed straight from registers.
 // ---------------------------------------------------------------------------------------
-// Q or K block of kRows rows: one scale over kRows x D values.
-// Codes go to rows of kStride bytes (D for query codes, the padded tile stride for keys).
-template <bool kBf16, int D, int kRows, bool kCenter, int kStride>
+// Q or K block of kRows rows.  Per block (the reference's "per_warp", sage/reference.py:61-77):
+// one scale over kRows x D values.  Per thread group (its "per_thread", sage/reference.py:23-58):
+// a 32-row Q block has 8 scales, row r in group r % 8 (rows {t, t+8, t+16, t+24}); a 64-row K
+// block has 4, row r in group (r % 8) / 2 (rows {8a + 2t + c}).  The block's kSlots group scales
+// go to scale_out (per block: the one scale repeated), and key tiles carry them in the padding
+// of K row 0 as well (bytes [D, D + 4 * kSlots)).  Codes go to rows of kStride bytes (D for
+// query codes, the padded tile stride for keys).
+template <bool kBf16, int D, int kRows, bool kCenter, int kStride, int kSlots>
 __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int h, int row0, int length,
                                                const float* __restrict__ mean, int8_t* __restrict__ codes,
-                                               float* __restrict__ scale_out) {
+                                               float* __restrict__ scale_out, bool per_thread) {
   constexpr int kGroups = D / 8;
   constexpr int kRowsPerIter = kWave / kGroups;
   constexpr int kIters = kRows / kRowsPerIter;
+  static_assert(kSlots == 1 || kSlots == (kRows == 32 ? 8 : 4), "one scale or one per thread group");
   const int lane = threadIdx.x & 63;
   const int group = lane % kGroups;
   const int sub = lane / kGroups;
@@ -184,7 +190,7 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
   for (int i = 0; i < 8; ++i) mu[i] = kCenter ? mean[group * 8 + i] : 0.0f;
 
   uint4 raw[kIters];
-  float amax = 0.0f;
+  float amax[2] = {0.0f, 0.0f};  // by iteration parity: a lane's rows fall in at most two groups
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
     const int row = row0 + it * kRowsPerIter + sub;
@@ -200,12 +206,28 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
     for (int i = 0; i < 8; ++i) {
       // padded rows are zero after centring (sage/reference.py:13-20 pads the centred K)
       const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
-      amax = fmaxf(amax, fabsf(x));
+      amax[it & 1] = fmaxf(amax[it & 1], fabsf(x));
     }
   }
-  amax = wave_max(amax);
-  const float scale = scale_from_amax(amax);
-  const Divisor divisor(scale);
+  // group of row r = it * kRowsPerIter + sub within the block, for each iteration parity
+  const auto group_of = [&](int parity) {
+    const int r = (parity * kRowsPerIter + sub) & 7;
+    return kRows == 32 ? r : r >> 1;
+  };
+  float scale[2];
+  if (!per_thread) {
+    scale[0] = scale[1] = scale_from_amax(wave_max(fmaxf(amax[0], amax[1])));
+  } else {
+    // lanes whose rows share a group: the kGroups column lanes of one sub-row (Q), or of the two
+    // sub-rows 2j, 2j + 1 (K) -- aligned runs of lanes; at D = 64 both parities are one group
+    constexpr int kShare = kGroups * (kRows == 32 ? 1 : 2);
+    amax[0] = group_max<kShare>(amax[0]);
+    amax[1] = group_max<kShare>(amax[1]);
+    if (kRowsPerIter == 8) amax[0] = amax[1] = fmaxf(amax[0], amax[1]);
+    scale[0] = scale_from_amax(amax[0]);
+    scale[1] = scale_from_amax(amax[1]);
+  }
+  const Divisor divisor[2] = {Divisor(scale[0]), Divisor(scale[1])};
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
     const int row = row0 + it * kRowsPerIter + sub;
@@ -215,15 +237,25 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
-      c[i] = code_word(x, divisor);
+      c[i] = code_word(x, divisor[it & 1]);
     }
     uint2 packed = make_uint2(pack_low_bytes(c[0], c[1], c[2], c[3]), pack_low_bytes(c[4], c[5], c[6], c[7]));
     *reinterpret_cast<uint2*>(codes + static_cast<long>(it * kRowsPerIter + sub) * kStride + group * 8) = packed;
   }
-  if (lane == 0) {
-    *scale_out = scale;
-    // key tiles also carry their scale in the padding of K row 0 (bytes [D, D + 4))
-    if constexpr (kStride != D) *reinterpret_cast<float*>(codes + D) = scale;
+  // key tiles also carry their scales in the padding of K row 0 (bytes [D, D + 4 * kSlots))
+  float* tile_scales = kStride != D ? reinterpret_cast<float*>(codes + D) : nullptr;
+  if (!per_thread || kSlots == 1) {
+    if (lane < kSlots) {
+      scale_out[lane] = scale[0];
+      if (tile_scales != nullptr) tile_scales[lane] = scale[0];
+    }
+  } else if (group == 0 && (kRows == 32 || (sub & 1) == 0)) {
+    // one lane per (sub-row group, parity) writes its group's scale
+#pragma unroll
+    for (int parity = 0; parity < 2; ++parity) {
+      scale_out[group_of(parity)] = scale[parity];
+      if (tile_scales != nullptr) tile_scales[group_of(parity)] = scale[parity];
+    }
   }
 }
 
@@ -240,9 +272,10 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
     const int qb = unit - bh * p.nqb;
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
-    quantize_block<kBf16, D, kQueryBlock, false, D>(
+    quantize_block<kBf16, D, kQueryBlock, false, D, kQueryScaleSlots>(
         p.query, b, h, qb * kQueryBlock, p.query_length, nullptr,
-        p.query_code + (static_cast<long>(bh) * p.sq32 + qb * kQueryBlock) * D, p.query_scale + unit);
+        p.query_code + (static_cast<long>(bh) * p.sq32 + qb * kQueryBlock) * D,
+        p.query_scale + static_cast<long>(unit) * kQueryScaleSlots, p.per_thread);
     return;
   }
   if (block < p.q_blocks_wg + p.k_blocks_wg) {
@@ -253,8 +286,9 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
     int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * kv_tile_bytes(D);
-    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D)>(p.key, b, h, kb * kKeyBlock, p.key_length,
-                                              p.key_mean + static_cast<long>(bh) * D, tile, p.key_scale + unit);
+    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots>(
+        p.key, b, h, kb * kKeyBlock, p.key_length, p.key_mean + static_cast<long>(bh) * D, tile,
+        p.key_scale + static_cast<long>(unit) * kKeyScaleSlots, p.per_thread);
     return;
   }
 
@@ -371,8 +405,9 @@ __global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParam
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
     int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * sage_tile_bytes(D);
-    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D)>(p.key, b, h, kb * kKeyBlock, p.key_length,
-                                              p.key_mean + static_cast<long>(bh) * D, tile, p.key_scale + unit);
+    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), 1>(p.key, b, h, kb * kKeyBlock, p.key_length,
+                                                 p.key_mean + static_cast<long>(bh) * D, tile, p.key_scale + unit,
+                                                 false);
     return;
   }
 

@@ -180,10 +180,13 @@ __device__ __forceinline__ void issue_query_loads(const Params& p, int bh, int q
 
 // Part 2, after the wait: the wave's 32-row query block quantised in registers exactly as the
 // prep kernel does it (sage/reference.py:61-77: one scale amax / 127 + 1e-7 over the
-// zero-padded 32 x D block, codes round-half-even(x / scale) clamped to +-127).  The block amax
-// is a wave-wide max; the 16 codes of each chunk are packed in element order, the layout of
-// the prepared code rows.  Returns the scale.
-template <int D, class Params>
+// zero-padded 32 x D block, codes round-half-even(x / scale) clamped to +-127; with kPerThread,
+// sage/reference.py:23-39: one scale per thread group of rows {t, t+8, t+16, t+24}).  The
+// amax is a wave-wide max (per block) or a max over the 8 lanes holding the group's rows (lane
+// (n, h) holds row q0 + n, so the lanes whose index agrees in its low three bits); the 16 codes
+// of each chunk are packed in element order, the layout of the prepared code rows.  Returns the
+// scale of this lane's query row.
+template <int D, bool kPerThread = false, class Params>
 __device__ __forceinline__ float quantize_query_block(const Params& p, int q0, int n, const v4i (&raw)[D / 16],
                                                      v4i (&qf)[D / 32]) {
   constexpr int kChunksD = D / 32;
@@ -200,7 +203,13 @@ __device__ __forceinline__ float quantize_query_block(const Params& p, int q0, i
   for (int i = 0; i < 2 * kChunksD; ++i)
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[i][e]));
-  amax = wave_max(amax);
+  if constexpr (kPerThread) {
+    amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  } else {
+    amax = wave_max(amax);
+  }
   const float scale = scale_from_amax(amax);
   const Divisor divisor(scale);
 #pragma unroll

@@ -16,9 +16,11 @@ import torch  # noqa: F401  (load torch's HIP runtime first; see module docstrin
 
 from .build import LIBRARY_PATH
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 QUERY_BLOCK = 32
 KEY_BLOCK = 64
+QUERY_SCALE_SLOTS = 8  # per 32-row Q block: one per thread group (per-block prep repeats its scale)
+KEY_SCALE_SLOTS = 4  # per 64-row K block
 
 FLOAT16 = 0
 BFLOAT16 = 1
@@ -38,6 +40,8 @@ EXPORTED_SYMBOLS = (
 )
 
 PREPARE_SKIP_QUERY = 1  # piper_prepare_args.flags
+PREPARE_QK_PER_THREAD = 2
+ATTENTION_QK_PER_THREAD = 1  # piper_attention_args.flags / piper_attention_fused_args.flags
 
 # piper_mfma_probe kinds, workgroup size and operations per MFMA (PIPER_MFMA_PROBE_* in the header)
 MFMA_PROBE_I8 = 0
@@ -138,7 +142,7 @@ class PiperAttentionArgs(ctypes.Structure):
         ("plan", _i32),
         ("shape", PiperShape),
         ("scale", ctypes.c_float),
-        ("reserved", _i32),
+        ("flags", _i32),
         ("prepared", PiperPrepared),
         ("output", _ptr),
     ]
@@ -152,6 +156,8 @@ class PiperAttentionFusedArgs(ctypes.Structure):
         ("is_causal", _i32),
         ("plan", _i32),
         ("scale", ctypes.c_float),
+        ("flags", _i32),
+        ("reserved", _i32),
         ("shape", PiperShape),
         ("query", PiperTensor),
         ("prepared", PiperPrepared),

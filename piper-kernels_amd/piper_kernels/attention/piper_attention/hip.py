@@ -28,8 +28,10 @@ class PreparedPiperAttention:
     """Quantised operands (layouts documented in ``include/piper_mi355x.h``)."""
 
     query_code: torch.Tensor | None  # int8 [B, H, Sq32, D]; None when the kernel quantises Q
-    query_scale: torch.Tensor | None  # fp32 [B, H, Sq32/32]; None when the kernel quantises Q
-    key_scale: torch.Tensor  # fp32 [B, H, Sk64/64]
+    # fp32 [B, H, Sq32/32, 8]: per 32-row block, the scale of each thread group t (rows t, t+8,
+    # t+16, t+24); per_warp repeats the block scale.  None when the kernel quantises Q
+    query_scale: torch.Tensor | None
+    key_scale: torch.Tensor  # fp32 [B, H, Sk64/64, 4]: per 64-row block and thread group
     value_scale: torch.Tensor  # fp32 [B, H, Sk64]
     key_mean: torch.Tensor  # fp32 [B, H, D]
     value_mean: torch.Tensor  # fp32 [B, H, D]
@@ -40,6 +42,7 @@ class PreparedPiperAttention:
     is_causal: bool
     plan: MI355XPlan
     query: torch.Tensor | None = None  # [B, H, Sq, D] input, kept for the fused launch
+    qk_granularity: str = "per_warp"  # the reference's Q/K scale granularity (sage/reference.py:80-108)
 
     @property
     def fused_query(self) -> bool:
@@ -69,8 +72,9 @@ class PreparedPiperAttention:
         return rows[..., :d].contiguous().view(torch.int8).reshape(b, h, -1, d)
 
     def key_tile_scale(self) -> torch.Tensor:
-        """Copy of each tile's K scale kept in the padding of its first K row: [B, H, nkb]."""
-        return self._region("key_scale", 4).contiguous().view(torch.float32).flatten(2)
+        """Copy of each tile's four K scale slots kept in the padding of its first K row:
+        [B, H, nkb, 4]."""
+        return self._region("key_scale", 4 * native.KEY_SCALE_SLOTS).contiguous().view(torch.float32)
 
     def value_code_transposed(self) -> torch.Tensor:
         """V codes as stored: [B, H, Sk64/64, D, 64]."""
@@ -112,13 +116,21 @@ def _prepare_piper_attention(
     plan: MI355XPlan | None = None,
     workspace: torch.Tensor | None = None,
     quantize_query: bool = True,
+    qk_granularity: str = "per_warp",
 ) -> PreparedPiperAttention:
     """Quantise Q/K/V on the GPU (one HIP prep pipeline) and allocate the output.
 
     With ``quantize_query=False`` only K and V are quantised and the bundle keeps the query
     itself: ``_launch_piper_attention`` then runs the fused entry point, whose kernel
     quantises each query block in its prologue (bit-identical codes and scales).
+    ``qk_granularity`` is the reference's ``quantize_query_key`` granularity
+    (``sage/reference.py:80-108``): ``"per_warp"`` (one scale per 32-row Q / 64-row K block, the
+    reference's grouped GPU path) or ``"per_thread"`` (its portable path's default: 8 scales per
+    Q block, 4 per K block, over interleaved rows).
     """
+    if qk_granularity not in ("per_warp", "per_thread"):
+        raise ValueError(f"unknown Q/K quantization granularity: {qk_granularity}")
+    per_thread = qk_granularity == "per_thread"
     lib = native.load_library()
     batch, heads, sq, d = query.shape
     sk = key.shape[2]
@@ -136,8 +148,12 @@ def _prepare_piper_attention(
 
     prepared = PreparedPiperAttention(
         query_code=empty((batch, heads, sq32, d), torch.int8) if quantize_query else None,
-        query_scale=empty((batch, heads, sq32 // native.QUERY_BLOCK), torch.float32) if quantize_query else None,
-        key_scale=empty((batch, heads, nkb), torch.float32),
+        query_scale=(
+            empty((batch, heads, sq32 // native.QUERY_BLOCK, native.QUERY_SCALE_SLOTS), torch.float32)
+            if quantize_query
+            else None
+        ),
+        key_scale=empty((batch, heads, nkb, native.KEY_SCALE_SLOTS), torch.float32),
         value_scale=empty((batch, heads, sk64), torch.float32),
         key_mean=empty((batch, heads, d), torch.float32),
         value_mean=empty((batch, heads, d), torch.float32),
@@ -147,6 +163,7 @@ def _prepare_piper_attention(
         scale=float(scale),
         is_causal=bool(is_causal),
         plan=plan,
+        qk_granularity=qk_granularity,
     )
     query, q_arg = _native_input(query)
     if not quantize_query:
@@ -159,7 +176,7 @@ def _prepare_piper_attention(
         abi_version=native.ABI_VERSION,
         dtype=_DTYPE_CODES[query.dtype],
         is_causal=int(bool(is_causal)),
-        flags=0 if quantize_query else native.PREPARE_SKIP_QUERY,
+        flags=(0 if quantize_query else native.PREPARE_SKIP_QUERY) | (native.PREPARE_QK_PER_THREAD if per_thread else 0),
         shape=shape,
         query=q_arg,
         key=k_arg,
@@ -191,6 +208,7 @@ def _launch_piper_attention(
     if out.shape != (batch, heads, sq, d) or not out.is_contiguous() or out.dtype not in _DTYPE_CODES:
         raise ValueError("output must be a contiguous [B, H, Sq, D] float16/bfloat16/float32 tensor")
     device = out.device
+    flags = native.ATTENTION_QK_PER_THREAD if prepared.qk_granularity == "per_thread" else 0
     if prepared.fused_query:
         query = prepared.query
         fused = native.PiperAttentionFusedArgs(
@@ -200,6 +218,8 @@ def _launch_piper_attention(
             is_causal=int(prepared.is_causal),
             plan=prepared.plan.plan_id,
             scale=ctypes.c_float(prepared.scale).value,
+            flags=flags,
+            reserved=0,
             shape=_native_shape(batch, heads, sq, sk, d),
             query=native.PiperTensor(query.data_ptr(), *query.stride()[:3]),
             prepared=prepared.native_prepared(),
@@ -217,7 +237,7 @@ def _launch_piper_attention(
         plan=prepared.plan.plan_id,
         shape=_native_shape(batch, heads, sq, sk, d),
         scale=ctypes.c_float(prepared.scale).value,
-        reserved=0,
+        flags=flags,
         prepared=prepared.native_prepared(),
         output=out.data_ptr(),
     )
@@ -235,10 +255,13 @@ def _run_piper_attention(
     *,
     plan: MI355XPlan | None = None,
     fuse_query: bool = True,
+    qk_granularity: str = "per_warp",
 ) -> torch.Tensor:
     """The operator: prep of K and V, then the attention kernel, which quantises the query in
     its prologue (``fuse_query=False``: the prep quantises Q too; the output is the same)."""
-    prepared = _prepare_piper_attention(query, key, value, scale, is_causal, plan=plan, quantize_query=not fuse_query)
+    prepared = _prepare_piper_attention(
+        query, key, value, scale, is_causal, plan=plan, quantize_query=not fuse_query, qk_granularity=qk_granularity
+    )
     return _launch_piper_attention(prepared)
 
 

@@ -42,12 +42,19 @@ def load_golden(path: Path) -> dict:
     return data
 
 
-def gpu_prepare(q, k, v, scale, is_causal, device, plan=None, quantize_query=True):
+def gpu_prepare(q, k, v, scale, is_causal, device, plan=None, quantize_query=True, qk_granularity="per_warp"):
     from piper_kernels.attention.piper_attention.hip import _prepare_piper_attention
 
     with torch.no_grad():
         prepared = _prepare_piper_attention(
-            q.to(device), k.to(device), v.to(device), scale, is_causal, plan=plan, quantize_query=quantize_query
+            q.to(device),
+            k.to(device),
+            v.to(device),
+            scale,
+            is_causal,
+            plan=plan,
+            quantize_query=quantize_query,
+            qk_granularity=qk_granularity,
         )
     torch.cuda.synchronize(device)
     return prepared
@@ -69,9 +76,9 @@ def prepared_numpy(prepared) -> dict:
     vcode = vcode.transpose(0, 1, 2, 4, 3).reshape(b, h, -1, d)
     return {
         "query_code_padded": prepared.query_code.cpu().numpy(),
-        "query_block_scale": prepared.query_scale.cpu().numpy(),
+        "query_slot_scale": None if prepared.query_scale is None else prepared.query_scale.cpu().numpy(),
         "key_code_padded": prepared.key_code().cpu().numpy(),
-        "key_block_scale": prepared.key_scale.cpu().numpy(),
+        "key_slot_scale": prepared.key_scale.cpu().numpy(),
         "key_tile_scale": prepared.key_tile_scale().cpu().numpy(),
         "value_code_padded": vcode,
         "value_scale_padded": prepared.value_scale.cpu().numpy(),
@@ -89,18 +96,26 @@ def _bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
     return a.shape == b.shape and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
 
 
+def _slots(expected: dict, name: str, slots: int) -> np.ndarray:
+    """The scale slots the prep stores per block: the oracle's per-thread-group scales, or the
+    per-block scale repeated (golden fixtures hold only the per-block ones)."""
+    if f"{name}_slot_scale" in expected:
+        return expected[f"{name}_slot_scale"]
+    return np.repeat(np.asarray(expected[f"{name}_block_scale"])[..., None], slots, axis=-1)
+
+
 def assert_prep_bit_exact(got: dict, expected: dict, shape, is_causal: bool) -> None:
     """Every code, scale and mean equal bit for bit; padding as documented in the header."""
     b, h, sq, sk, d = shape
     qc = got["query_code_padded"]
     assert np.array_equal(qc[:, :, :sq], expected["query_code"]), "query codes differ"
     assert not qc[:, :, sq:].any(), "query padding rows must be zero"
-    assert _bits_equal(got["query_block_scale"], expected["query_block_scale"]), "query scales differ"
+    assert _bits_equal(got["query_slot_scale"], _slots(expected, "query", 8)), "query scales differ"
     kc = got["key_code_padded"]
     assert np.array_equal(kc[:, :, :sk], expected["key_code"]), "key codes differ"
     assert not kc[:, :, sk:].any(), "key padding rows must be zero"
-    assert _bits_equal(got["key_block_scale"], expected["key_block_scale"]), "key scales differ"
-    assert _bits_equal(got["key_tile_scale"], expected["key_block_scale"]), "tile copies of the key scales differ"
+    assert _bits_equal(got["key_slot_scale"], _slots(expected, "key", 4)), "key scales differ"
+    assert _bits_equal(got["key_tile_scale"], _slots(expected, "key", 4)), "tile copies of the key scales differ"
     assert _bits_equal(got["key_mean"], expected["key_mean"]), "key means differ"
     assert _bits_equal(got["value_mean"], expected["value_mean"]), "value means differ"
     if is_causal:

@@ -92,6 +92,45 @@ def test_random_shapes_match_oracle(shape, gfx950_device) -> None:
     assert_attention_close(out32, expected, f"random {shape}", key_length=sk)
 
 
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(str(x) for x in s[:5]) + f"-{s[5]}-c{int(s[6])}")
+def test_per_thread_granularity_matches_oracle(shape, gfx950_device) -> None:
+    """The reference portable path's default Q/K granularity (reference.py:42, "per_thread":
+    sage/reference.py:23-58): codes and every thread-group scale bit for bit, the output within
+    the same tolerance, against the oracle's per_thread restatement."""
+    b, h, sq, sk, d, dtype, causal = shape
+    log(f"[case] per_thread {shape}")
+    g = torch.Generator().manual_seed(2000 + sq + sk + d)
+    # every thread group gets its own magnitude, so a scale read from the wrong group shows:
+    # query row r scaled by 1 + (r % 8) / 8 (group r % 8), key row r by 1 + ((r % 8) // 2) / 4
+    q_rows = 1 + (torch.arange(sq) % 8).reshape(1, 1, sq, 1) / 8
+    k_rows = 1 + (torch.arange(sk) % 8 // 2).reshape(1, 1, sk, 1) / 4
+    q = (torch.randn((b, h, sq, d), generator=g) * q_rows).to(dtype)
+    k = (torch.randn((b, h, sk, d), generator=g) * k_rows + torch.randn((b, h, 1, d), generator=g)).to(dtype)
+    v = (torch.randn((b, h, sk, d), generator=g) + 2 * torch.randn((b, h, 1, d), generator=g)).to(dtype)
+    scale = d**-0.5
+    prep = oracle.prepare(q, k, v, causal, "per_thread")
+    prepared = gpu_prepare(q, k, v, scale, causal, gfx950_device, qk_granularity="per_thread")
+    assert_prep_bit_exact(prepared_numpy(prepared), prep, prepared.shape, causal)
+    expected = oracle.attention_from_prepared(prep, scale, causal)
+    out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
+    assert_attention_close(out32, expected, f"per_thread {shape}", key_length=sk)
+    # the fused entry point quantises the query per thread group in its prologue, bit-identically
+    fused = gpu_prepare(q, k, v, scale, causal, gfx950_device, quantize_query=False, qk_granularity="per_thread")
+    assert torch.equal(gpu_attention(fused, torch.float32).cpu(), torch.from_numpy(out32))
+
+
+@pytest.mark.parametrize("fixture", FIXTURES, ids=[p.stem for p in FIXTURES])
+def test_per_thread_output_matches_golden_fixture(fixture, gfx950_device) -> None:
+    g = load_golden(fixture)
+    log(f"[case] per_thread golden {fixture.stem}")
+    prepared = gpu_prepare(
+        g["query"], g["key"], g["value"], g["scale"], g["is_causal"], gfx950_device, quantize_query=False,
+        qk_granularity="per_thread",
+    )
+    out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
+    assert_attention_close(out32, g["output_per_thread"], f"{fixture.stem} per_thread", key_length=g["key"].shape[2])
+
+
 MEAN_CASES = [
     # (workload, batches, heads): head subsets of the BASELINE configurations at their full S
     ("c2", None, [0, 7, 23]),

@@ -86,8 +86,9 @@ def test_prepared_layout_sizes(lib, shape) -> None:
     layout = lib.prepared_layout(native.PiperShape(*shape))
     sq32, sk64 = -(-sq // 32) * 32, -(-sk // 64) * 64
     assert layout.query_code_bytes == b * h * sq32 * d
-    assert layout.query_scale_bytes == b * h * (sq32 // 32) * 4
-    assert layout.key_scale_bytes == b * h * (sk64 // 64) * 4
+    # one scale slot per thread group of the per_thread granularity: 8 per Q block, 4 per K block
+    assert layout.query_scale_bytes == b * h * (sq32 // 32) * 8 * 4
+    assert layout.key_scale_bytes == b * h * (sk64 // 64) * 4 * 4
     assert layout.value_scale_bytes == b * h * sk64 * 4
     assert layout.mean_bytes == b * h * d * 4
     # one record per 64-key tile, laid out as the attention kernel's LDS stage: K rows of D + 16
@@ -144,6 +145,10 @@ def test_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward(args, 0)
     args.plan = 0
+    args.flags = 2
+    with pytest.raises(RuntimeError, match="unknown flags"):
+        lib.attention_forward(args, 0)
+    args.flags = native.ATTENTION_QK_PER_THREAD
     with pytest.raises(RuntimeError, match="NULL"):
         lib.attention_forward(args, 0)
     args.is_causal = 1
@@ -154,8 +159,13 @@ def test_attention_validates_before_launching(lib) -> None:
 
 def test_prepare_flags(lib) -> None:
     args = native.PiperPrepareArgs(abi_version=native.ABI_VERSION, dtype=native.FLOAT16, shape=native.PiperShape(1, 1, 8, 8, 64))
-    args.flags = 2
-    with pytest.raises(RuntimeError, match="unknown flags"):
+    for flags in (4, 8, native.PREPARE_SKIP_QUERY | 4):
+        args.flags = flags
+        with pytest.raises(RuntimeError, match="unknown flags"):
+            lib.prepare(args, 0)
+    # the per-thread-group granularity is a known flag: validation goes on to the pointers
+    args.flags = native.PREPARE_QK_PER_THREAD
+    with pytest.raises(RuntimeError, match="query pointer is NULL"):
         lib.prepare(args, 0)
     # skipping the query: its (NULL) pointer is not inspected, the key's is
     args.flags = native.PREPARE_SKIP_QUERY
@@ -201,7 +211,10 @@ def test_fused_attention_validates_before_launching(lib) -> None:
     args.plan = 16
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward_fused(args, 0)
-    args.plan, args.abi_version = 0, 2
+    args.plan, args.flags = 0, 4
+    with pytest.raises(RuntimeError, match="unknown flags"):
+        lib.attention_forward_fused(args, 0)
+    args.flags, args.abi_version = native.ATTENTION_QK_PER_THREAD, native.ABI_VERSION + 1
     with pytest.raises(RuntimeError, match="ABI version mismatch"):
         lib.attention_forward_fused(args, 0)
 
