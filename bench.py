@@ -55,6 +55,12 @@ def parse_args() -> argparse.Namespace:
         "--two-step", action="store_true", help="time the prep of Q, K, V + attention on prepared query codes"
     )
     parser.add_argument(
+        "--qk-granularity",
+        choices=["per_thread", "per_warp"],
+        default="per_thread",
+        help="Q/K scale granularity (the operator's default: per_thread, as the reference's portable path)",
+    )
+    parser.add_argument(
         "--operator",
         choices=["piper_attention", "sage_attention_2pp"],
         default="piper_attention",
@@ -152,7 +158,9 @@ def main() -> int:
         launch = _launch_piper_attention
 
         def prepare():
-            return _prepare_piper_attention(q, k, v, scale, workload.is_causal, quantize_query=args.two_step)
+            return _prepare_piper_attention(
+                q, k, v, scale, workload.is_causal, quantize_query=args.two_step, qk_granularity=args.qk_granularity
+            )
 
     def step(events=None):
         if events is not None:
@@ -254,6 +262,7 @@ def main() -> int:
         result["dtype"] = "int8 QK, fp8 e4m3 PV"
     else:
         result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
+        result["config"]["qk_granularity"] = args.qk_granularity
     # the sustained dense MFMA rate of this GPU (library probe, after the timed region)
     from piper_kernels._hip import library as native
     from piper_kernels.measure import measure_mfma_peak

@@ -42,7 +42,7 @@ class PreparedPiperAttention:
     is_causal: bool
     plan: MI355XPlan
     query: torch.Tensor | None = None  # [B, H, Sq, D] input, kept for the fused launch
-    qk_granularity: str = "per_warp"  # the reference's Q/K scale granularity (sage/reference.py:80-108)
+    qk_granularity: str = "per_thread"  # the reference's Q/K scale granularity (sage/reference.py:80-108)
 
     @property
     def fused_query(self) -> bool:
@@ -116,7 +116,7 @@ def _prepare_piper_attention(
     plan: MI355XPlan | None = None,
     workspace: torch.Tensor | None = None,
     quantize_query: bool = True,
-    qk_granularity: str = "per_warp",
+    qk_granularity: str = "per_thread",
 ) -> PreparedPiperAttention:
     """Quantise Q/K/V on the GPU (one HIP prep pipeline) and allocate the output.
 
@@ -124,9 +124,10 @@ def _prepare_piper_attention(
     itself: ``_launch_piper_attention`` then runs the fused entry point, whose kernel
     quantises each query block in its prologue (bit-identical codes and scales).
     ``qk_granularity`` is the reference's ``quantize_query_key`` granularity
-    (``sage/reference.py:80-108``): ``"per_warp"`` (one scale per 32-row Q / 64-row K block, the
-    reference's grouped GPU path) or ``"per_thread"`` (its portable path's default: 8 scales per
-    Q block, 4 per K block, over interleaved rows).
+    (``sage/reference.py:80-108``): ``"per_thread"`` (the default, as in its portable path --
+    ``reference.py:42`` -- which is what the reference runs on MI355X: 8 scales per Q block, 4
+    per K block, over interleaved rows) or ``"per_warp"`` (one scale per 32-row Q / 64-row K
+    block, its grouped SM12x Triton path).
     """
     if qk_granularity not in ("per_warp", "per_thread"):
         raise ValueError(f"unknown Q/K quantization granularity: {qk_granularity}")
@@ -255,10 +256,11 @@ def _run_piper_attention(
     *,
     plan: MI355XPlan | None = None,
     fuse_query: bool = True,
-    qk_granularity: str = "per_warp",
+    qk_granularity: str = "per_thread",
 ) -> torch.Tensor:
     """The operator: prep of K and V, then the attention kernel, which quantises the query in
-    its prologue (``fuse_query=False``: the prep quantises Q too; the output is the same)."""
+    its prologue (``fuse_query=False``: the prep quantises Q too; the output is the same).
+    Q/K scales per thread group by default, the granularity of the reference's portable path."""
     prepared = _prepare_piper_attention(
         query, key, value, scale, is_causal, plan=plan, quantize_query=not fuse_query, qk_granularity=qk_granularity
     )
