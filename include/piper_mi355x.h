@@ -226,7 +226,7 @@ typedef struct piper_attention_fused_args {
  *
  * Tile record (PIPER_SAGE_TILE_BYTES(D) bytes per 64 keys, the kernel's LDS stage image):
  *   [0, PIPER_SAGE_V_OFFSET(D))  int8 K codes [64][D] in rows of D + 16 bytes; bytes
- *                                [D, D + 4) of row 0 hold the tile's K scale (float)
+ *                                [D, D + 16) of row 0 hold the tile's 4 K scale slots (float)
  *   [PIPER_SAGE_V_OFFSET(D), +80 * D)  FP8 E4M3 V^T codes [D][64] in rows of 80 bytes
  *   padding to a KiB multiple; padding bytes are unspecified.
  * ------------------------------------------------------------------------------------- */
@@ -234,7 +234,7 @@ typedef struct piper_attention_fused_args {
 #define PIPER_SAGE_TILE_BYTES(head_dim) ((PIPER_SAGE_V_OFFSET(head_dim) + 80 * (head_dim) + 1023) / 1024 * 1024)
 
 typedef struct piper_sage_prepared {
-  float* key_scale;   /* [B, H, Sk64/64] INT8 K scales */
+  float* key_scale;   /* [B, H, Sk64/64, 4] INT8 K scales (PIPER_KEY_SCALE_SLOTS, as piper_prepared) */
   float* key_mean;    /* [B, H, D] the K smoothing mean (torch's CPU order, as piper_prepared) */
   float* value_scale; /* [B, H, D] FP8 V scales, per channel */
   void* kv_tiles;     /* [B, H, Sk64/64] tile records, 16-byte aligned */
@@ -251,8 +251,8 @@ typedef struct piper_sage_layout {
 typedef struct piper_sage_prepare_args {
   int32_t abi_version; /* PIPER_ABI_VERSION */
   int32_t dtype;       /* PIPER_FLOAT16 or PIPER_BFLOAT16: dtype of key and value */
-  int32_t reserved0;
-  int32_t reserved1;
+  int32_t flags;       /* 0 or PIPER_PREPARE_QK_PER_THREAD (K scales per thread group) */
+  int32_t reserved;    /* 0 */
   piper_shape shape;   /* query_length is not used by the prep */
   piper_tensor key;
   piper_tensor value;
@@ -268,6 +268,9 @@ typedef struct piper_sage_attention_args {
   int32_t is_causal;
   int32_t plan;         /* OR of PIPER_PLAN_* bits (the same launch plans) */
   float scale;          /* softmax scale, finite and > 0 */
+  int32_t flags;        /* PIPER_ATTENTION_QK_PER_THREAD after a per-thread-group K prep: the
+                           query is quantised per thread group as well */
+  int32_t reserved;     /* 0 */
   piper_shape shape;
   piper_tensor query;   /* [B, H, Sq, D], the layout rules of piper_prepare_args.query */
   piper_sage_prepared prepared; /* from piper_sage_prepare */

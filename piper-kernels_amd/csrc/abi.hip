@@ -262,7 +262,7 @@ int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layo
   const int64_t d = shape->head_dim;
   const int64_t nkb = ceil_div(shape->key_length, PIPER_KEY_BLOCK);
   const int64_t chunks = piper::cascade_chunks(static_cast<int>(shape->key_length));
-  layout->key_scale_bytes = bh * nkb * 4;
+  layout->key_scale_bytes = bh * nkb * PIPER_KEY_SCALE_SLOTS * 4;
   layout->mean_bytes = bh * d * 4;
   layout->kv_tile_bytes = PIPER_SAGE_TILE_BYTES(d);
   layout->kv_tiles_bytes = bh * nkb * PIPER_SAGE_TILE_BYTES(d);
@@ -279,6 +279,7 @@ int piper_sage_prepare(const piper_sage_prepare_args* a, void* stream) {
   if (a->dtype != PIPER_FLOAT16 && a->dtype != PIPER_BFLOAT16)
     return fail(PIPER_ERROR_UNSUPPORTED, "input dtype must be float16 or bfloat16");
   if (int st = check_shape(&a->shape)) return st;
+  if ((a->flags & ~PIPER_PREPARE_QK_PER_THREAD) != 0) return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   if (int st = check_input("key", a->key)) return st;
   if (int st = check_input("value", a->value)) return st;
   const piper_sage_prepared& o = a->prepared;
@@ -325,6 +326,7 @@ int piper_sage_prepare(const piper_sage_prepare_args* a, void* stream) {
   qp.value_scale = o.value_scale;
   qp.key_scale = o.key_scale;
   qp.kv_tiles = static_cast<uint8_t*>(o.kv_tiles);
+  qp.per_thread = (a->flags & PIPER_PREPARE_QK_PER_THREAD) ? 1 : 0;
 
   const hipError_t err =
       piper::launch_sage_prep(a->dtype == PIPER_BFLOAT16, static_cast<int>(s.head_dim), mp, qp, static_cast<hipStream_t>(stream));
@@ -349,6 +351,8 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   if (!(std::isfinite(a->scale) && a->scale > 0.0f))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
   if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
+  if ((a->flags & ~PIPER_ATTENTION_QK_PER_THREAD) != 0)
+    return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   if (int st = check_input("query", a->query)) return st;
   const piper_sage_prepared& o = a->prepared;
   if (!o.value_scale || !o.kv_tiles || !a->output)
@@ -373,6 +377,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   sp.causal_forward = (a->plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
   sp.xcd_remap = (a->plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
   sp.causal_interleave = (a->plan & PIPER_PLAN_CAUSAL_INTERLEAVE) ? 1 : 0;
+  sp.per_thread = (a->flags & PIPER_ATTENTION_QK_PER_THREAD) ? 1 : 0;
   if (static_cast<int64_t>(sp.query_tiles) * sp.batch_heads > 0x7fffffff)
     return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
 

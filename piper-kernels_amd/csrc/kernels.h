@@ -150,8 +150,9 @@ struct SageQuantParams {
   int v_blocks_wg;
   const float* key_mean;
   const float* value_scale;
-  float* key_scale;
+  float* key_scale;   // [batch_heads][nkb][kKeyScaleSlots]
   uint8_t* kv_tiles;  // [batch_heads][nkb][sage_tile_bytes(D)]
+  int per_thread;     // 1: K scales per thread group; 0: one per block, repeated in every slot
 };
 
 struct SageParams {
@@ -170,6 +171,7 @@ struct SageParams {
   int causal_forward;
   int xcd_remap;
   int causal_interleave;
+  int per_thread;  // Q/K scales per thread group (the tile's four K slots, per-row-group Q scales)
 };
 
 hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream);

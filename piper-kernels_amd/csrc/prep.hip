@@ -405,9 +405,9 @@ __global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParam
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
     int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * sage_tile_bytes(D);
-    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), 1>(p.key, b, h, kb * kKeyBlock, p.key_length,
-                                                 p.key_mean + static_cast<long>(bh) * D, tile, p.key_scale + unit,
-                                                 false);
+    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots>(
+        p.key, b, h, kb * kKeyBlock, p.key_length, p.key_mean + static_cast<long>(bh) * D, tile,
+        p.key_scale + static_cast<long>(unit) * kKeyScaleSlots, p.per_thread);
     return;
   }
 

@@ -54,13 +54,15 @@ __device__ __forceinline__ uint32_t pack_fp8(float a, float b, float c, float d)
 // Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave,
 // in two parts.  Head: raw scores, masks, block maximum and the frame move (rescale of the
 // accumulators when the running maximum grows; exact, otherwise the weight is 1).  Tail:
-// probabilities, denominator share, FP8 codes and the PV MFMAs.  ct = query scale * key scale
-// * softmax scale * log2 e; mrun is the running maximum (log2 units, per query), den this lane
-// half's share of the denominator; x carries the raw scores from head to tail.
-template <int D, bool kCausal>
-__device__ __forceinline__ void sage_block_head(const v16i (&s)[2], float ct, int t, int q0, int n, int h,
-                                                int key_length, float (&x)[32], v16f (&acc)[D / 32], float& den,
-                                                float& mrun) {
+// probabilities, denominator share, FP8 codes and the PV MFMAs.  ct[g] = query scale * key scale
+// * softmax scale * log2 e for the keys of K thread group g (keys k with (k % 8) / 2 == g; all
+// four equal for per-block K scales); register 4q + i holds key 16h + 4q + i (or 32 + ...), so
+// it belongs to group 2 (q % 2) + i / 2.  mrun is the running maximum (log2 units, per query),
+// den this lane half's share of the denominator; x carries the raw scores from head to tail.
+template <int D, bool kCausal, bool kPerThread>
+__device__ __forceinline__ void sage_block_head(const v16i (&s)[2], const float (&ct)[4], int t, int q0, int n,
+                                                int h, int key_length, float (&x)[32], v16f (&acc)[D / 32],
+                                                float& den, float& mrun) {
   constexpr int kChunksD = D / 32;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -90,9 +92,22 @@ __device__ __forceinline__ void sage_block_head(const v16i (&s)[2], float ct, in
       }
     }
   }
-  // ct > 0, so the maximum commutes with the scaling: max(RN(x ct)) = RN(max(x) ct)
-  const float raw_max = cross_half_max(max32(x));
-  const float block_max = raw_max * ct - kLog2Of448;
+  // ct > 0, so the maximum commutes with the scaling: max(RN(x ct)) = RN(max(x) ct) -- per K
+  // thread group when the groups have their own scales
+  float block_max;
+  if constexpr (kPerThread) {
+    float gmax[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int r = 4 * (g >> 1) + 2 * (g & 1);  // registers r, r+1, r+8, r+9 of each half
+      gmax[g] = cross_half_max(fmaxf(fmaxf(fmaxf(x[r], x[r + 1]), fmaxf(x[r + 8], x[r + 9])),
+                                     fmaxf(fmaxf(x[16 + r], x[17 + r]), fmaxf(x[24 + r], x[25 + r]))));
+    }
+    block_max = fmaxf(fmaxf(gmax[0] * ct[0], gmax[1] * ct[1]), fmaxf(gmax[2] * ct[2], gmax[3] * ct[3])) -
+                kLog2Of448;
+  } else {
+    block_max = cross_half_max(max32(x)) * ct[0] - kLog2Of448;
+  }
   const float next = fmaxf(mrun, block_max);
   const bool grow = next > mrun;
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -107,8 +122,8 @@ __device__ __forceinline__ void sage_block_head(const v16i (&s)[2], float ct, in
 }
 
 template <int D, int NW>
-__device__ __forceinline__ void sage_block_tail(const char* stage, const float (&x)[32], float ct, int n, int h,
-                                                v16f (&acc)[D / 32], float& den, float mrun) {
+__device__ __forceinline__ void sage_block_tail(const char* stage, const float (&x)[32], const float (&ct)[4], int n,
+                                                int h, v16f (&acc)[D / 32], float& den, float mrun) {
   using L = SageLayout<D, NW>;
   constexpr int kChunksD = D / 32;
   // ---- p = exp2(s ct - m') in [0, 448], the denominator share and the FP8 codes ----
@@ -116,10 +131,11 @@ __device__ __forceinline__ void sage_block_tail(const char* stage, const float (
   uint32_t pw[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const float e0 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 0], ct, -mrun));
-    const float e1 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 1], ct, -mrun));
-    const float e2 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 2], ct, -mrun));
-    const float e3 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 3], ct, -mrun));
+    const float c01 = ct[2 * (q & 1)], c23 = ct[2 * (q & 1) + 1];
+    const float e0 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 0], c01, -mrun));
+    const float e1 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 1], c01, -mrun));
+    const float e2 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 2], c23, -mrun));
+    const float e3 = __builtin_amdgcn_exp2f(fmaf(x[4 * q + 3], c23, -mrun));
     ps[0] += e0;
     ps[1] += e1;
     ps[2] += e2;
@@ -148,7 +164,7 @@ __device__ __forceinline__ void sage_block_tail(const char* stage, const float (
 constexpr int kSageStages = 6;
 constexpr int kSageLead = 4;
 
-template <int D, int NW, bool kCausal, bool kBarrier>
+template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
 __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                           int wave, int lane, const v4i (&qf)[D / 32], float cq, int q0, int n,
                                           int h, int krow, const v16i& bias, const v16i (&s_cur)[2],
@@ -158,20 +174,30 @@ __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t
                 lane);
   if (t < wave_tiles) {
     const char* stage = smem + (t % kSageStages) * L::kStageBytes;
-    const float ct = cq * *reinterpret_cast<const float*>(stage + D);  // K scale in row 0's padding
+    // the K scales of the tile's four thread groups sit in the padding of K row 0
+    float ct[4];
+    if constexpr (kPerThread) {
+      const float4 ks = *reinterpret_cast<const float4*>(stage + D);
+      ct[0] = cq * ks.x;
+      ct[1] = cq * ks.y;
+      ct[2] = cq * ks.z;
+      ct[3] = cq * ks.w;
+    } else {
+      ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
+    }
     float x[32];
     // the next block's QK MFMAs first: they run under this block's softmax (issuing them after
     // the frame move, or interleaving them with the softmax, measured 1-5% slower; feeding the
     // biased accumulator bits to the exp FMA with a folded constant saves the 32 subtractions
     // but costs register copies and measured 3% slower)
     block_scores<D, L>(smem + ((t + 1) % kSageStages) * L::kStageBytes, qf, h, krow, bias, s_next);
-    sage_block_head<D, kCausal>(s_cur, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
+    sage_block_head<D, kCausal, kPerThread>(s_cur, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
     sage_block_tail<D, NW>(stage, x, ct, n, h, acc, den, mrun);
   }
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }
 
-template <int D, int NW, bool kCausal, int kOut>
+template <int D, int NW, bool kCausal, int kOut, bool kPerThread>
 __global__ void __launch_bounds__(NW * 64, 1) sage_attention_kernel(const SageParams p) {
   using L = SageLayout<D, NW>;
   constexpr int kChunksD = D / 32;
@@ -211,7 +237,7 @@ __global__ void __launch_bounds__(NW * 64, 1) sage_attention_kernel(const SagePa
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kSageLead * (L::kRounds - 1)) : "memory");
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
-    cq = quantize_query_block<D>(p, q0, n, raw, qf) * p.scale_log2e;
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * p.scale_log2e;
   } else {
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
@@ -236,13 +262,13 @@ __global__ void __launch_bounds__(NW * 64, 1) sage_attention_kernel(const SagePa
 
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    sage_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
+    sage_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
                                      s_a, s_b, acc, den, mrun);
-    sage_step<D, NW, kCausal, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
+    sage_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
                                     s_b, s_a, acc, den, mrun);
   }
   if (t < tiles)
-    sage_step<D, NW, kCausal, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
+    sage_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
                                      s_a, s_b, acc, den, mrun);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may outlive the waves
 
@@ -265,22 +291,28 @@ __global__ void __launch_bounds__(NW * 64, 1) sage_attention_kernel(const SagePa
   }
 }
 
-template <int D, int NW, bool kCausal>
+template <int D, int NW, bool kCausal, bool kPerThread>
 static hipError_t sage_launch_out(int out_dtype, const SageParams& sp, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(sp.query_tiles * sp.batch_heads));
   const dim3 block(NW * 64);
   switch (out_dtype) {
-    case 0: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 0>), grid, block, 0, stream, sp); break;
-    case 1: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 1>), grid, block, 0, stream, sp); break;
-    default: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 2>), grid, block, 0, stream, sp); break;
+    case 0: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 0, kPerThread>), grid, block, 0, stream, sp); break;
+    case 1: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 1, kPerThread>), grid, block, 0, stream, sp); break;
+    default: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 2, kPerThread>), grid, block, 0, stream, sp); break;
   }
   return hipGetLastError();
 }
 
+template <int D, int NW, bool kCausal>
+static hipError_t sage_launch_granularity(int out_dtype, const SageParams& sp, hipStream_t stream) {
+  return sp.per_thread ? sage_launch_out<D, NW, kCausal, true>(out_dtype, sp, stream)
+                       : sage_launch_out<D, NW, kCausal, false>(out_dtype, sp, stream);
+}
+
 template <int D, int NW>
 static hipError_t sage_launch_causal(bool causal, int out_dtype, const SageParams& sp, hipStream_t stream) {
-  return causal ? sage_launch_out<D, NW, true>(out_dtype, sp, stream)
-                : sage_launch_out<D, NW, false>(out_dtype, sp, stream);
+  return causal ? sage_launch_granularity<D, NW, true>(out_dtype, sp, stream)
+                : sage_launch_granularity<D, NW, false>(out_dtype, sp, stream);
 }
 
 hipError_t launch_sage_attention(int head_dim, bool causal, int out_dtype, int waves, const SageParams& sp,

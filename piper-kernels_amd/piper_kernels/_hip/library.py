@@ -188,8 +188,8 @@ class PiperSagePrepareArgs(ctypes.Structure):
     _fields_ = [
         ("abi_version", _i32),
         ("dtype", _i32),
-        ("reserved0", _i32),
-        ("reserved1", _i32),
+        ("flags", _i32),
+        ("reserved", _i32),
         ("shape", PiperShape),
         ("key", PiperTensor),
         ("value", PiperTensor),
@@ -207,6 +207,8 @@ class PiperSageAttentionArgs(ctypes.Structure):
         ("is_causal", _i32),
         ("plan", _i32),
         ("scale", ctypes.c_float),
+        ("flags", _i32),
+        ("reserved", _i32),
         ("shape", PiperShape),
         ("query", PiperTensor),
         ("prepared", PiperSagePrepared),

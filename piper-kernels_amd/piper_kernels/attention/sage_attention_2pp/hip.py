@@ -27,7 +27,7 @@ _DTYPE_CODES = {torch.float16: native.FLOAT16, torch.bfloat16: native.BFLOAT16, 
 class PreparedSageAttention2pp:
     """Quantised K/V (layouts documented in ``include/piper_mi355x.h``) and the query itself."""
 
-    key_scale: torch.Tensor  # fp32 [B, H, Sk64/64]
+    key_scale: torch.Tensor  # fp32 [B, H, Sk64/64, 4]: per 64-row block and K thread group
     key_mean: torch.Tensor  # fp32 [B, H, D]
     value_scale: torch.Tensor  # fp32 [B, H, D], per channel
     kv_tiles: torch.Tensor  # uint8 [B, H, Sk64/64, sage_tile_bytes(D)]: K rows, FP8 V^T rows
@@ -37,6 +37,7 @@ class PreparedSageAttention2pp:
     scale: float
     is_causal: bool
     plan: MI355XPlan
+    qk_granularity: str = "per_thread"  # the reference's Q/K scale granularity (sage/reference.py:80-108)
 
     def native_prepared(self) -> native.PiperSagePrepared:
         return native.PiperSagePrepared(
@@ -77,8 +78,15 @@ def _prepare_sage_attention_2pp(
     *,
     plan: MI355XPlan | None = None,
     workspace: torch.Tensor | None = None,
+    qk_granularity: str = "per_thread",
 ) -> PreparedSageAttention2pp:
-    """K/V statistics, INT8 K and FP8 V on the GPU (one HIP prep pipeline); allocate the output."""
+    """K/V statistics, INT8 K and FP8 V on the GPU (one HIP prep pipeline); allocate the output.
+
+    ``qk_granularity``: ``"per_thread"`` (the default of the reference's portable path,
+    ``sage_attention_2pp/reference.py:35``) or ``"per_warp"`` (its grouped SM12x Triton path).
+    """
+    if qk_granularity not in ("per_warp", "per_thread"):
+        raise ValueError(f"unknown Q/K quantization granularity: {qk_granularity}")
     lib = native.load_library()
     batch, heads, sq, d = query.shape
     sk = key.shape[2]
@@ -94,7 +102,7 @@ def _prepare_sage_attention_2pp(
 
     query, _ = _native_input(query)
     prepared = PreparedSageAttention2pp(
-        key_scale=empty((batch, heads, nkb), torch.float32),
+        key_scale=empty((batch, heads, nkb, native.KEY_SCALE_SLOTS), torch.float32),
         key_mean=empty((batch, heads, d), torch.float32),
         value_scale=empty((batch, heads, d), torch.float32),
         kv_tiles=empty((batch, heads, nkb, native.sage_tile_bytes(d)), torch.uint8),
@@ -104,6 +112,7 @@ def _prepare_sage_attention_2pp(
         scale=float(scale),
         is_causal=bool(is_causal),
         plan=plan,
+        qk_granularity=qk_granularity,
     )
     if workspace is None or workspace.numel() < layout.workspace_bytes:
         workspace = empty((max(layout.workspace_bytes, 1),), torch.uint8)
@@ -112,6 +121,7 @@ def _prepare_sage_attention_2pp(
     args = native.PiperSagePrepareArgs(
         abi_version=native.ABI_VERSION,
         dtype=_DTYPE_CODES[key.dtype],
+        flags=native.PREPARE_QK_PER_THREAD if qk_granularity == "per_thread" else 0,
         shape=shape,
         key=k_arg,
         value=v_arg,
@@ -144,6 +154,8 @@ def _launch_sage_attention_2pp(
         is_causal=int(prepared.is_causal),
         plan=prepared.plan.plan_id,
         scale=ctypes.c_float(prepared.scale).value,
+        flags=native.ATTENTION_QK_PER_THREAD if prepared.qk_granularity == "per_thread" else 0,
+        reserved=0,
         shape=native.PiperShape(batch, heads, sq, sk, d),
         query=native.PiperTensor(query.data_ptr(), *query.stride()[:3]),
         prepared=prepared.native_prepared(),
@@ -165,8 +177,9 @@ def _run_sage_attention_2pp(
     is_causal: bool,
     *,
     plan: MI355XPlan | None = None,
+    qk_granularity: str = "per_thread",
 ) -> torch.Tensor:
-    prepared = _prepare_sage_attention_2pp(query, key, value, scale, is_causal, plan=plan)
+    prepared = _prepare_sage_attention_2pp(query, key, value, scale, is_causal, plan=plan, qk_granularity=qk_granularity)
     return _launch_sage_attention_2pp(prepared)
 
 

@@ -34,11 +34,13 @@ MAX_ABS = 5e-3
 COSINE = 0.99999
 
 
-def _prepare(q, k, v, scale, causal, device, plan=None):
+def _prepare(q, k, v, scale, causal, device, plan=None, qk_granularity="per_warp"):
     from piper_kernels.attention.sage_attention_2pp.hip import _prepare_sage_attention_2pp
 
     with torch.no_grad():
-        prepared = _prepare_sage_attention_2pp(q.to(device), k.to(device), v.to(device), scale, causal, plan=plan)
+        prepared = _prepare_sage_attention_2pp(
+            q.to(device), k.to(device), v.to(device), scale, causal, plan=plan, qk_granularity=qk_granularity
+        )
     torch.cuda.synchronize(device)
     return prepared
 
@@ -99,9 +101,9 @@ def test_prep_bit_exact(gfx950_device, case) -> None:
     prepared = _prepare(q, k, v, d**-0.5, causal, gfx950_device)
     expected = oracle.prepare(q, k, v)
     assert _bits_equal(prepared.key_mean.cpu().numpy(), expected["key_mean"]), "key means differ"
-    assert _bits_equal(prepared.key_scale.cpu().numpy(), expected["key_block_scale"]), "key scales differ"
-    tile_scale = prepared.kv_tiles[..., d : d + 4].contiguous().view(torch.float32).flatten(2).cpu().numpy()
-    assert _bits_equal(tile_scale, expected["key_block_scale"]), "tile copies of the key scales differ"
+    assert _bits_equal(prepared.key_scale.cpu().numpy(), expected["key_slot_scale"]), "key scales differ"
+    tile_scale = prepared.kv_tiles[..., d : d + 16].contiguous().view(torch.float32).cpu().numpy()
+    assert _bits_equal(tile_scale, expected["key_slot_scale"]), "tile copies of the key scales differ"
     kc = prepared.key_code().cpu().numpy()
     assert np.array_equal(kc[:, :, :sk], expected["key_code"]), "key codes differ"
     assert not kc[:, :, sk:].any(), "key padding rows must be zero"
@@ -149,7 +151,8 @@ def test_reference_gate(gfx950_device, dtype, head_dim, is_causal) -> None:
         actual = sage_attention_2pp(query.to(gfx950_device), key.to(gfx950_device), value.to(gfx950_device),
                                     is_causal=is_causal)
     expected = piper_oracle.cast_output(
-        oracle.sage_attention_2pp_reference(query, key, value, head_dim**-0.5, is_causal), str(dtype)[6:]
+        oracle.sage_attention_2pp_reference(query, key, value, head_dim**-0.5, is_causal, granularity="per_thread"),
+        str(dtype)[6:],
     )
     error = np.abs(actual.float().cpu().numpy() - expected)
     assert actual.shape == query.shape and actual.dtype is dtype
@@ -206,7 +209,7 @@ def test_quality_against_fp64_sdpa(gfx950_device) -> None:
     with torch.no_grad():
         actual = sage_attention_2pp(q.to(gfx950_device), k.to(gfx950_device), v.to(gfx950_device)).float().cpu().numpy()
     sdpa = piper_oracle.sdpa_float64(q, k, v)
-    reference = oracle.sage_attention_2pp_reference(q, k, v)
+    reference = oracle.sage_attention_2pp_reference(q, k, v, granularity="per_thread")  # the operator's default
     err, ref_err = np.abs(actual - sdpa), np.abs(reference - sdpa)
     log(f"[sage sdpa] max {err.max():.3e} (reference {ref_err.max():.3e}) cos {_cosine(actual, sdpa):.6f}")
     assert err.mean() < 0.01 and err.max() < 0.2
@@ -227,7 +230,7 @@ def test_golden_fixture(gfx950_device, fixture, waves) -> None:
     sk, d = k.shape[2], k.shape[3]
     prepared = _prepare(q, k, v, g["scale"], g["is_causal"], gfx950_device, plan=MI355XPlan(waves=waves))
     assert _bits_equal(prepared.key_mean.cpu().numpy(), g["key_mean"])
-    assert _bits_equal(prepared.key_scale.cpu().numpy(), g["key_block_scale"])
+    assert _bits_equal(prepared.key_scale.cpu().numpy(), np.repeat(g["key_block_scale"][..., None], 4, axis=-1))
     assert _bits_equal(prepared.value_scale.cpu().numpy(), g["value_scale"])
     assert np.array_equal(prepared.key_code().cpu().numpy()[:, :, :sk], g["key_code"])
     assert np.array_equal(prepared.value_code().cpu().numpy()[:, :, :sk], g["value_code"])
@@ -236,3 +239,29 @@ def test_golden_fixture(gfx950_device, fixture, waves) -> None:
     assert err.mean() <= MEAN_ABS and err.max() <= MAX_ABS
     modes = np.abs(g["output_fp32_accumulation"] - g["output_reference"]).mean()
     assert np.abs(actual - g["output_reference"]).mean() <= modes + MEAN_ABS
+
+
+@pytest.mark.parametrize("case", SHAPES, ids=_id)
+def test_per_thread_granularity(gfx950_device, case) -> None:
+    """The default of the reference's portable path (reference.py:35, "per_thread"): K codes and
+    the four K group scales bit for bit, and the output (query quantised per thread group in
+    the prologue) against the oracle's per_thread restatement in the kernel's arithmetic."""
+    shape, dtype, causal = case
+    log(f"[sage per_thread] {shape} {dtype} causal={causal}")
+    b, h, sq, sk, d = shape
+    g = torch.Generator().manual_seed(83)
+    # every thread group its own magnitude: query row r x (1 + (r % 8) / 8), key row r x (1 + ((r % 8) // 2) / 4)
+    q = (torch.randn(b, h, sq, d, generator=g) * (1 + (torch.arange(sq) % 8).reshape(1, 1, sq, 1) / 8)).to(dtype)
+    k = (torch.randn(b, h, sk, d, generator=g) * (1 + (torch.arange(sk) % 8 // 2).reshape(1, 1, sk, 1) / 4)
+         + 0.5 * torch.randn(b, h, 1, d, generator=g)).to(dtype)
+    v = (torch.randn(b, h, sk, d, generator=g) + 2.0 * torch.randn(b, h, 1, d, generator=g)).to(dtype)
+    prepared = _prepare(q, k, v, d**-0.5, causal, gfx950_device, qk_granularity="per_thread")
+    prep = oracle.prepare(q, k, v, "per_thread")
+    assert _bits_equal(prepared.key_scale.cpu().numpy(), prep["key_slot_scale"]), "key scales differ"
+    assert np.array_equal(prepared.key_code().cpu().numpy()[:, :, :sk], prep["key_code"]), "key codes differ"
+    actual = _launch(prepared).cpu().numpy()
+    fp32 = oracle.attention_from_prepared(prep, d**-0.5, causal, accumulate="fp32")
+    err = np.abs(actual - fp32)
+    log(f"   vs fp32-accumulation oracle: mean {err.mean():.2e} max {err.max():.2e}")
+    assert np.isfinite(actual).all()
+    assert err.mean() <= MEAN_ABS and err.max() <= MAX_ABS and _cosine(actual, fp32) >= COSINE

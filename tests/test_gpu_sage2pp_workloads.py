@@ -39,13 +39,15 @@ def _check_heads(name: str, batches: list[int], heads: list[int], row_slices: li
     log(f"[sage case] {name} batches={batches} heads={heads} shape={tuple(q.shape)}")
     prep = oracle.prepare(q, k, v)
     with torch.no_grad():
-        prepared = _prepare_sage_attention_2pp(q.to(device), k.to(device), v.to(device), scale, w.is_causal)
+        prepared = _prepare_sage_attention_2pp(
+            q.to(device), k.to(device), v.to(device), scale, w.is_causal, qk_granularity="per_warp"
+        )
         out32 = torch.empty(q.shape, device=device, dtype=torch.float32)
         _launch_sage_attention_2pp(prepared, output=out32)
     torch.cuda.synchronize(device)
     sk = w.key_length
     assert _bits_equal(prepared.key_mean.cpu().numpy(), prep["key_mean"]), "key means differ"
-    assert _bits_equal(prepared.key_scale.cpu().numpy(), prep["key_block_scale"]), "key scales differ"
+    assert _bits_equal(prepared.key_scale.cpu().numpy(), prep["key_slot_scale"]), "key scales differ"
     assert _bits_equal(prepared.value_scale.cpu().numpy(), prep["value_scale"]), "value scales differ"
     assert np.array_equal(prepared.key_code().cpu().numpy()[:, :, :sk], prep["key_code"]), "key codes differ"
     assert np.array_equal(prepared.value_code().cpu().numpy()[:, :, :sk], prep["value_code"]), "value codes differ"

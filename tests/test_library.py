@@ -227,7 +227,7 @@ def test_sage_prepared_layout_sizes(lib, shape) -> None:
     # K rows of D + 16 bytes, FP8 V^T rows of 80 bytes: 19 KiB (D = 128) and 10 KiB (D = 64)
     assert layout.kv_tile_bytes == native.sage_tile_bytes(d) == {128: 19 * 1024, 64: 10 * 1024}[d]
     assert layout.kv_tiles_bytes == b * h * nkb * layout.kv_tile_bytes
-    assert layout.key_scale_bytes == b * h * nkb * 4
+    assert layout.key_scale_bytes == b * h * nkb * 4 * 4  # four K thread-group slots per block
     assert layout.mean_bytes == b * h * d * 4
     assert layout.workspace_bytes == mean_workspace_bytes(b * h, sk, d)
 
@@ -239,6 +239,10 @@ def test_sage_prepare_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="float16 or bfloat16"):
         lib.sage_prepare(args, 0)
     args.dtype = native.FLOAT16
+    args.flags = 1  # PIPER_PREPARE_SKIP_QUERY means nothing to this prep (it never quantises Q)
+    with pytest.raises(RuntimeError, match="unknown flags"):
+        lib.sage_prepare(args, 0)
+    args.flags = native.PREPARE_QK_PER_THREAD
     with pytest.raises(RuntimeError, match="key pointer is NULL"):
         lib.sage_prepare(args, 0)
     args.key = native.PiperTensor(fake, 512, 512, 64)
@@ -269,7 +273,10 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     args.plan = 16
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.sage_attention_forward(args, 0)
-    args.plan = 0
+    args.plan, args.flags = 0, 2
+    with pytest.raises(RuntimeError, match="unknown flags"):
+        lib.sage_attention_forward(args, 0)
+    args.flags = native.ATTENTION_QK_PER_THREAD
     with pytest.raises(RuntimeError, match="output pointer is NULL"):
         lib.sage_attention_forward(args, 0)
     args.is_causal = 1
