@@ -325,6 +325,14 @@ int piper_sage_attention_forward(const piper_sage_attention_args* args, void* st
 /* Kind VALU with one wave-wide ds_read_b128 (of zeros) after every 8 FMAs: stores the same word
  * as kind VALU; t(VALU_LDS) - t(VALU) is the issue cost of 8 * iterations LDS reads. */
 #define PIPER_MFMA_PROBE_VALU_LDS 6
+/* Conversion checks of the attention kernels' probability codes (`iterations` is not used).  On
+ * entry the 512 words of each workgroup's part of `sink` hold FP32 values; thread t packs values
+ * 4 (t % 128) .. 4 (t % 128) + 3 with the kernel's own packer, the first value in byte 0, and
+ * stores the word over word t.  P_CODES_U8: Piper Attention's UINT8 codes (round half to even,
+ * saturated to [0, 255]; the replaced reference rule is reference.py:104-107), each byte holding
+ * u - 128 as the PV MFMA's signed operand.  P_CODES_FP8: SageAttention2++'s FP8 E4M3 codes. */
+#define PIPER_MFMA_PROBE_P_CODES_U8 7
+#define PIPER_MFMA_PROBE_P_CODES_FP8 8
 #define PIPER_MFMA_PROBE_THREADS 512
 #define PIPER_MFMA_PROBE_OPS(kind) ((kind) == PIPER_MFMA_PROBE_F8 ? 131072 : 65536)
 int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream);

@@ -389,7 +389,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
 }
 
 int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream) {
-  if (kind < PIPER_MFMA_PROBE_I8 || kind > PIPER_MFMA_PROBE_VALU_LDS)
+  if (kind < PIPER_MFMA_PROBE_I8 || kind > PIPER_MFMA_PROBE_P_CODES_FP8)
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown MFMA probe kind %d", kind);
   if (workgroups < 1 || workgroups > 65536 || iterations < 1 || iterations > (1 << 24))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "probe needs 1..65536 workgroups and 1..2^24 iterations, got %d and %d",

@@ -41,14 +41,6 @@ struct TileLayout : StagePieces<kv_tile_bytes(D), NW> {  // the tile record is t
   static constexpr int kCorrOffset = kv_corr_offset(D);  // D ints: biased 128 * colsum
 };
 
-__device__ __forceinline__ uint32_t pack_codes(float e0, float e1, float e2, float e3) {
-  uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(e0, 0, 0u);
-  w = __builtin_amdgcn_cvt_pk_u8_f32(e1, 1, w);
-  w = __builtin_amdgcn_cvt_pk_u8_f32(e2, 2, w);
-  w = __builtin_amdgcn_cvt_pk_u8_f32(e3, 3, w);
-  return w ^ 0x80808080u;  // u - 128 as signed INT8
-}
-
 // Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave.
 // ct[g]: the score multiplier q_scale * k_scale * softmax_scale * log2(e) of key thread group g
 // (keys k with (k % 8) / 2 == g; all four equal for per-block K scales).  Output register r of

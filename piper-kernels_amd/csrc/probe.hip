@@ -23,8 +23,15 @@
 // x = 2^-x, 0.641186; stores the bits of the 16-chain sum).  Kind 6 is kind 2 with a wave-wide
 // ds_read_b128 of zeros after every 8 FMAs (the FMA result word, 64 * iterations, is unchanged):
 // t(6) - t(2) is what 8 * iterations LDS reads add to a VALU-bound wave.
+//
+// Kinds 7 and 8 check conversions rather than time them: on entry, the 512 words of each
+// workgroup's part of `sink` hold FP32 values; thread t packs values 4 (t % 128) .. + 3 with the
+// attention kernels' own probability-code packers (kind 7: Piper Attention's UINT8 codes,
+// stored as u - 128 per byte; kind 8: SageAttention2++'s FP8 E4M3 codes) and stores the word
+// over word t.  `iterations` is not used.
 #include "common.h"
 #include "kernels.h"
+#include "quant.h"
 
 namespace piper {
 
@@ -34,7 +41,13 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 template <int kKind>
 __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* sink, int iterations) {
   uint32_t total = 0;
-  if constexpr (kKind == 0) {
+  if constexpr (kKind == 7 || kKind == 8) {
+    const float* values = reinterpret_cast<const float*>(sink) + static_cast<long>(blockIdx.x) * kProbeThreads;
+    const int i = 4 * (threadIdx.x % (kProbeThreads / 4));
+    const float a = values[i], b = values[i + 1], c = values[i + 2], d = values[i + 3];
+    __syncthreads();  // every read of this workgroup's words precedes every store over them
+    total = kKind == 7 ? pack_codes(a, b, c, d) : pack_fp8(a, b, c, d);
+  } else if constexpr (kKind == 0) {
     v4i a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     asm volatile("" : "+v"(a));  // opaque: the products cannot be folded
     v16i acc[4];
@@ -165,7 +178,9 @@ hipError_t launch_mfma_probe(int kind, int workgroups, int iterations, uint32_t*
     case 3: hipLaunchKernelGGL(mfma_probe_kernel<3>, grid, block, 0, stream, sink, iterations); break;
     case 4: hipLaunchKernelGGL(mfma_probe_kernel<4>, grid, block, 0, stream, sink, iterations); break;
     case 5: hipLaunchKernelGGL(mfma_probe_kernel<5>, grid, block, 0, stream, sink, iterations); break;
-    default: hipLaunchKernelGGL(mfma_probe_kernel<6>, grid, block, 0, stream, sink, iterations); break;
+    case 6: hipLaunchKernelGGL(mfma_probe_kernel<6>, grid, block, 0, stream, sink, iterations); break;
+    case 7: hipLaunchKernelGGL(mfma_probe_kernel<7>, grid, block, 0, stream, sink, iterations); break;
+    default: hipLaunchKernelGGL(mfma_probe_kernel<8>, grid, block, 0, stream, sink, iterations); break;
   }
   return hipGetLastError();
 }

@@ -1,5 +1,7 @@
 // Quantisation arithmetic shared by the prep kernels and the attention prologue (which can
-// quantise its own query block): one definition, so every path produces the same codes.
+// quantise its own query block): one definition, so every path produces the same codes.  The
+// probability-code packers of the two attention kernels live here too, so that the library's
+// probe checks the very functions the kernels run.
 //
 // Reference: sage/reference.py:61-77 (per-group scale amax / 127 + 1e-7, round half to even,
 // clamp to +-127) and reference.py:22-32 (the same rule per V row).
@@ -78,6 +80,27 @@ __device__ __forceinline__ int code_of(float x, const Divisor& d) {
 // operand, 4-7 bytes of the first, 0x0c a zero byte).
 __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | __builtin_amdgcn_perm(d, c, 0x04000c0cu);
+}
+
+// Piper Attention's UINT8 probability codes, e0 in byte 0, as u - 128 in signed INT8 (the PV
+// MFMA's operand).  v_cvt_pk_u8_f32 rounds half to even and saturates to [0, 255]: the
+// reference's round().clamp(0, 255) (reference.py:104-107) in one instruction per code.
+__device__ __forceinline__ uint32_t pack_codes(float e0, float e1, float e2, float e3) {
+  uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(e0, 0, 0u);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(e1, 1, w);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(e2, 2, w);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(e3, 3, w);
+  return w ^ 0x80808080u;  // u - 128 as signed INT8
+}
+
+// SageAttention2++'s FP8 E4M3 probability codes, a in byte 0 (round to nearest even, like
+// torch's float8_e4m3fn cast).  Both 16-bit halves are written, so the word starts from an
+// undefined register (no clearing move).
+__device__ __forceinline__ uint32_t pack_fp8(float a, float b, float c, float d) {
+  int undef;
+  asm volatile("" : "=v"(undef));
+  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, undef, false));
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
 }
 
 }  // namespace piper

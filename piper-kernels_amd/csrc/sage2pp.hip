@@ -42,15 +42,6 @@ struct SageLayout : StagePieces<sage_tile_bytes(D), NW> {  // the tile record is
   static constexpr int kVOffset = sage_v_offset(D);
 };
 
-// Four FP8 E4M3 codes in one word, a in byte 0.  Both 16-bit halves are written, so the word
-// starts from an undefined register (no clearing move).
-__device__ __forceinline__ uint32_t pack_fp8(float a, float b, float c, float d) {
-  int undef;
-  asm volatile("" : "=v"(undef));
-  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, undef, false));
-  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
-}
-
 // Online softmax and PV of one 64-key block (block index t, staged at `stage`) for one wave,
 // in two parts.  Head: raw scores, masks, block maximum and the frame move (rescale of the
 // accumulators when the running maximum grows; exact, otherwise the weight is 1).  Tail:

@@ -51,6 +51,8 @@ MFMA_PROBE_I8_VALU = 3  # the INT8 MFMAs interleaved with the FP32 FMAs
 MFMA_PROBE_MAX3 = 4  # v_max3_f32 only
 MFMA_PROBE_EXP = 5  # v_exp_f32 only
 MFMA_PROBE_VALU_LDS = 6  # the FP32 FMAs with a ds_read_b128 after every 8
+MFMA_PROBE_P_CODES_U8 = 7  # Piper Attention's UINT8 probability-code packer on FP32 values from the sink
+MFMA_PROBE_P_CODES_FP8 = 8  # SageAttention2++'s FP8 E4M3 probability-code packer, the same way
 MFMA_PROBE_THREADS = 512
 MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 

@@ -161,6 +161,8 @@ def mfma_probe_expected(kind: int, iterations: int) -> int:
         return struct.unpack("<I", struct.pack("<f", 16.0))[0]
     if kind == native.MFMA_PROBE_EXP:
         raise ValueError("the exp probe converges to an irrational value: check it with exp_probe_ok")
+    if kind in (native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8):
+        raise ValueError("the conversion kinds store codes of their input values: use probability_codes")
     return struct.unpack("<I", struct.pack("<f", float(iterations * 4096)))[0]
 
 
@@ -174,6 +176,37 @@ def exp_probe_ok(words) -> bool:
 
     values = np.asarray(words, dtype=np.uint32).view(np.float32)
     return bool((values == values[0]).all() and abs(float(values[0]) - 16 * EXP_PROBE_FIXED_POINT) < 1e-4)
+
+
+def probability_codes(values, codes: str, device: torch.device):
+    """The attention kernels' probability codes of FP32 ``values``, computed on the GPU by the
+    kernels' own packers (the probe's conversion kinds): ``codes="u8"`` gives Piper Attention's
+    UINT8 codes u (the packer's bytes u - 128, shifted back), ``codes="fp8"``
+    SageAttention2++'s FP8 E4M3 bit patterns.  Returns a uint8 array of the same length."""
+    import numpy as np
+
+    from ._hip import library as native
+
+    kinds = {"u8": native.MFMA_PROBE_P_CODES_U8, "fp8": native.MFMA_PROBE_P_CODES_FP8}
+    if codes not in kinds:
+        raise ValueError(f"codes must be 'u8' or 'fp8', got {codes!r}")
+    flat = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    per_group = native.MFMA_PROBE_THREADS  # values read by one workgroup; it packs them into 128 words
+    workgroups = max(1, -(-flat.size // per_group))
+    host = np.zeros(workgroups * per_group, dtype=np.float32)
+    host[: flat.size] = flat
+    sink = torch.from_numpy(host.view(np.int32)).to(device)
+    stream = torch.cuda.current_stream(device)
+    with torch.cuda.device(device):
+        native.load_library().mfma_probe(kinds[codes], workgroups, 1, sink.data_ptr(), stream.cuda_stream)
+        stream.synchronize()
+    words = sink.cpu().numpy().view(np.uint32).reshape(workgroups, 4, per_group // 4)
+    if not (words == words[:, :1]).all():  # thread t and t + 128k pack the same four values
+        raise RuntimeError("probability-code probe: threads packing the same values disagree")
+    packed = np.ascontiguousarray(words[:, 0]).view(np.uint8).reshape(-1)  # little-endian: value 4i + j in byte j of word i
+    if codes == "u8":
+        packed = packed ^ np.uint8(0x80)
+    return packed[: flat.size]
 
 
 def _time_probe(lib, kind: int, workgroups: int, iterations: int, launches: int, device: torch.device) -> float:

@@ -294,7 +294,8 @@ def test_mfma_probe_constants_match_the_header(tmp_path) -> None:
                       '  printf("%d %d %d %d %d %d %d\\n", PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8, PIPER_MFMA_PROBE_THREADS,\n'
                       '         PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8),\n'
                       '         PIPER_MFMA_PROBE_VALU, PIPER_MFMA_PROBE_I8_VALU);\n'
-                      '  printf("%d %d %d\\n", PIPER_MFMA_PROBE_MAX3, PIPER_MFMA_PROBE_EXP, PIPER_MFMA_PROBE_VALU_LDS);\n'
+                      '  printf("%d %d %d %d %d\\n", PIPER_MFMA_PROBE_MAX3, PIPER_MFMA_PROBE_EXP, PIPER_MFMA_PROBE_VALU_LDS,\n'
+                      '         PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8);\n'
                       '  return 0; }\n')
     exe = tmp_path / "probe"
     subprocess.run(["gcc", f"-I{REPO / 'include'}", str(source), "-o", str(exe)], check=True)
@@ -302,14 +303,15 @@ def test_mfma_probe_constants_match_the_header(tmp_path) -> None:
     assert values == [native.MFMA_PROBE_I8, native.MFMA_PROBE_F8, native.MFMA_PROBE_THREADS,
                       native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8],
                       native.MFMA_PROBE_VALU, native.MFMA_PROBE_I8_VALU, native.MFMA_PROBE_MAX3,
-                      native.MFMA_PROBE_EXP, native.MFMA_PROBE_VALU_LDS]
+                      native.MFMA_PROBE_EXP, native.MFMA_PROBE_VALU_LDS, native.MFMA_PROBE_P_CODES_U8,
+                      native.MFMA_PROBE_P_CODES_FP8]
     # 32x32x32 INT8 and 32x32x64 FP8: two operations per multiply-add
     assert native.MFMA_PROBE_OPS == {native.MFMA_PROBE_I8: 2 * 32 * 32 * 32, native.MFMA_PROBE_F8: 2 * 32 * 32 * 64}
 
 
 def test_mfma_probe_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
-        lib.mfma_probe(7, 1, 1, 0x1000, 0)
+        lib.mfma_probe(9, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
         lib.mfma_probe(-1, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="workgroups and"):
@@ -332,6 +334,17 @@ def test_mfma_probe_expected_words() -> None:
     assert mfma_probe_expected(native.MFMA_PROBE_VALU, 2048) == 0x48000000
     assert mfma_probe_expected(native.MFMA_PROBE_I8_VALU, 2048) == 2048 * 2048 + 64 * 2048
     assert mfma_probe_expected(native.MFMA_PROBE_MAX3, 7) == 0x41800000  # 16.0
+    for kind in (native.MFMA_PROBE_EXP, native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8):
+        with pytest.raises(ValueError):
+            mfma_probe_expected(kind, 1)
+
+
+def test_probability_codes_rejects_unknown_codes() -> None:
+    import torch
+    from piper_kernels.measure import probability_codes
+
+    with pytest.raises(ValueError, match="'u8' or 'fp8'"):
+        probability_codes([0.5], "int4", torch.device("cpu"))
 
 
 def test_exp_probe_check() -> None:
