@@ -171,6 +171,61 @@ def test_gfx950_without_library_raises(monkeypatch, tmp_path) -> None:
         piper_attention(q, k, v)
 
 
+def test_every_native_call_runs_under_the_input_device_guard(monkeypatch) -> None:
+    """Like the reference's device-guard test (test_dispatch.py:37-96): the prep and the kernel
+    launch are issued with the inputs' device current, on that device's current stream.  The
+    library is a recording stand-in (layout queries go to the real, host-only function)."""
+    from piper_kernels.attention.piper_attention import hip
+
+    real = native.load_library()
+    guard = []  # devices of the guards currently entered
+    calls = []
+
+    class Guard:
+        def __init__(self, device):
+            self.device = torch.device(device)
+
+        def __enter__(self):
+            guard.append(self.device)
+
+        def __exit__(self, *exc):
+            guard.pop()
+
+    class Recorder:
+        def prepared_layout(self, shape):
+            return real.prepared_layout(shape)
+
+        def prepare(self, args, stream):
+            calls.append(("prepare", list(guard), stream, args.flags))
+
+        def attention_forward(self, args, stream):
+            calls.append(("attention_forward", list(guard), stream, args.flags))
+
+        def attention_forward_fused(self, args, stream):
+            calls.append(("attention_forward_fused", list(guard), stream, args.flags))
+
+    streams = []
+
+    def current_stream(device=None):
+        streams.append(torch.device(device))
+        return SimpleNamespace(cuda_stream=0x5EED)
+
+    monkeypatch.setattr(native, "load_library", lambda *a: Recorder())
+    monkeypatch.setattr(torch.cuda, "device", Guard)
+    monkeypatch.setattr(torch.cuda, "current_stream", current_stream)
+    monkeypatch.setattr(torch.Tensor, "record_stream", lambda self, stream: None)
+    q, k, v = _inputs()
+    hip._run_piper_attention(q, k, v, 64**-0.5, False)  # the operator's path: fused query
+    hip._run_piper_attention(q, k, v, 64**-0.5, True, fuse_query=False, qk_granularity="per_warp")
+    device = q.device
+    assert [c[0] for c in calls] == ["prepare", "attention_forward_fused", "prepare", "attention_forward"]
+    assert all(c[1] == [device] and c[2] == 0x5EED for c in calls)  # inside exactly the inputs' guard
+    assert set(streams) == {device}
+    assert calls[0][3] == native.PREPARE_SKIP_QUERY | native.PREPARE_QK_PER_THREAD
+    assert calls[1][3] == native.ATTENTION_QK_PER_THREAD
+    assert calls[2][3] == 0 and calls[3][3] == 0
+
+
 # ---- plan ----------------------------------------------------------------------------
 def test_plan_selection() -> None:
     from piper_kernels.attention.piper_attention import _plan

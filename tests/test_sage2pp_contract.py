@@ -123,3 +123,52 @@ def test_custom_op_is_registered_with_reference_schema_and_fake() -> None:
     q = torch.empty((2, 3, 5, 64), dtype=torch.bfloat16, device="meta").transpose(0, 1)
     out = torch.ops.piper_kernels.sage_attention_2pp(q, q, q, 0.125, False)
     assert out.device.type == "meta" and out.shape == q.shape and out.is_contiguous()
+
+
+def test_every_native_call_runs_under_the_input_device_guard(monkeypatch) -> None:
+    """The SageAttention2++ prep and launch are issued with the inputs' device current, on that
+    device's current stream (as the reference's device-guard test, test_dispatch.py:37-96)."""
+    from types import SimpleNamespace
+
+    from piper_kernels.attention.sage_attention_2pp import hip
+
+    real = native.load_library()
+    guard, calls, streams = [], [], []
+
+    class Guard:
+        def __init__(self, device):
+            self.device = torch.device(device)
+
+        def __enter__(self):
+            guard.append(self.device)
+
+        def __exit__(self, *exc):
+            guard.pop()
+
+    class Recorder:
+        def sage_prepared_layout(self, shape):
+            return real.sage_prepared_layout(shape)
+
+        def sage_prepare(self, args, stream):
+            calls.append(("sage_prepare", list(guard), stream, args.flags))
+
+        def sage_attention_forward(self, args, stream):
+            calls.append(("sage_attention_forward", list(guard), stream, args.flags))
+
+    def current_stream(device=None):
+        streams.append(torch.device(device))
+        return SimpleNamespace(cuda_stream=0x5EED)
+
+    monkeypatch.setattr(native, "load_library", lambda *a: Recorder())
+    monkeypatch.setattr(torch.cuda, "device", Guard)
+    monkeypatch.setattr(torch.cuda, "current_stream", current_stream)
+    monkeypatch.setattr(torch.Tensor, "record_stream", lambda self, stream: None)
+    q, k, v = _inputs()
+    hip._run_sage_attention_2pp(q, k, v, q.shape[-1] ** -0.5, False)
+    hip._run_sage_attention_2pp(q, k, v, q.shape[-1] ** -0.5, True, qk_granularity="per_warp")
+    assert [c[0] for c in calls] == ["sage_prepare", "sage_attention_forward"] * 2
+    assert all(c[1] == [q.device] and c[2] == 0x5EED for c in calls)
+    assert set(streams) == {q.device}
+    assert calls[0][3] == native.PREPARE_QK_PER_THREAD  # the sage prep never quantises Q
+    assert calls[1][3] == native.ATTENTION_QK_PER_THREAD
+    assert calls[2][3] == 0 and calls[3][3] == 0
