@@ -376,8 +376,8 @@ def piper_attention_reference(
 ) -> np.ndarray:
     """Full quantised reference (reference.py:35-118). Returns the FP32 pre-cast output.
 
-    ``granularity`` defaults to ``per_thread`` like ``reference.py:42``; the HIP backend
-    quantises per block, which is ``per_warp`` here.
+    ``granularity`` defaults to ``per_thread`` like ``reference.py:42`` (the HIP operator's
+    default too); ``per_warp`` is the per-block granularity of the reference's grouped path.
     """
     width = q.shape[-1]
     scale = width**-0.5 if scale is None else float(scale)
