@@ -157,14 +157,24 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
 
 // LDS ring of kStages tile records.  Iteration t consumes block t (stage t % kStages), issues
 // the QK MFMAs of block t + 1 first so they run under the softmax VALU work, and starts the
-// direct copy of block t + kLead.  A workgroup barrier follows every second iteration; the
-// barrier after iteration i waits for every copy issued before iteration i.  With 6 stages
-// and a lead of 4: a copy issued at iteration t is complete and published by the barrier
-// after iteration t + 1 or t + 2, before its first read (QK at iteration t + kLead - 1), and
-// the stage it overwrites was last read at iteration t - 2, before the barrier after t - 2
-// or t - 1.
-constexpr int kStages = 6;
-constexpr int kLead = 4;
+// direct copy of block t + kLead.  The barrier after iteration i waits for every copy issued
+// before iteration i.
+// 8-wave workgroups (one per CU): 6 stages, a lead of 4 and a barrier after every second
+// iteration.  A copy issued at iteration t is complete and published by the barrier after
+// iteration t + 1 or t + 2, before its first read (QK at iteration t + kLead - 1), and the
+// stage it overwrites was last read at iteration t - 2, before the barrier after t - 2 or t - 1.
+// 4-wave workgroups (two per CU: at D = 128 two 4-stage rings take 144 KiB of the CU's
+// 160 KiB): 4 stages, a lead of 3 and a barrier after every iteration.  A copy issued at
+// iteration t is published by the barrier after t + 1, before its first read at t + 2, and
+// the stage it overwrites was last read at iteration t - 1, before the barrier after t - 1.
+template <int NW>
+struct Ring {
+  static constexpr int kStages = NW == 4 ? 4 : 6;
+  static constexpr int kLead = NW == 4 ? 3 : 4;
+  static constexpr bool kEveryIteration = NW == 4;
+  static_assert(kStages >= kLead + (kEveryIteration ? 1 : 2), "a copy must not overwrite a stage still being read");
+  static_assert(kLead >= (kEveryIteration ? 3 : 4), "a copy must be published before its first read");
+};
 
 template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
@@ -173,12 +183,14 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
                                               const v16i (&s_cur)[2], v16i (&s_next)[2], float (&num)[D / 32][16],
                                               float& den, float& mref) {
   using L = TileLayout<D, NW>;
+  using R = Ring<NW>;
   // unconditional (clamped) so every iteration issues the same number of copies; a clamped
   // copy lands in a stage no iteration reads before it is written again
-  copy_block<L>(p, smem + ((t + kLead) % kStages) * L::kStageBytes, bh, min(t + kLead, tiles - 1), wave, lane);
+  copy_block<L>(p, smem + ((t + R::kLead) % R::kStages) * L::kStageBytes, bh, min(t + R::kLead, tiles - 1), wave,
+                lane);
   if (t < wave_tiles) {
-    block_scores<D, L>(smem + ((t + 1) % kStages) * L::kStageBytes, qf, h, krow, bias, s_next);  // unused past the end
-    const char* stage = smem + (t % kStages) * L::kStageBytes;
+    block_scores<D, L>(smem + ((t + 1) % R::kStages) * L::kStageBytes, qf, h, krow, bias, s_next);  // unused past the end
+    const char* stage = smem + (t % R::kStages) * L::kStageBytes;
     // the K scales of the tile's four thread groups sit in the padding of K row 0
     float ct[4];
     if constexpr (kPerThread) {
@@ -195,11 +207,14 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }
 
+// Two waves per SIMD (at most 256 VGPRs): one 8-wave or two 4-wave workgroups per CU.
 template <int D, int NW, bool kCausal, int kOut, bool kPerThread>
-__global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnParams p) {
   using L = TileLayout<D, NW>;
+  using R = Ring<NW>;
   constexpr int kChunksD = D / 32;
-  __shared__ __attribute__((aligned(16))) char smem[kStages * L::kStageBytes];
+  constexpr int kLead = R::kLead;
+  __shared__ __attribute__((aligned(16))) char smem[R::kStages * L::kStageBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -283,11 +298,12 @@ __global__ void __launch_bounds__(NW * 64, 1) attention_kernel(const AttnParams 
   v16i s_a[2], s_b[2];  // scores of the current and the next block, alternating
   if (wave_tiles > 0) block_scores<D, L>(smem, qf, h, krow, bias, s_a);
 
-  // unrolled by two so both score sets keep static names; one barrier per pair
+  // unrolled by two so both score sets keep static names; one barrier per pair (8 waves) or
+  // per iteration (4 waves)
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    pipeline_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
-                                         krow, bias, s_a, s_b, num, den, mref);
+    pipeline_step<D, NW, kCausal, kPerThread, R::kEveryIteration>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq,
+                                                               q0, n, h, krow, bias, s_a, s_b, num, den, mref);
     pipeline_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
                                         h, krow, bias, s_b, s_a, num, den, mref);
   }

@@ -232,6 +232,11 @@ def test_plan_selection() -> None:
 
     assert _plan.heuristic_plan(1, 24, 16384) == MI355XPlan(waves=8)
     assert _plan.heuristic_plan(1, 2, 193) == MI355XPlan(waves=4)
+    # Piper Attention's untuned shapes: two 4-wave workgroups per CU unless long and non-causal
+    assert _plan.piper_heuristic_plan(1, 24, 16384, False) == MI355XPlan(waves=8)
+    assert _plan.piper_heuristic_plan(1, 24, 16384, True) == MI355XPlan(waves=4)
+    assert _plan.piper_heuristic_plan(2, 32, 8192, False) == MI355XPlan(waves=4)
+    assert _plan.piper_heuristic_plan(1, 1, 32768, False) == MI355XPlan(waves=4)  # 8-wave grid too small
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
                                         "causal_interleave": False, "block_m": 256, "block_n": 64}
@@ -273,7 +278,7 @@ def test_frozen_plan_table_lookup_and_fallback(tmp_path, monkeypatch) -> None:
     try:
         # batch * heads is the key: B2 H12 is the same shape as B1 H24
         assert _plan.select_plan(2, 12, 4096, 4096, 128, False) == MI355XPlan(4, True, False)
-        assert _plan.select_plan(1, 24, 4096, 4096, 128, True) == _plan.heuristic_plan(1, 24, 4096)
+        assert _plan.select_plan(1, 24, 4096, 4096, 128, True) == _plan.piper_heuristic_plan(1, 24, 4096, True)
         assert _plan.select_plan(1, 24, 16384, 16384, 128, False) == MI355XPlan()
     finally:
         _plan.frozen_plans.cache_clear()
