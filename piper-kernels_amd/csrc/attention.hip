@@ -155,27 +155,6 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   }
 }
 
-// LDS ring of kStages tile records.  Iteration t consumes block t (stage t % kStages), issues
-// the QK MFMAs of block t + 1 first so they run under the softmax VALU work, and starts the
-// direct copy of block t + kLead.  The barrier after iteration i waits for every copy issued
-// before iteration i.
-// 8-wave workgroups (one per CU): 6 stages, a lead of 4 and a barrier after every second
-// iteration.  A copy issued at iteration t is complete and published by the barrier after
-// iteration t + 1 or t + 2, before its first read (QK at iteration t + kLead - 1), and the
-// stage it overwrites was last read at iteration t - 2, before the barrier after t - 2 or t - 1.
-// 4-wave workgroups (two per CU: at D = 128 two 4-stage rings take 144 KiB of the CU's
-// 160 KiB): 4 stages, a lead of 3 and a barrier after every iteration.  A copy issued at
-// iteration t is published by the barrier after t + 1, before its first read at t + 2, and
-// the stage it overwrites was last read at iteration t - 1, before the barrier after t - 1.
-template <int NW>
-struct Ring {
-  static constexpr int kStages = NW == 4 ? 4 : 6;
-  static constexpr int kLead = NW == 4 ? 3 : 4;
-  static constexpr bool kEveryIteration = NW == 4;
-  static_assert(kStages >= kLead + (kEveryIteration ? 1 : 2), "a copy must not overwrite a stage still being read");
-  static_assert(kLead >= (kEveryIteration ? 3 : 4), "a copy must be published before its first read");
-};
-
 template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                               int wave, int lane, const v4i (&qf)[D / 32], float cq,

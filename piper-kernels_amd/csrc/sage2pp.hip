@@ -148,23 +148,17 @@ __device__ __forceinline__ void sage_block_tail(const char* stage, const float (
   }
 }
 
-// The LDS ring of the Piper Attention kernel: kStages tile records, block t + kLead copied at
-// iteration t, one workgroup barrier per two iterations (see attention.hip's pipeline_step
-// for the argument that every stage is published before it is read and read before it is
-// overwritten).
-constexpr int kSageStages = 6;
-constexpr int kSageLead = 4;
-
 template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
 __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                           int wave, int lane, const v4i (&qf)[D / 32], float cq, int q0, int n,
                                           int h, int krow, const v16i& bias, const v16i (&s_cur)[2],
                                           v16i (&s_next)[2], v16f (&acc)[D / 32], float& den, float& mrun) {
   using L = SageLayout<D, NW>;
-  copy_block<L>(p, smem + ((t + kSageLead) % kSageStages) * L::kStageBytes, bh, min(t + kSageLead, tiles - 1), wave,
+  using R = Ring<NW>;  // the Piper Attention kernel's ring (stream.h)
+  copy_block<L>(p, smem + ((t + R::kLead) % R::kStages) * L::kStageBytes, bh, min(t + R::kLead, tiles - 1), wave,
                 lane);
   if (t < wave_tiles) {
-    const char* stage = smem + (t % kSageStages) * L::kStageBytes;
+    const char* stage = smem + (t % R::kStages) * L::kStageBytes;
     // the K scales of the tile's four thread groups sit in the padding of K row 0
     float ct[4];
     if constexpr (kPerThread) {
@@ -181,7 +175,7 @@ __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t
     // the frame move, or interleaving them with the softmax, measured 1-5% slower; feeding the
     // biased accumulator bits to the exp FMA with a folded constant saves the 32 subtractions
     // but costs register copies and measured 3% slower)
-    block_scores<D, L>(smem + ((t + 1) % kSageStages) * L::kStageBytes, qf, h, krow, bias, s_next);
+    block_scores<D, L>(smem + ((t + 1) % R::kStages) * L::kStageBytes, qf, h, krow, bias, s_next);
     sage_block_head<D, kCausal, kPerThread>(s_cur, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
     sage_block_tail<D, NW>(stage, x, ct, n, h, acc, den, mrun);
   }
@@ -189,10 +183,12 @@ __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t
 }
 
 template <int D, int NW, bool kCausal, int kOut, bool kPerThread>
-__global__ void __launch_bounds__(NW * 64, 1) sage_attention_kernel(const SageParams p) {
+__global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const SageParams p) {
   using L = SageLayout<D, NW>;
+  using R = Ring<NW>;
   constexpr int kChunksD = D / 32;
-  __shared__ __attribute__((aligned(16))) char smem[kSageStages * L::kStageBytes];
+  constexpr int kSageLead = R::kLead;
+  __shared__ __attribute__((aligned(16))) char smem[R::kStages * L::kStageBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -253,8 +249,8 @@ __global__ void __launch_bounds__(NW * 64, 1) sage_attention_kernel(const SagePa
 
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    sage_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
-                                     s_a, s_b, acc, den, mrun);
+    sage_step<D, NW, kCausal, kPerThread, R::kEveryIteration>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
+                                                           h, krow, bias, s_a, s_b, acc, den, mrun);
     sage_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
                                     s_b, s_a, acc, den, mrun);
   }

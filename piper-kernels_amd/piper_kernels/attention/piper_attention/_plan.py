@@ -103,8 +103,8 @@ def frozen_plans() -> dict:
 
 
 def heuristic_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
-    """8-wave workgroups unless that leaves most CUs idle; then 4-wave workgroups (the
-    SageAttention2++ operator's plan, and Piper Attention's for long non-causal sequences)."""
+    """8-wave workgroups unless that leaves most CUs idle; then 4-wave workgroups (Piper
+    Attention's plan for long non-causal sequences)."""
     wide = MI355XPlan(waves=8)
     if wide.workgroups(batch, heads, query_length) >= COMPUTE_UNITS:
         return wide
@@ -119,6 +119,12 @@ def piper_heuristic_plan(batch: int, heads: int, query_length: int, is_causal: b
     if is_causal or query_length <= 8192:
         return MI355XPlan(waves=4)
     return heuristic_plan(batch, heads, query_length)
+
+
+def sage_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
+    """The SageAttention2++ operator's plan: 4-wave workgroups, two per CU, on every shape
+    (measured 4-22% faster than 8-wave workgroups at c2-c5: c2 22%, c3 4%, c4 9%, c5 5%)."""
+    return MI355XPlan(waves=4)
 
 
 def select_plan(batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool) -> MI355XPlan:

@@ -237,6 +237,7 @@ def test_plan_selection() -> None:
     assert _plan.piper_heuristic_plan(1, 24, 16384, True) == MI355XPlan(waves=4)
     assert _plan.piper_heuristic_plan(2, 32, 8192, False) == MI355XPlan(waves=4)
     assert _plan.piper_heuristic_plan(1, 1, 32768, False) == MI355XPlan(waves=4)  # 8-wave grid too small
+    assert _plan.sage_plan(1, 24, 16384) == MI355XPlan(waves=4)  # SageAttention2++: two per CU everywhere
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
                                         "causal_interleave": False, "block_m": 256, "block_n": 64}
