@@ -174,7 +174,8 @@ typedef struct piper_prepare_args {
 /* Launch-plan bits of piper_attention_args.plan (results are identical for every plan; only
  * the speed differs).  Default (0): 8 query waves of 32 queries per workgroup, causal query
  * tiles dispatched longest first, workgroups of one head kept on one XCD. */
-#define PIPER_PLAN_FOUR_WAVES 1     /* 4 query waves per workgroup (for grids below the CU count) */
+#define PIPER_PLAN_FOUR_WAVES 1     /* 4 query waves per workgroup, two workgroups per CU (4-stage LDS
+                                       rings); the default is 8 waves, one workgroup per CU */
 #define PIPER_PLAN_CAUSAL_FORWARD 2 /* causal: query tiles in forward order */
 #define PIPER_PLAN_NO_XCD_REMAP 4   /* hardware workgroup order */
 #define PIPER_PLAN_CAUSAL_INTERLEAVE 8 /* causal, longest first: query tiles dispatched longest first
