@@ -127,7 +127,7 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py runs on exactly one GPU (asked for --gpus {args.gpus}); this build has no "
-            "multi-GPU path -- see DESIGN.md for how the operator would shard.",
+            "multi-GPU path (heads are independent: the operator would shard over (batch, head) pairs).",
             file=sys.stderr,
         )
         return 2

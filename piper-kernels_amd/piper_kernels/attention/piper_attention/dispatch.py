@@ -6,7 +6,7 @@ supported NVIDIA targets to its Triton custom op and everything else to its port
 PyTorch reference.  This package *is* the gfx950 backend: a gfx950 HIP device goes to
 the ``piper_kernels::piper_attention`` custom op backed by the hand-written HIP kernels;
 any other device raises ``NotImplementedError`` (the portable reference stays with the
-reference package -- see INTEGRATION.md for wiring this backend into its dispatch), and
+reference package, whose dispatch would route gfx950 devices to this backend), and
 a gfx950 device without the built library raises instead of silently computing on the CPU.
 """
 
