@@ -13,6 +13,8 @@
  *                               (K/V means triton.py:638-699, Q/K quantisation
  *                               attention/kernels/qk_quantization/int8/sage/triton.py:238-356,
  *                               per-key V quantisation triton.py:176-246 / :839-860)
+ *   piper_prepare_static     <- no reference counterpart: piper_prepare with the mean partials in
+ *                               a static per-GPU scratch, for callers that cannot allocate
  *   piper_attention_forward  <- _launch_piper_attention
  *                               src/piper_kernels/attention/piper_attention/triton.py:893-951
  *                               (fused kernel _piper_attention_kernel triton.py:303-635)
@@ -285,8 +287,22 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout);
 
 /* Quantise Q, K, V into args->prepared on `stream` (a hipStream_t; NULL = default stream);
  * with PIPER_PREPARE_SKIP_QUERY only K and V.
- * Launches: FP64 mean partials, mean finalisation, one quantisation kernel. */
+ * Launches: FP32 mean partials (torch's CPU order), mean finalisation, one quantisation kernel. */
 int piper_prepare(const piper_prepare_args* args, void* stream);
+
+/* piper_prepare without a caller workspace.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  args->workspace must be NULL and args->workspace_bytes 0; the FP32
+ * mean partials go to a static scratch array inside the library instead, of
+ * PIPER_STATIC_SCRATCH_BYTES bytes per GPU (each GPU the library runs on holds its own copy
+ * until the process ends).  Shapes whose piper_layout.workspace_bytes exceeds it are rejected
+ * with PIPER_ERROR_UNSUPPORTED before anything is launched (2 * B * H * (ceil(Sk / 256) + 1) *
+ * D * 4 bytes for Sk <= 2^19: 10.1 MiB for 80 batch-heads at Sk = 32768, D = 128).  Call it with the
+ * stream's device current.  It calls no allocator.  Every call on one GPU shares that GPU's
+ * scratch: calls on one stream are ordered, calls that overlap on one GPU (other streams or
+ * threads) race.  Outputs are identical to piper_prepare's. */
+#define PIPER_STATIC_SCRATCH_BYTES (16ll << 20)
+int piper_prepare_static(const piper_prepare_args* args, void* stream);
 
 /* Fused INT8-QK / UINT8-P x INT8-V online-softmax attention on `stream`. */
 int piper_attention_forward(const piper_attention_args* args, void* stream);

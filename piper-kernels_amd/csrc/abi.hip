@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "kernels.h"
 #include "piper_mi355x.h"
@@ -22,6 +23,9 @@ static_assert(PIPER_SAGE_V_OFFSET(128) == piper::sage_v_offset(128), "SageAttent
 static_assert(PIPER_MFMA_PROBE_THREADS == piper::kProbeThreads, "probe workgroup size");
 static_assert(PIPER_QUERY_SCALE_SLOTS == piper::kQueryScaleSlots && PIPER_KEY_SCALE_SLOTS == piper::kKeyScaleSlots,
               "scale slots per block");
+
+// Static scratch of piper_prepare_static (see device_scratch below).
+static __device__ __align__(256) unsigned char scratch[PIPER_STATIC_SCRATCH_BYTES];
 
 namespace {
 
@@ -60,6 +64,35 @@ int check_input(const char* name, const piper_tensor& t) {
     return fail(PIPER_ERROR_INVALID_ARGUMENT,
                 "%s must be 16-byte aligned with batch/head/sequence strides that are multiples of 8 elements",
                 name);
+  return PIPER_OK;
+}
+
+// Static scratch of piper_prepare_static: the prep's FP32 mean partials for callers that cannot
+// allocate.  Each GPU the library runs on holds its own copy until the process ends.  In host
+// code `scratch` only names the symbol: its device address on the current GPU comes from
+// hipGetSymbolAddress, looked up once per device (device_scratch) and used for every launch.
+// The mean pass writes every partial the finalisation reads, so nothing needs clearing between
+// calls; calls that overlap on one GPU share the array and race.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+
+int device_scratch(void** address) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(PIPER_ERROR_UNSUPPORTED, "device %d is beyond the %d this build tracks", device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return fail(PIPER_ERROR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                  hipGetErrorString(err));
+    g_scratch_address[device] = ptr;
+  }
+  *address = g_scratch_address[device];
   return PIPER_OK;
 }
 
@@ -164,7 +197,9 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
   return PIPER_OK;
 }
 
-int piper_prepare(const piper_prepare_args* a, void* stream) {
+// Validation and launches of piper_prepare; with use_scratch, the mean partials go to this
+// GPU's static scratch instead of the caller's workspace (piper_prepare_static).
+static int prepare_call(const piper_prepare_args* a, bool use_scratch, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
   if (a->abi_version != PIPER_ABI_VERSION)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", a->abi_version,
@@ -189,9 +224,20 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte aligned");
   piper_layout layout;
   if (int st = piper_prepared_layout(&a->shape, &layout)) return st;
-  if (a->workspace == nullptr || a->workspace_bytes < layout.workspace_bytes)
+  void* workspace = a->workspace;
+  if (use_scratch) {
+    if (a->workspace != nullptr || a->workspace_bytes != 0)
+      return fail(PIPER_ERROR_INVALID_ARGUMENT, "piper_prepare_static takes no workspace (pass NULL and 0)");
+    if (layout.workspace_bytes > PIPER_STATIC_SCRATCH_BYTES)
+      return fail(PIPER_ERROR_UNSUPPORTED,
+                  "shape needs %lld bytes of prep scratch, more than the static %lld bytes of piper_prepare_static "
+                  "(use piper_prepare with a workspace)",
+                  (long long)layout.workspace_bytes, (long long)PIPER_STATIC_SCRATCH_BYTES);
+    if (int st = device_scratch(&workspace)) return st;
+  } else if (a->workspace == nullptr || a->workspace_bytes < layout.workspace_bytes) {
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "workspace needs %lld bytes, got %lld",
                 (long long)layout.workspace_bytes, (long long)a->workspace_bytes);
+  }
 
   const piper_shape& s = a->shape;
   const int bh = static_cast<int>(s.batch * s.heads);
@@ -202,7 +248,7 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   piper::MeanParams mp{};
   mp.key = to_input(a->key);
   mp.value = to_input(a->value);
-  mp.partials = static_cast<float*>(a->workspace);
+  mp.partials = static_cast<float*>(workspace);
   mp.key_mean = o.key_mean;
   mp.value_mean = o.value_mean;
   mp.batch_heads = bh;
@@ -242,6 +288,10 @@ int piper_prepare(const piper_prepare_args* a, void* stream) {
   g_last_error[0] = '\0';
   return PIPER_OK;
 }
+
+int piper_prepare(const piper_prepare_args* a, void* stream) { return prepare_call(a, false, stream); }
+
+int piper_prepare_static(const piper_prepare_args* a, void* stream) { return prepare_call(a, true, stream); }
 
 int piper_attention_forward(const piper_attention_args* a, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");

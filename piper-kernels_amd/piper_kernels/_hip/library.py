@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "piper_abi_version",
     "piper_prepared_layout",
     "piper_prepare",
+    "piper_prepare_static",
     "piper_attention_forward",
     "piper_attention_forward_fused",
     "piper_sage_prepared_layout",
@@ -39,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "piper_last_error",
 )
 
+STATIC_SCRATCH_BYTES = 16 << 20  # PIPER_STATIC_SCRATCH_BYTES: piper_prepare_static's per-GPU scratch
 PREPARE_SKIP_QUERY = 1  # piper_prepare_args.flags
 PREPARE_QK_PER_THREAD = 2
 ATTENTION_QK_PER_THREAD = 1  # piper_attention_args.flags / piper_attention_fused_args.flags
@@ -237,6 +239,8 @@ class NativeLibrary:
         lib.piper_prepared_layout.restype = ctypes.c_int
         lib.piper_prepare.argtypes = [ctypes.POINTER(PiperPrepareArgs), _ptr]
         lib.piper_prepare.restype = ctypes.c_int
+        lib.piper_prepare_static.argtypes = [ctypes.POINTER(PiperPrepareArgs), _ptr]
+        lib.piper_prepare_static.restype = ctypes.c_int
         lib.piper_attention_forward.argtypes = [ctypes.POINTER(PiperAttentionArgs), _ptr]
         lib.piper_attention_forward.restype = ctypes.c_int
         lib.piper_attention_forward_fused.argtypes = [ctypes.POINTER(PiperAttentionFusedArgs), _ptr]
@@ -275,6 +279,10 @@ class NativeLibrary:
 
     def prepare(self, args: PiperPrepareArgs, stream: int) -> None:
         self._check(self._lib.piper_prepare(ctypes.byref(args), _ptr(stream)), "piper_prepare")
+
+    def prepare_static(self, args: PiperPrepareArgs, stream: int) -> None:
+        """piper_prepare with the library's static per-GPU scratch (no workspace in ``args``)."""
+        self._check(self._lib.piper_prepare_static(ctypes.byref(args), _ptr(stream)), "piper_prepare_static")
 
     def attention_forward(self, args: PiperAttentionArgs, stream: int) -> None:
         self._check(self._lib.piper_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_attention_forward")

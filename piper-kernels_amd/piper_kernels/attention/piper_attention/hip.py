@@ -117,6 +117,7 @@ def _prepare_piper_attention(
     workspace: torch.Tensor | None = None,
     quantize_query: bool = True,
     qk_granularity: str = "per_thread",
+    static_workspace: bool = False,
 ) -> PreparedPiperAttention:
     """Quantise Q/K/V on the GPU (one HIP prep pipeline) and allocate the output.
 
@@ -127,7 +128,9 @@ def _prepare_piper_attention(
     (``sage/reference.py:80-108``): ``"per_thread"`` (the default, as in its portable path --
     ``reference.py:42`` -- which is what the reference runs on MI355X: 8 scales per Q block, 4
     per K block, over interleaved rows) or ``"per_warp"`` (one scale per 32-row Q / 64-row K
-    block, its grouped SM12x Triton path).
+    block, its grouped SM12x Triton path).  ``static_workspace=True`` runs ``piper_prepare_static``
+    instead: no workspace is allocated, the library's static per-GPU scratch holds the mean
+    partials (same outputs; calls overlapping on one GPU race).
     """
     if qk_granularity not in ("per_warp", "per_thread"):
         raise ValueError(f"unknown Q/K quantization granularity: {qk_granularity}")
@@ -169,7 +172,9 @@ def _prepare_piper_attention(
     query, q_arg = _native_input(query)
     if not quantize_query:
         prepared = replace(prepared, query=query)
-    if workspace is None or workspace.numel() < layout.workspace_bytes:
+    if static_workspace:
+        workspace = None
+    elif workspace is None or workspace.numel() < layout.workspace_bytes:
         workspace = empty((max(layout.workspace_bytes, 1),), torch.uint8)
     key, k_arg = _native_input(key)
     value, v_arg = _native_input(value)
@@ -183,15 +188,19 @@ def _prepare_piper_attention(
         key=k_arg,
         value=v_arg,
         prepared=prepared.native_prepared(),
-        workspace=workspace.data_ptr(),
-        workspace_bytes=workspace.numel(),
+        workspace=None if workspace is None else workspace.data_ptr(),
+        workspace_bytes=0 if workspace is None else workspace.numel(),
     )
     with torch.cuda.device(device):
-        lib.prepare(args, torch.cuda.current_stream(device).cuda_stream)
+        stream = torch.cuda.current_stream(device)
+        if static_workspace:
+            lib.prepare_static(args, stream.cuda_stream)
+        else:
+            lib.prepare(args, stream.cuda_stream)
     # the caching allocator must not recycle inputs or workspace before the stream reaches them
-    stream = torch.cuda.current_stream(device)
     for tensor in (query, key, value, workspace):
-        tensor.record_stream(stream)
+        if tensor is not None:
+            tensor.record_stream(stream)
     return prepared
 
 

@@ -184,6 +184,34 @@ def test_prepare_flags(lib) -> None:
         lib.prepare(args, 0)
 
 
+def test_prepare_static_validates_before_touching_the_gpu(lib) -> None:
+    """piper_prepare_static rejects a caller workspace and shapes beyond its static scratch on the
+    host, before it looks up the device scratch (so these run without a GPU)."""
+    fake = 0x1000
+    tensor = native.PiperTensor(fake, 1 << 20, 1 << 20, 128)
+    args = native.PiperPrepareArgs(
+        abi_version=native.ABI_VERSION,
+        dtype=native.FLOAT16,
+        flags=native.PREPARE_SKIP_QUERY,
+        shape=native.PiperShape(1, 1, 64, 64, 128),
+        key=tensor,
+        value=tensor,
+        prepared=native.PiperPrepared(None, None, fake, fake, fake, fake, fake),
+        workspace=fake,
+        workspace_bytes=1 << 20,
+    )
+    with pytest.raises(RuntimeError, match="takes no workspace"):
+        lib.prepare_static(args, 0)
+    args.workspace, args.workspace_bytes = None, 0
+    # 128 batch-heads at Sk = 32768, D = 128 need 2 * 128 * 129 * 128 * 4 bytes: just over 16 MiB
+    args.shape = native.PiperShape(2, 64, 32768, 32768, 128)
+    assert lib.prepared_layout(args.shape).workspace_bytes > native.STATIC_SCRATCH_BYTES
+    with pytest.raises(RuntimeError, match="more than the static 16777216 bytes"):
+        lib.prepare_static(args, 0)
+    # the largest BASELINE workload fits (c5: 80 batch-heads at Sk = 32768)
+    assert lib.prepared_layout(native.PiperShape(2, 40, 32768, 32768, 128)).workspace_bytes <= native.STATIC_SCRATCH_BYTES
+
+
 def test_fused_attention_validates_before_launching(lib) -> None:
     fake = 0x1000
     args = native.PiperAttentionFusedArgs(
