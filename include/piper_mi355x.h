@@ -183,7 +183,9 @@ typedef struct piper_prepare_args {
 #define PIPER_PLAN_CAUSAL_INTERLEAVE 8 /* causal, longest first: query tiles dispatched longest first
                                           across the heads of each XCD (across all heads with
                                           PIPER_PLAN_NO_XCD_REMAP) instead of head by head */
-#define PIPER_PLAN_MASK 15
+#define PIPER_PLAN_THREE_WORKGROUPS 16 /* three 4-wave workgroups per CU (three waves per SIMD, 2-stage LDS
+                                          rings); overrides PIPER_PLAN_FOUR_WAVES.  Piper Attention only */
+#define PIPER_PLAN_MASK 31
 
 /* piper_attention_args.flags / piper_attention_fused_args.flags */
 #define PIPER_ATTENTION_QK_PER_THREAD 1 /* Q/K scales per thread group: read slot (row % 8) of the

@@ -132,7 +132,9 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   if (!aligned16(o.kv_tiles) || !aligned16(o.value_mean) || (reinterpret_cast<uintptr_t>(output) & 7u) != 0)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
 
-  const int waves = (plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
+  // 3: three 4-wave workgroups per CU (attention_w3_kernel)
+  const int waves = (plan & PIPER_PLAN_THREE_WORKGROUPS) ? 3 : (plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
+  const int block_m = 32 * (waves == 3 ? 4 : waves);
   piper::AttnParams ap{};
   ap.query_code = o.query_code;
   ap.query_scale = o.query_scale;
@@ -147,7 +149,7 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   ap.sk64 = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK) * PIPER_KEY_BLOCK);
   ap.nqb = ap.sq32 / PIPER_QUERY_BLOCK;
   ap.nkb = ap.sk64 / PIPER_KEY_BLOCK;
-  ap.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * waves));
+  ap.query_tiles = static_cast<int>(ceil_div(s.query_length, block_m));
   ap.scale_log2e = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   ap.causal_forward = (plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
   ap.xcd_remap = (plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
@@ -400,7 +402,8 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
   if (!(std::isfinite(a->scale) && a->scale > 0.0f))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
-  if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
+  if (a->plan < 0 || a->plan > PIPER_PLAN_MASK || (a->plan & PIPER_PLAN_THREE_WORKGROUPS))
+    return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
   if ((a->flags & ~PIPER_ATTENTION_QK_PER_THREAD) != 0)
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   if (int st = check_input("query", a->query)) return st;

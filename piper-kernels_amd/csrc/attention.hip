@@ -312,6 +312,139 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
   }
 }
 
+// Three 4-wave workgroups per CU: three waves per SIMD (at most 168 VGPRs), each from another
+// workgroup, so one wave's waits on its MFMA results, LDS reads and barriers are covered by the
+// other two waves' VALU work.  That needs the register file of the two-wave kernels' look-ahead
+// (the next block's scores, 32 VGPRs) and most of its LDS: each workgroup streams the tile
+// records through two stages (2 x 20 KiB at D = 128, 120 KiB per CU).  Iteration t: wait for
+// this wave's copies of tile t, barrier (every copy of tile t landed and published, every read
+// of tile t - 1 done), start the copy of tile t + 1 into the stage tile t - 1 used, then the
+// scores, softmax and PV of tile t.  The arithmetic is block_update's, so the output is
+// bit-identical to the other plans.
+template <int D, bool kCausal, int kOut, bool kPerThread>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3, 3)))
+attention_w3_kernel(const AttnParams p) {
+  constexpr int NW = 4;
+  using L = TileLayout<D, NW>;
+  constexpr int kChunksD = D / 32;
+  constexpr int kStages = 2;
+  __shared__ __attribute__((aligned(16))) char smem[kStages * L::kStageBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5;
+  const int n = lane & 31;
+  const TileCoord tc = workgroup_tile<kCausal>(p);
+  const int bh = __builtin_amdgcn_readfirstlane(tc.bh);
+  const int qtile = __builtin_amdgcn_readfirstlane(tc.qtile);
+  const int q0 = qtile * (NW * 32) + wave * 32;
+  const bool wave_live = q0 < p.query_length;
+
+  int tiles = p.nkb;
+  int wave_tiles = wave_live ? p.nkb : 0;
+  if constexpr (kCausal) {
+    const int last_query = min(p.query_length, (qtile + 1) * NW * 32) - 1;
+    tiles = last_query / kKeyBlock + 1;
+    wave_tiles = wave_live ? (min(p.query_length, q0 + 32) - 1) / kKeyBlock + 1 : 0;
+  }
+
+  v4i qf[kChunksD];
+  float cq = 0.0f;
+  const bool fused_live = p.fused_query && wave_live;
+  v4i raw[D / 16];
+  if (fused_live) issue_query_loads<D>(p, bh, q0, n, h, raw);
+  if (!p.fused_query && q0 < p.sq32) {
+    const int8_t* qrow = p.query_code + (static_cast<long>(bh) * p.sq32 + q0 + n) * D + 16 * h;
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) qf[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
+    cq = p.query_scale[(static_cast<long>(bh) * p.nqb + (q0 >> 5)) * kQueryScaleSlots + (kPerThread ? (n & 7) : 0)] *
+         p.scale_log2e;
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) asm volatile("" ::"v"(qf[c]));
+    asm volatile("" ::"v"(cq));
+  } else {
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
+  }
+
+  copy_block<L>(p, smem, bh, 0, wave, lane);  // tile 0 into stage 0
+  if (fused_live) {
+    // wait for the query loads only (issued before this wave's copies of tile 0)
+    if (wave < L::kFullWaves)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds - 1) : "memory");
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * p.scale_log2e;
+  }
+
+  float num[kChunksD][16];
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) num[j][r] = 0.0f;
+  float den = 0.0f;
+  float mref = -__builtin_inff();
+  const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+  v16i bias = {kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias,
+               kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias};
+  asm volatile("" : "+v"(bias));
+
+  for (int t = 0; t < tiles; ++t) {
+    // this wave's copies of tile t landed; after the barrier every wave's have, and every read
+    // of tile t - 1 (stage (t + 1) % 2) is done
+    stage_barrier<0>();
+    if (t + 1 < tiles) copy_block<L>(p, smem + ((t + 1) & 1) * L::kStageBytes, bh, t + 1, wave, lane);
+    if (t < wave_tiles) {
+      const char* stage = smem + (t & 1) * L::kStageBytes;
+      v16i sc[2];
+      block_scores<D, L>(stage, qf, h, krow, bias, sc);
+      float ct[4];
+      if constexpr (kPerThread) {
+        const float4 ks = *reinterpret_cast<const float4*>(stage + D);
+        ct[0] = cq * ks.x;
+        ct[1] = cq * ks.y;
+        ct[2] = cq * ks.z;
+        ct[3] = cq * ks.w;
+      } else {
+        ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
+      }
+      block_update<D, NW, kCausal>(stage, sc, ct, t, q0, n, h, num, den, mref);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const int query = q0 + n;
+  if (!wave_live || query >= p.query_length) return;
+  const float rden = 1.0f / fmaxf(den, 1e-30f);
+  const float* vmean = p.value_mean + static_cast<long>(bh) * D;
+  const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * j + 8 * g + 4 * h;
+      float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (!kCausal) m = *reinterpret_cast<const float4*>(vmean + d0);
+      store4<kOut>(p.output, out_row + d0, fmaf(num[j][4 * g + 0], rden, m.x), fmaf(num[j][4 * g + 1], rden, m.y),
+                   fmaf(num[j][4 * g + 2], rden, m.z), fmaf(num[j][4 * g + 3], rden, m.w));
+    }
+  }
+}
+
+template <int D, bool kCausal, bool kPerThread>
+static hipError_t launch_w3(int out_dtype, const AttnParams& ap, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(ap.query_tiles * ap.batch_heads));
+  const dim3 block(256);
+  switch (out_dtype) {
+    case 0: hipLaunchKernelGGL((attention_w3_kernel<D, kCausal, 0, kPerThread>), grid, block, 0, stream, ap); break;
+    case 1: hipLaunchKernelGGL((attention_w3_kernel<D, kCausal, 1, kPerThread>), grid, block, 0, stream, ap); break;
+    default: hipLaunchKernelGGL((attention_w3_kernel<D, kCausal, 2, kPerThread>), grid, block, 0, stream, ap); break;
+  }
+  return hipGetLastError();
+}
+
 template <int D, int NW, bool kCausal, bool kPerThread>
 static hipError_t launch_out(int out_dtype, const AttnParams& ap, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(ap.query_tiles * ap.batch_heads));
@@ -326,8 +459,12 @@ static hipError_t launch_out(int out_dtype, const AttnParams& ap, hipStream_t st
 
 template <int D, int NW, bool kCausal>
 static hipError_t launch_granularity(int out_dtype, const AttnParams& ap, hipStream_t stream) {
-  return ap.per_thread ? launch_out<D, NW, kCausal, true>(out_dtype, ap, stream)
-                       : launch_out<D, NW, kCausal, false>(out_dtype, ap, stream);
+  if constexpr (NW == 3)
+    return ap.per_thread ? launch_w3<D, kCausal, true>(out_dtype, ap, stream)
+                         : launch_w3<D, kCausal, false>(out_dtype, ap, stream);
+  else
+    return ap.per_thread ? launch_out<D, NW, kCausal, true>(out_dtype, ap, stream)
+                         : launch_out<D, NW, kCausal, false>(out_dtype, ap, stream);
 }
 
 template <int D, int NW>
@@ -338,12 +475,16 @@ static hipError_t launch_causal(bool causal, int out_dtype, const AttnParams& ap
 
 hipError_t launch_attention(int head_dim, bool causal, int out_dtype, int waves, const AttnParams& ap,
                             hipStream_t stream) {
+  // waves: 8 or 4 query waves per workgroup with two waves per SIMD, or 3 for three 4-wave
+  // workgroups per CU (attention_w3_kernel)
   if (head_dim == 128) {
-    return waves == 4 ? launch_causal<128, 4>(causal, out_dtype, ap, stream)
-                      : launch_causal<128, 8>(causal, out_dtype, ap, stream);
+    return waves == 3   ? launch_causal<128, 3>(causal, out_dtype, ap, stream)
+           : waves == 4 ? launch_causal<128, 4>(causal, out_dtype, ap, stream)
+                        : launch_causal<128, 8>(causal, out_dtype, ap, stream);
   }
-  return waves == 4 ? launch_causal<64, 4>(causal, out_dtype, ap, stream)
-                    : launch_causal<64, 8>(causal, out_dtype, ap, stream);
+  return waves == 3   ? launch_causal<64, 3>(causal, out_dtype, ap, stream)
+         : waves == 4 ? launch_causal<64, 4>(causal, out_dtype, ap, stream)
+                      : launch_causal<64, 8>(causal, out_dtype, ap, stream);
 }
 
 }  // namespace piper

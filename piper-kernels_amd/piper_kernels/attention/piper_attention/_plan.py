@@ -26,7 +26,8 @@ PLAN_FOUR_WAVES = 1
 PLAN_CAUSAL_FORWARD = 2
 PLAN_NO_XCD_REMAP = 4
 PLAN_CAUSAL_INTERLEAVE = 8
-PLAN_MASK = 15
+PLAN_THREE_WORKGROUPS = 16
+PLAN_MASK = 31
 
 
 @dataclass(frozen=True)
@@ -40,16 +41,22 @@ class MI355XPlan:
     workgroups of one head run on one XCD (its L2 then serves the head's K/V tiles).
     ``causal_interleave``: causal, longest first, across the heads of an XCD rather than head
     by head (a shorter tail for short and medium sequences; less L2 reuse for long ones).
+    ``three_per_cu`` (4-wave workgroups only): three workgroups per CU, so three waves share each
+    SIMD (a 2-stage LDS ring per workgroup and no score look-ahead, to fit 168 VGPRs) instead of
+    two.
     """
 
     waves: int = 8
     causal_longest_first: bool = True
     xcd_remap: bool = True
     causal_interleave: bool = False
+    three_per_cu: bool = False
 
     def __post_init__(self) -> None:
         if self.waves not in (4, 8):
             raise ValueError(f"waves must be 4 or 8, got {self.waves}")
+        if self.three_per_cu and self.waves != 4:
+            raise ValueError("three workgroups per CU need 4-wave workgroups")
 
     @property
     def block_m(self) -> int:
@@ -59,22 +66,31 @@ class MI355XPlan:
     def plan_id(self) -> int:
         """The ``plan`` field of ``piper_attention_args`` (an OR of PIPER_PLAN_* bits)."""
         return (
-            (PLAN_FOUR_WAVES if self.waves == 4 else 0)
+            (PLAN_FOUR_WAVES if self.waves == 4 and not self.three_per_cu else 0)
             | (0 if self.causal_longest_first else PLAN_CAUSAL_FORWARD)
             | (0 if self.xcd_remap else PLAN_NO_XCD_REMAP)
             | (PLAN_CAUSAL_INTERLEAVE if self.causal_interleave else 0)
+            | (PLAN_THREE_WORKGROUPS if self.three_per_cu else 0)
         )
 
     @classmethod
     def from_id(cls, plan_id: int) -> "MI355XPlan":
-        if not 0 <= plan_id <= PLAN_MASK:
+        if not 0 <= plan_id <= PLAN_MASK or (plan_id & PLAN_THREE_WORKGROUPS and plan_id & PLAN_FOUR_WAVES):
             raise ValueError(f"unknown plan id {plan_id}")
+        three = bool(plan_id & PLAN_THREE_WORKGROUPS)
         return cls(
-            waves=4 if plan_id & PLAN_FOUR_WAVES else 8,
+            waves=4 if plan_id & PLAN_FOUR_WAVES or three else 8,
             causal_longest_first=not plan_id & PLAN_CAUSAL_FORWARD,
             xcd_remap=not plan_id & PLAN_NO_XCD_REMAP,
             causal_interleave=bool(plan_id & PLAN_CAUSAL_INTERLEAVE),
+            three_per_cu=three,
         )
+
+    @classmethod
+    def all_plans(cls) -> list["MI355XPlan"]:
+        """Every distinct plan, by plan id (PIPER_PLAN_THREE_WORKGROUPS implies 4-wave workgroups, so
+        ids that also carry PIPER_PLAN_FOUR_WAVES name the same plans and are left out)."""
+        return [cls.from_id(i) for i in range(PLAN_MASK + 1) if not (i & PLAN_THREE_WORKGROUPS and i & PLAN_FOUR_WAVES)]
 
     def workgroups(self, batch: int, heads: int, query_length: int) -> int:
         return batch * heads * (-(-query_length // self.block_m))
@@ -103,8 +119,8 @@ def frozen_plans() -> dict:
 
 
 def heuristic_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
-    """8-wave workgroups unless that leaves most CUs idle; then 4-wave workgroups (Piper
-    Attention's plan for long non-causal sequences)."""
+    """8-wave workgroups unless that leaves most CUs idle; then 4-wave workgroups (the two-waves-
+    per-SIMD plans' choice by grid size)."""
     wide = MI355XPlan(waves=8)
     if wide.workgroups(batch, heads, query_length) >= COMPUTE_UNITS:
         return wide
@@ -112,13 +128,11 @@ def heuristic_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
 
 
 def piper_heuristic_plan(batch: int, heads: int, query_length: int, is_causal: bool) -> MI355XPlan:
-    """Piper Attention's plan for an untuned shape.  Its 4-wave workgroups run two per CU (a
-    4-stage LDS ring each), out of phase with each other: measured 2-22% faster than 8-wave
-    workgroups on causal and short sequences (c1, c2, c4), and within 2% on long non-causal
-    ones (c3, c5), which keep the 8-wave workgroups unless their grid leaves CUs idle."""
-    if is_causal or query_length <= 8192:
-        return MI355XPlan(waves=4)
-    return heuristic_plan(batch, heads, query_length)
+    """Piper Attention's plan for an untuned shape: three 4-wave workgroups per CU.  With three
+    waves per SIMD from three independent workgroups, one wave's MFMA, LDS and barrier waits are
+    filled by the other two: measured 7-24% faster than the two-waves-per-SIMD plans at c2-c5 and
+    within 1% of the best at c1 (tiny grid)."""
+    return MI355XPlan(waves=4, three_per_cu=True)
 
 
 def sage_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:

@@ -1,7 +1,8 @@
 """Offline launch-plan tuner for the MI355X backend (never called at run time).
 
 Counterpart of the reference's ``benchmarks/tune_piper_attention.py:53-221``: a bounded
-search over the plan axes the gfx950 kernel exposes (query waves per workgroup, causal
+search over the plan axes the gfx950 kernel exposes (query waves per workgroup and
+workgroups per CU, causal
 query-tile order -- forward, longest first head by head, or longest first across the heads of
 an XCD -- and XCD-aware workgroup order), quality-gated, whose result is frozen into
 ``mi355x_plans.json`` for ``select_plan``.
@@ -39,9 +40,11 @@ def candidate_plans(is_causal: bool):
 
     # causal orders: (longest first, interleaved across heads); both flags only matter when causal
     orders = ((True, False), (True, True), (False, False)) if is_causal else ((True, False),)
+    # occupancy: one 8-wave workgroup, two 4-wave workgroups or three 4-wave workgroups per CU
+    occupancy = ((8, False), (4, False), (4, True))
     return [
-        MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x, causal_interleave=i)
-        for w, (o, i), x in product((8, 4), orders, (True, False))
+        MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x, causal_interleave=i, three_per_cu=t)
+        for (w, t), (o, i), x in product(occupancy, orders, (True, False))
     ]
 
 
@@ -98,7 +101,7 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
     return {
         "key": {"batch_heads": batch_heads, "query_length": ql, "key_length": kl, "head_dim": hd, "is_causal": causal},
         "plan": {"waves": best.waves, "causal_longest_first": best.causal_longest_first, "xcd_remap": best.xcd_remap,
-                 "causal_interleave": best.causal_interleave},
+                 "causal_interleave": best.causal_interleave, "three_per_cu": best.three_per_cu},
         "candidates": [
             {"plan_id": p.plan_id, **p.as_dict(), "median_ms": round(medians[p], 5), "bitwise_equal_to_default": passed[p]}
             for p in plans

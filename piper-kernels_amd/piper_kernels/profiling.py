@@ -3,6 +3,8 @@
     python -m piper_kernels.profiling attention --workload c3 --launches 3
         prepare one workload once, then launch only the fused attention kernel (the operator's
         path: the kernel quantises the query itself; --two-step: prepared query codes)
+    python -m piper_kernels.profiling attention --workload c3 --plan 16
+        the same with launch plan 16 (PIPER_PLAN_* bits; default: the plan select_plan picks)
     python -m piper_kernels.profiling prep --workload c3 --launches 3
         run only the prep pipeline (mean partials, mean finalisation, quantisation; K and V
         only unless --two-step)
@@ -36,6 +38,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--bytes", type=int, default=1 << 30)
     parser.add_argument("--two-step", action="store_true", help="quantise the query in the prep, not the kernel")
     parser.add_argument("--operator", choices=["piper_attention", "sage_attention_2pp"], default="piper_attention")
+    parser.add_argument("--plan", type=int, default=None, help="Piper Attention launch plan id (default: the selected plan)")
     args = parser.parse_args(argv)
 
     import torch
@@ -72,8 +75,11 @@ def main(argv: list[str] | None = None) -> int:
         torch.cuda.synchronize()
         print(f"{args.operator} {args.what} {args.workload} x {args.launches} done", flush=True)
         return 0
+    from piper_kernels.attention.piper_attention._plan import MI355XPlan
+
+    plan = None if args.plan is None else MI355XPlan.from_id(args.plan)
     with torch.no_grad():
-        prepared = _prepare_piper_attention(q, k, v, scale, w.is_causal, quantize_query=not fused)
+        prepared = _prepare_piper_attention(q, k, v, scale, w.is_causal, plan=plan, quantize_query=not fused)
         for _ in range(args.launches):
             if args.what == "attention":
                 _launch_piper_attention(prepared)

@@ -232,19 +232,22 @@ def test_plan_selection() -> None:
 
     assert _plan.heuristic_plan(1, 24, 16384) == MI355XPlan(waves=8)
     assert _plan.heuristic_plan(1, 2, 193) == MI355XPlan(waves=4)
-    # Piper Attention's untuned shapes: two 4-wave workgroups per CU unless long and non-causal
-    assert _plan.piper_heuristic_plan(1, 24, 16384, False) == MI355XPlan(waves=8)
-    assert _plan.piper_heuristic_plan(1, 24, 16384, True) == MI355XPlan(waves=4)
-    assert _plan.piper_heuristic_plan(2, 32, 8192, False) == MI355XPlan(waves=4)
-    assert _plan.piper_heuristic_plan(1, 1, 32768, False) == MI355XPlan(waves=4)  # 8-wave grid too small
+    # Piper Attention's untuned shapes: three 4-wave workgroups per CU
+    for shape in ((1, 24, 16384, False), (1, 24, 16384, True), (2, 32, 8192, False), (1, 1, 32768, False)):
+        assert _plan.piper_heuristic_plan(*shape) == MI355XPlan(waves=4, three_per_cu=True)
     assert _plan.sage_plan(1, 24, 16384) == MI355XPlan(waves=4)  # SageAttention2++: two per CU everywhere
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
-                                        "causal_interleave": False, "block_m": 256, "block_n": 64}
+                                        "causal_interleave": False, "three_per_cu": False, "block_m": 256,
+                                        "block_n": 64}
+    assert MI355XPlan(4, three_per_cu=True).plan_id == 16 and MI355XPlan(4, three_per_cu=True).block_m == 128
     with pytest.raises(ValueError):
         MI355XPlan(waves=2)
     with pytest.raises(ValueError):
-        MI355XPlan.from_id(16)
+        MI355XPlan(waves=8, three_per_cu=True)
+    for bad in (17, 32, -1):
+        with pytest.raises(ValueError):
+            MI355XPlan.from_id(bad)
 
 
 def test_plan_ids_round_trip_and_match_the_header() -> None:
@@ -252,16 +255,14 @@ def test_plan_ids_round_trip_and_match_the_header() -> None:
 
     header = (REPO / "include" / "piper_mi355x.h").read_text()
     for name, value in (("FOUR_WAVES", 1), ("CAUSAL_FORWARD", 2), ("NO_XCD_REMAP", 4), ("CAUSAL_INTERLEAVE", 8),
-                        ("MASK", 15)):
+                        ("THREE_WORKGROUPS", 16), ("MASK", 31)):
         assert f"#define PIPER_PLAN_{name} {value}" in header
     assert (_plan.PLAN_FOUR_WAVES, _plan.PLAN_CAUSAL_FORWARD, _plan.PLAN_NO_XCD_REMAP) == (1, 2, 4)
-    assert (_plan.PLAN_CAUSAL_INTERLEAVE, _plan.PLAN_MASK) == (8, 15)
-    ids = set()
-    for plan_id in range(16):
-        plan = MI355XPlan.from_id(plan_id)
-        assert plan.plan_id == plan_id
-        ids.add(plan)
-    assert len(ids) == 16
+    assert (_plan.PLAN_CAUSAL_INTERLEAVE, _plan.PLAN_THREE_WORKGROUPS, _plan.PLAN_MASK) == (8, 16, 31)
+    plans = MI355XPlan.all_plans()
+    assert len(set(plans)) == len(plans) == 24
+    for plan in plans:
+        assert MI355XPlan.from_id(plan.plan_id) == plan
 
 
 def test_frozen_plan_table_lookup_and_fallback(tmp_path, monkeypatch) -> None:
@@ -280,7 +281,7 @@ def test_frozen_plan_table_lookup_and_fallback(tmp_path, monkeypatch) -> None:
         # batch * heads is the key: B2 H12 is the same shape as B1 H24
         assert _plan.select_plan(2, 12, 4096, 4096, 128, False) == MI355XPlan(4, True, False)
         assert _plan.select_plan(1, 24, 4096, 4096, 128, True) == _plan.piper_heuristic_plan(1, 24, 4096, True)
-        assert _plan.select_plan(1, 24, 16384, 16384, 128, False) == MI355XPlan()
+        assert _plan.select_plan(1, 24, 16384, 16384, 128, False) == _plan.piper_heuristic_plan(1, 24, 16384, False)
     finally:
         _plan.frozen_plans.cache_clear()
 

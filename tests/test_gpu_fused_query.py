@@ -67,9 +67,8 @@ def test_fused_query_matches_two_step_bitwise(gfx950_device, shape) -> None:
 def test_fused_query_every_plan(gfx950_device) -> None:
     q, k, v = _inputs((1, 2, 700, 700, 128, torch.float16, True), seed=72)
     reference = None
-    for plan_id in range(16):
-        plan = MI355XPlan.from_id(plan_id)
-        log(f"[fused] plan {plan_id}")
+    for plan in MI355XPlan.all_plans():
+        log(f"[fused] plan {plan.plan_id}")
         two_step, fused = _both(q, k, v, True, gfx950_device, plan=plan)
         out = gpu_attention(fused)
         assert torch.equal(out, gpu_attention(two_step))

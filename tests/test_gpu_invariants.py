@@ -81,7 +81,7 @@ def test_plans_and_repeated_runs_are_bitwise_identical(gfx950_device) -> None:
     k = torch.randn_like(q)
     v = torch.randn_like(q)
     outs = []
-    for plan in [MI355XPlan.from_id(i) for i in range(16)] + [MI355XPlan()]:
+    for plan in MI355XPlan.all_plans() + [MI355XPlan()]:
         prepared = gpu_prepare(q, k, v, 128**-0.5, True, gfx950_device, plan=plan)
         outs.append(gpu_attention(prepared, torch.float32).cpu())
     assert all(torch.equal(outs[0], o) for o in outs[1:])

@@ -141,7 +141,7 @@ def test_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 16
+    args.plan = 32
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward(args, 0)
     args.plan = 0
@@ -236,7 +236,7 @@ def test_fused_attention_validates_before_launching(lib) -> None:
     args.query = native.PiperTensor(fake, 512, 512, 64)
     with pytest.raises(RuntimeError, match="output pointer is NULL"):
         lib.attention_forward_fused(args, 0)
-    args.plan = 16
+    args.plan = 32
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward_fused(args, 0)
     args.plan, args.flags = 0, 4
@@ -298,7 +298,7 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.sage_attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 16
+    args.plan = 32
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.sage_attention_forward(args, 0)
     args.plan, args.flags = 0, 2
