@@ -305,8 +305,13 @@ def prepare(q, k, v, is_causal: bool, granularity: str = "per_warp") -> dict:
 # streaming recurrence
 # --------------------------------------------------------------------------------------
 def attention_from_prepared(
-    prepared: dict, scale: float, is_causal: bool, query_offset: int = 0
-) -> np.ndarray:
+    prepared: dict,
+    scale: float,
+    is_causal: bool,
+    query_offset: int = 0,
+    tie_window: float | None = None,
+    flip_ties: bool = False,
+):
     """The 64-key streaming loop and epilogue of reference.py:61-117, in FP32.
 
     Rows are independent, so ``prepared`` may hold a contiguous subset of the query rows
@@ -316,6 +321,16 @@ def attention_from_prepared(
     Integer products are computed with FP32 matmuls, which are exact here: every partial
     sum is an integer of magnitude below 2**24 (|QK| <= 128*127**2, |PV| <= 64*255*127).
     Returns the FP32 output before the cast to the input dtype.
+
+    With ``tie_window`` (a relative distance, e.g. 1e-5) it also returns, per query row, how
+    far the output may move if every probability code whose unrounded value y = p * s_v * 255
+    lies within ``tie_window * y`` of a rounding tie (a half integer) rounds the other way --
+    what an implementation with other FP32 rounding (exp2/log2, operation order) can do.  A
+    flip of code u_k by one moves output column d by v_code[k, d] * beta / 255 / den, carried
+    by the same recurrence as the numerator, so the bound per row is that recurrence applied
+    to sum_k max_d |v_code[k, d]| over the near-tie keys, divided by the final denominator:
+    ``(out, flip_bound [B, H, Sq])``.  ``flip_ties=True`` (for testing that bound) rounds
+    exactly those near-tie codes the other way.
     """
     q_code = prepared["query_code"]
     k_code = prepared["key_code"]
@@ -329,6 +344,7 @@ def attention_from_prepared(
     scale32 = np.float32(scale)
     out = np.empty((batch, heads, query_length, width), dtype=np.float32)
     query_positions = np.arange(query_length) + query_offset
+    flip_bound = np.zeros((batch, heads, query_length), dtype=np.float64) if tie_window is not None else None
     with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
         for b in range(batch):
             for h in range(heads):
@@ -336,6 +352,7 @@ def attention_from_prepared(
                 numerator = np.zeros((query_length, width), dtype=np.float32)
                 denominator = np.zeros(query_length, dtype=np.float32)
                 running_max = np.full(query_length, -np.inf, dtype=np.float32)
+                flips = np.zeros(query_length, dtype=np.float64)  # the flip bound's numerator
                 for start in range(0, key_length, PV_BLOCK):
                     stop = min(start + PV_BLOCK, key_length)
                     integer_scores = qf @ k_code[b, h, start:stop].astype(np.float32).T
@@ -357,17 +374,28 @@ def attention_from_prepared(
                     probabilities = np.nan_to_num(np.exp(scores - block_max[:, None]))
                     numerator *= old_weight[:, None]
                     denominator = denominator * old_weight + probabilities.sum(axis=-1) * current_weight
-                    p_codes = np.clip(
-                        np.rint(probabilities * block_v_scale[None, :] * P_UINT8_RANGE),
-                        np.float32(0.0),
-                        P_UINT8_RANGE,
-                    )
+                    unrounded = probabilities * block_v_scale[None, :] * P_UINT8_RANGE
+                    p_codes = np.clip(np.rint(unrounded), np.float32(0.0), P_UINT8_RANGE)
+                    if tie_window is not None:
+                        y = unrounded.astype(np.float64)
+                        tie = np.floor(y) + 0.5
+                        near = (np.abs(y - tie) <= tie_window * np.maximum(y, 1.0)) & (tie < 255.0)
+                        if flip_ties:  # round the near-tie codes the other way
+                            other = np.where(p_codes > tie, np.floor(y), np.floor(y) + 1.0).astype(np.float32)
+                            p_codes = np.where(near, other, p_codes)
+                        vmax = np.abs(v_code[b, h, start:stop].astype(np.float64)).max(axis=-1)
+                        weight64 = np.nan_to_num(current_weight.astype(np.float64))
+                        flips = flips * np.nan_to_num(old_weight.astype(np.float64)) + (near @ vmax) * weight64 / 255.0
                     partial = p_codes @ v_code[b, h, start:stop].astype(np.float32)
                     numerator += partial * (current_weight / P_UINT8_RANGE)[:, None]
                     running_max = next_max
                 result = numerator / np.maximum(denominator, DENOMINATOR_FLOOR)[:, None]
                 result += v_mean[b, h][None, :]
                 out[b, h] = result
+                if flip_bound is not None:
+                    flip_bound[b, h] = flips / np.maximum(denominator.astype(np.float64), float(DENOMINATOR_FLOOR))
+    if flip_bound is not None:
+        return out, flip_bound
     return out
 
 

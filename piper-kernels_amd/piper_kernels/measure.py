@@ -3,9 +3,9 @@
 * ``attention_operations`` -- the operation count of
   ``benchmarks/benchmark_attention.py:184-193``: 4*B*H*pairs*D, pairs = Sq*Skv, or the
   causal triangle Sq*(Sq+1)/2.
-* ``measure_quality`` -- the metric definitions of ``benchmarks/lib/quality.py:88-252``:
-  mean/max absolute error, relative L1/L2 error, SQNR in dB and cosine similarity over the
-  finite pairs, with non-finite values counted separately.
+* ``measure_quality`` -- the metrics defined in ``benchmarks/lib/quality.py:88-252`` (mean/max
+  absolute error, relative L1/L2 error, SQNR in dB and cosine similarity over the finite pairs,
+  non-finite values counted separately), evaluated in float64 on the host.
 
 ``measure_mfma_peak`` has no counterpart in the reference (whose benchmarks quote published
 peaks only): it times the library's back-to-back MFMA probe to give the sustained dense
@@ -41,6 +41,8 @@ def effective_tops(operations: int, milliseconds: float) -> float:
 
 @dataclass(frozen=True)
 class QualityMetrics:
+    """Error of an output against a reference (field names as in the benchmark records)."""
+
     mean_absolute_error: float
     max_absolute_error: float
     relative_l1_error: float
@@ -55,64 +57,71 @@ class QualityMetrics:
         return asdict(self)
 
 
-def _comparison_dtype(actual: torch.Tensor, reference: torch.Tensor) -> torch.dtype:
-    if (
-        torch.float64 in (actual.dtype, reference.dtype)
-        or not actual.is_floating_point()
-        or not reference.is_floating_point()
-    ):
-        return torch.float64
-    return torch.float32
+def _as_float64_vector(tensor: torch.Tensor) -> torch.Tensor:
+    if tensor.dtype in (torch.int64, torch.uint64):
+        # float64 holds integers exactly only up to 2^53
+        raise ValueError("64-bit integer tensors cannot be compared exactly in float64")
+    return tensor.detach().reshape(-1).to(device="cpu", dtype=torch.float64)
+
+
+def _sqnr_db(signal_energy: float, noise_energy: float) -> float:
+    if noise_energy == 0.0:
+        return math.inf if signal_energy > 0.0 else math.nan
+    return 10.0 * math.log10(signal_energy / noise_energy) if signal_energy > 0.0 else -math.inf
+
+
+def _cosine(x: torch.Tensor, y: torch.Tensor) -> float:
+    xx, yy = float(x.square().sum()), float(y.square().sum())
+    if xx == 0.0 or yy == 0.0:
+        return 1.0 if xx == yy else 0.0  # two zero vectors agree; a zero and a non-zero do not
+    return max(-1.0, min(1.0, float(torch.dot(x, y)) / math.sqrt(xx * yy)))
 
 
 def measure_quality(actual: torch.Tensor, reference: torch.Tensor) -> QualityMetrics:
-    """Compare ``actual`` with ``reference`` over finite pairs (quality.py:170-252)."""
+    """Error of ``actual`` against ``reference`` (same shape, any floating or small integer dtype).
+
+    The metric definitions are those of the reference's benchmark harness
+    (``benchmarks/lib/quality.py:88-252``); everything is evaluated in float64 on the host:
+
+    * over the positions where both tensors are finite, with e = actual - reference: mean and
+      max of |e|, relative L1 error sum|e| / sum|reference|, relative L2 error
+      ||e||_2 / ||reference||_2, SQNR = 10 log10(sum reference^2 / sum e^2) dB and the cosine
+      of the angle between the two vectors;
+    * counts of non-finite values in each tensor, and of positions where at least one is
+      non-finite and they disagree (NaN against NaN, or the same infinity, agrees).
+
+    With no finite pair every error metric is NaN.
+    """
     if actual.shape != reference.shape:
-        raise ValueError(f"shape mismatch: actual {actual.shape}, reference {reference.shape}")
-    if actual.dtype in (torch.int64, torch.uint64) or reference.dtype in (torch.int64, torch.uint64):
-        raise ValueError(
-            "int64 and uint64 quality inputs are unsupported because float64 cannot "
-            "preserve every full-width integer value"
-        )
-    dtype = _comparison_dtype(actual, reference)
-    a = actual.detach().to(dtype).flatten()
-    r = reference.detach().to(dtype).flatten()
-    a_finite = torch.isfinite(a)
-    r_finite = torch.isfinite(r)
-    finite = a_finite & r_finite
-    nonfinite_positions = ~a_finite | ~r_finite
-    matching = (torch.isnan(a) & torch.isnan(r)) | (a == r)
-    mismatch = int(torch.count_nonzero(nonfinite_positions & ~matching))
-    a_nonfinite = int(torch.count_nonzero(~a_finite))
-    r_nonfinite = int(torch.count_nonzero(~r_finite))
-    if not bool(torch.any(finite)):
-        nan = math.nan
-        return QualityMetrics(nan, nan, nan, nan, nan, nan, a_nonfinite, r_nonfinite, mismatch)
-    a = a[finite]
-    r = r[finite]
-    error = a - r
-    abs_error = error.abs()
-    tiny = torch.finfo(dtype).tiny
-    ref_l1 = r.abs().sum()
-    ref_l2_sq = r.square().sum()
-    err_l2_sq = error.square().sum()
-    sqnr = 10 * torch.log10(ref_l2_sq / err_l2_sq)
-    a_norm = torch.linalg.vector_norm(a)
-    r_norm = torch.linalg.vector_norm(r)
-    if a_norm == 0 or r_norm == 0:
-        cosine = 1.0 if a_norm == 0 and r_norm == 0 else 0.0
-    else:
-        cosine = float((torch.dot(a, r) / (a_norm * r_norm)).clamp(-1, 1))
+        raise ValueError(f"shape mismatch: actual {tuple(actual.shape)}, reference {tuple(reference.shape)}")
+    x = _as_float64_vector(actual)
+    y = _as_float64_vector(reference)
+    x_ok, y_ok = torch.isfinite(x), torch.isfinite(y)
+    same = (x == y) | (torch.isnan(x) & torch.isnan(y))
+    counts = (
+        int((~x_ok).sum()),
+        int((~y_ok).sum()),
+        int(((~x_ok | ~y_ok) & ~same).sum()),
+    )
+    pairs = x_ok & y_ok
+    if not bool(pairs.any()):
+        return QualityMetrics(*([math.nan] * 6), *counts)
+    x, y = x[pairs], y[pairs]
+    error = x - y
+    magnitude = error.abs()
+    tiny = torch.finfo(torch.float64).tiny
+    signal_energy = float(y.square().sum())
+    noise_energy = float(error.square().sum())
     return QualityMetrics(
-        mean_absolute_error=float(abs_error.mean()),
-        max_absolute_error=float(abs_error.max()),
-        relative_l1_error=float(abs_error.sum() / ref_l1.clamp_min(tiny)),
-        relative_l2_error=float(torch.sqrt(err_l2_sq) / torch.sqrt(ref_l2_sq).clamp_min(tiny)),
-        sqnr_db=float(sqnr),
-        cosine_similarity=cosine,
-        actual_nonfinite_count=a_nonfinite,
-        reference_nonfinite_count=r_nonfinite,
-        nonfinite_mismatch_count=mismatch,
+        mean_absolute_error=float(magnitude.mean()),
+        max_absolute_error=float(magnitude.max()),
+        relative_l1_error=float(magnitude.sum()) / max(float(y.abs().sum()), tiny),
+        relative_l2_error=math.sqrt(noise_energy) / max(math.sqrt(signal_energy), tiny),
+        sqnr_db=_sqnr_db(signal_energy, noise_energy),
+        cosine_similarity=_cosine(x, y),
+        actual_nonfinite_count=counts[0],
+        reference_nonfinite_count=counts[1],
+        nonfinite_mismatch_count=counts[2],
     )
 
 

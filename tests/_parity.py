@@ -10,20 +10,18 @@ import torch
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
-# Gate of the attention output against the quantised oracle with matching (per-block)
-# granularity, on the FP32 pre-cast output.  The kernel and the oracle evaluate the same
-# formula with different FP32 rounding (exp2/log2 vs exp/log, operation order), so a P code
-# can differ by one where p*vs*255 lies within rounding of a half integer; one such flip
-# moves an output by |v_code| / (255 * den).  den grows with the key length, so short key
-# sequences get a looser max-abs bound.  Mean error and cosine are gated tightly everywhere.
-ATTENTION_MAX_ABS = 2e-3  # key length >= 1024
-ATTENTION_MAX_ABS_SHORT = 1e-2  # key length < 1024
+# Gate of the attention output against the quantised oracle with matching granularity, on the
+# FP32 pre-cast output: max |err| <= 2e-3 in every row (the stated example tolerance), mean
+# |err| <= 1e-4 and cosine >= 0.9999.  The kernel and the oracle evaluate the same formula with
+# different FP32 rounding (exp2/log2 vs exp/log, operation order): their unrounded probability
+# codes y = p * s_v * 255 agree to ~3e-6 relative, so a code whose y lies within that of a half
+# integer may round the other way.  Such a flip moves the row by |v_code| * beta / (255 * den);
+# the oracle bounds what all near-tie codes of a row can move it (TIE_WINDOW, a relative
+# distance), and that bound is added to the row's 2e-3.
+ATTENTION_MAX_ABS = 2e-3
 ATTENTION_MEAN_ABS = 1e-4
 ATTENTION_COSINE = 0.9999
-
-
-def max_abs_gate(key_length: int) -> float:
-    return ATTENTION_MAX_ABS if key_length >= 1024 else ATTENTION_MAX_ABS_SHORT
+TIE_WINDOW = 1e-5
 
 
 def log(msg: str) -> None:
@@ -148,16 +146,28 @@ def attention_metrics(actual: np.ndarray, expected: np.ndarray) -> dict:
     return q.as_dict()
 
 
+def oracle_attention(prepared: dict, scale: float, is_causal: bool, query_offset: int = 0):
+    """The oracle's FP32 output and its per-row tie-flip bound (see the gate above)."""
+    from oracle import piper_oracle as oracle
+
+    return oracle.attention_from_prepared(prepared, scale, is_causal, query_offset, tie_window=TIE_WINDOW)
+
+
 def assert_attention_close(actual: np.ndarray, expected: np.ndarray, label: str = "",
-                           max_abs: float | None = None, mean_abs: float = ATTENTION_MEAN_ABS,
-                           cosine: float = ATTENTION_COSINE, key_length: int = 1) -> dict:
-    if max_abs is None:
-        max_abs = max_abs_gate(key_length)
+                           flip_bound: np.ndarray | None = None, max_abs: float = ATTENTION_MAX_ABS,
+                           mean_abs: float = ATTENTION_MEAN_ABS, cosine: float = ATTENTION_COSINE) -> dict:
+    """Every row within max_abs (plus that row's tie-flip bound, [B, H, Sq], when given); mean
+    error and cosine over the whole tensor."""
     m = attention_metrics(actual, expected)
+    row_err = np.abs(np.asarray(actual, np.float64) - np.asarray(expected, np.float64)).max(axis=-1)
+    allowed = max_abs + (0.0 if flip_bound is None else flip_bound)
+    worst = np.unravel_index(int(np.argmax(row_err - allowed)), row_err.shape)
+    flipped_rows = 0 if flip_bound is None else int((flip_bound > 0).sum())
     log(f"[parity] {label} max_abs={m['max_absolute_error']:.3e} mean_abs={m['mean_absolute_error']:.3e} "
-        f"cos={m['cosine_similarity']:.7f} sqnr={m['sqnr_db']:.2f}dB")
+        f"cos={m['cosine_similarity']:.7f} sqnr={m['sqnr_db']:.2f}dB rows_with_near_ties={flipped_rows} "
+        f"worst_row={tuple(int(i) for i in worst)} err={row_err[worst]:.3e} allowed={np.broadcast_to(allowed, row_err.shape)[worst]:.3e}")
     assert np.all(np.isfinite(actual)), f"{label}: non-finite output"
-    assert m["max_absolute_error"] <= max_abs, f"{label}: {m}"
+    assert (row_err <= allowed).all(), f"{label}: row {worst} error {row_err[worst]:.3e} beyond its gate; {m}"
     assert m["mean_absolute_error"] <= mean_abs, f"{label}: {m}"
     assert m["cosine_similarity"] >= cosine, f"{label}: {m}"
     return m

@@ -322,6 +322,24 @@ def test_quality_metrics_have_expected_definitions() -> None:
     assert m.actual_nonfinite_count == m.reference_nonfinite_count == m.nonfinite_mismatch_count == 0
 
 
+def test_quality_metric_edge_cases() -> None:
+    exact = measure_quality(torch.tensor([1.0, -2.0]), torch.tensor([1.0, -2.0]))
+    assert exact.max_absolute_error == 0 and math.isinf(exact.sqnr_db) and exact.cosine_similarity == 1.0
+    zeros = measure_quality(torch.zeros(3), torch.zeros(3))
+    assert zeros.cosine_similarity == 1.0 and math.isnan(zeros.sqnr_db) and zeros.relative_l2_error == 0
+    assert measure_quality(torch.zeros(2), torch.ones(2)).cosine_similarity == 0.0
+    opposite = measure_quality(torch.tensor([1.0, 2.0]), torch.tensor([-1.0, -2.0]))
+    assert opposite.cosine_similarity == -1.0 and opposite.relative_l1_error == pytest.approx(2.0)
+    none = measure_quality(torch.tensor([math.nan]), torch.tensor([1.0]))
+    assert math.isnan(none.mean_absolute_error) and none.nonfinite_mismatch_count == 1
+    # integer and half inputs widen exactly; 64-bit integers are refused; shapes must match
+    assert measure_quality(torch.tensor([3], dtype=torch.int8), torch.tensor([1.0], dtype=torch.float16)).max_absolute_error == 2
+    with pytest.raises(ValueError, match="64-bit integer"):
+        measure_quality(torch.tensor([1]), torch.tensor([1.0]))
+    with pytest.raises(ValueError, match="shape mismatch"):
+        measure_quality(torch.zeros(2), torch.zeros(3))
+
+
 def test_quality_counts_nonfinite_values() -> None:
     m = measure_quality(torch.tensor([math.nan, math.inf, 1.0]), torch.tensor([math.nan, 2.0, 1.0]))
     assert m.mean_absolute_error == 0 and math.isinf(m.sqnr_db)
@@ -357,3 +375,36 @@ def test_student_t_workload_has_constant_value_heads() -> None:
     q, k, v = make_inputs(small, heads=[0, 39], batches=[1])
     assert torch.equal(v[0, 0], v[0, 0, :1].expand_as(v[0, 0]))
     assert not torch.equal(v[0, 1], v[0, 1, :1].expand_as(v[0, 1]))
+
+
+def test_integration_ops_coexist_with_the_reference_registration() -> None:
+    """INTEGRATION.md's HIP module registers its own qualified op, so it coexists with the
+    reference's Triton registration of piper_kernels::piper_attention (triton.py:984), which the
+    reference imports on ROCm too (dispatch.py:10-15); a second registration of one name raises."""
+    import re
+    import subprocess
+    import sys
+
+    text = (REPO / "INTEGRATION.md").read_text()
+    names = re.findall(r'custom_op\("(piper_kernels::[a-z0-9_]+)"', text)
+    assert names and "piper_kernels::piper_attention" not in names
+    script = f"""
+import torch
+SIG = "(Tensor query, Tensor key, Tensor value, float scale, bool is_causal) -> Tensor"
+lib = torch.library.Library("piper_kernels", "FRAGMENT")
+lib.define("piper_attention" + SIG)   # stand-in for the reference's Triton registration
+for name in {names!r}:
+    @torch.library.custom_op(name, mutates_args=())
+    def op(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scale: float, is_causal: bool) -> torch.Tensor:
+        return query.clone()
+try:
+    lib.define("piper_attention" + SIG)
+except RuntimeError:
+    print("duplicate registration refused")
+print(sorted(n for n in dir(torch.ops.piper_kernels) if n.startswith("piper_attention")))
+"""
+    result = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    assert result.returncode == 0, result.stderr
+    assert "duplicate registration refused" in result.stdout
+    assert "'piper_attention', 'piper_attention_hip'" in result.stdout
+

@@ -1,9 +1,10 @@
 """GPU parity of the HIP path with the CPU oracle: bit-exact prep, tolerance attention.
 
 Mirrors the reference's GPU suite (tests/attention/piper_attention/test_triton.py) on
-MI355X: the oracle here is the per-block ("per_warp") restatement of the reference,
-i.e. the granularity the kernels implement, exactly as test_triton.py:35-36 compares
-against the reference with matching granularity.
+MI355X: the HIP path is compared with the oracle at the same Q/K granularity, as
+test_triton.py:35-36 compares its backend with the reference.  Both of the reference's
+granularities run: per thread group ("per_thread", the portable path's default and the
+operator's) and per block ("per_warp", its grouped SM12x Triton path).
 """
 
 from __future__ import annotations
@@ -20,6 +21,7 @@ from _parity import (
     gpu_prepare,
     load_golden,
     log,
+    oracle_attention,
     prepared_numpy,
 )
 from oracle import piper_oracle as oracle
@@ -49,13 +51,18 @@ def test_prep_is_bit_exact_with_golden_fixture(fixture, gfx950_device) -> None:
 
 
 @pytest.mark.parametrize("fixture", FIXTURES, ids=[p.stem for p in FIXTURES])
-@pytest.mark.parametrize("plan", [MI355XPlan(waves=8), MI355XPlan(waves=4)], ids=["w8", "w4"])
+@pytest.mark.parametrize(
+    "plan", [MI355XPlan(waves=8), MI355XPlan(waves=4), MI355XPlan(waves=4, three_per_cu=True)], ids=["w8", "w4", "w3"]
+)
 def test_attention_matches_golden_fixture(fixture, plan, gfx950_device) -> None:
     g = load_golden(fixture)
-    log(f"[case] attention golden {fixture.stem} plan={plan.waves}")
+    log(f"[case] attention golden {fixture.stem} plan={plan.plan_id}")
     prepared = gpu_prepare(g["query"], g["key"], g["value"], g["scale"], g["is_causal"], gfx950_device, plan=plan)
     out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
-    assert_attention_close(out32, g["output_per_warp"], f"{fixture.stem} fp32", key_length=g["key"].shape[2])
+    expected, bound = oracle_attention(oracle.prepare(g["query"], g["key"], g["value"], g["is_causal"], "per_warp"),
+                                       g["scale"], g["is_causal"])
+    np.testing.assert_array_equal(expected, g["output_per_warp"])  # the fixture is the oracle's output
+    assert_attention_close(out32, g["output_per_warp"], f"{fixture.stem} fp32", flip_bound=bound)
     # the output in the input dtype is the FP32 result rounded to nearest even
     out = gpu_attention(prepared, prepared.output.dtype).float().cpu().numpy()
     np.testing.assert_array_equal(out, oracle.cast_output(out32, str(g["dtype"])))
@@ -87,9 +94,9 @@ def test_random_shapes_match_oracle(shape, gfx950_device) -> None:
     prep = oracle.prepare(q, k, v, causal, "per_warp")
     prepared = gpu_prepare(q, k, v, scale, causal, gfx950_device)
     assert_prep_bit_exact(prepared_numpy(prepared), prep, prepared.shape, causal)
-    expected = oracle.attention_from_prepared(prep, scale, causal)
+    expected, bound = oracle_attention(prep, scale, causal)
     out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
-    assert_attention_close(out32, expected, f"random {shape}", key_length=sk)
+    assert_attention_close(out32, expected, f"random {shape}", flip_bound=bound)
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(str(x) for x in s[:5]) + f"-{s[5]}-c{int(s[6])}")
@@ -101,9 +108,10 @@ def test_per_thread_granularity_matches_oracle(shape, gfx950_device) -> None:
     log(f"[case] per_thread {shape}")
     g = torch.Generator().manual_seed(2000 + sq + sk + d)
     # every thread group gets its own magnitude, so a scale read from the wrong group shows:
-    # query row r scaled by 1 + (r % 8) / 8 (group r % 8), key row r by 1 + ((r % 8) // 2) / 4
-    q_rows = 1 + (torch.arange(sq) % 8).reshape(1, 1, sq, 1) / 8
-    k_rows = 1 + (torch.arange(sk) % 8 // 2).reshape(1, 1, sk, 1) / 4
+    # query row r scaled by 1 + 4 (r % 8) / 7 (group r % 8: 1x to 5x), key row r by
+    # 1 + 4 ((r % 8) // 2) / 3 (group (r % 8) // 2: 1x to 5x)
+    q_rows = 1 + 4 * (torch.arange(sq) % 8).reshape(1, 1, sq, 1) / 7
+    k_rows = 1 + 4 * (torch.arange(sk) % 8 // 2).reshape(1, 1, sk, 1) / 3
     q = (torch.randn((b, h, sq, d), generator=g) * q_rows).to(dtype)
     k = (torch.randn((b, h, sk, d), generator=g) * k_rows + torch.randn((b, h, 1, d), generator=g)).to(dtype)
     v = (torch.randn((b, h, sk, d), generator=g) + 2 * torch.randn((b, h, 1, d), generator=g)).to(dtype)
@@ -111,9 +119,9 @@ def test_per_thread_granularity_matches_oracle(shape, gfx950_device) -> None:
     prep = oracle.prepare(q, k, v, causal, "per_thread")
     prepared = gpu_prepare(q, k, v, scale, causal, gfx950_device, qk_granularity="per_thread")
     assert_prep_bit_exact(prepared_numpy(prepared), prep, prepared.shape, causal)
-    expected = oracle.attention_from_prepared(prep, scale, causal)
+    expected, bound = oracle_attention(prep, scale, causal)
     out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
-    assert_attention_close(out32, expected, f"per_thread {shape}", key_length=sk)
+    assert_attention_close(out32, expected, f"per_thread {shape}", flip_bound=bound)
     # the fused entry point quantises the query per thread group in its prologue, bit-identically
     fused = gpu_prepare(q, k, v, scale, causal, gfx950_device, quantize_query=False, qk_granularity="per_thread")
     assert torch.equal(gpu_attention(fused, torch.float32).cpu(), torch.from_numpy(out32))
@@ -128,7 +136,10 @@ def test_per_thread_output_matches_golden_fixture(fixture, gfx950_device) -> Non
         qk_granularity="per_thread",
     )
     out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
-    assert_attention_close(out32, g["output_per_thread"], f"{fixture.stem} per_thread", key_length=g["key"].shape[2])
+    expected, bound = oracle_attention(oracle.prepare(g["query"], g["key"], g["value"], g["is_causal"], "per_thread"),
+                                       g["scale"], g["is_causal"])
+    np.testing.assert_array_equal(expected, g["output_per_thread"])
+    assert_attention_close(out32, g["output_per_thread"], f"{fixture.stem} per_thread", flip_bound=bound)
 
 
 MEAN_CASES = [

@@ -1,10 +1,15 @@
 """Parity at the BASELINE.json configurations (c1-c5) on MI355X.
 
 Heads are independent (own means, codes, softmax), so a head subset of a configuration is
-that configuration's computation for those heads.  Prep is compared bit for bit on the
-checked heads; the attention output on row slices (rows are independent; causal slices
-carry their absolute offset).  Size-independent properties run on the full shapes: exact
-preservation of constant-V heads (c5) and causal independence of future V rows (c4).
+that configuration's computation for those heads.  Each case runs at both of the reference's
+Q/K granularities: per thread group (the operator's path and the reference portable path's
+default, reference.py:42) and per block.  Prep is compared bit for bit on the checked heads
+(a prep that also quantises the query); the attention output comes from the operator's path
+-- a K/V prep and the fused entry point, whose kernel quantises the query in its prologue --
+checked to equal the two-step path bit for bit and compared with the oracle on row slices
+(rows are independent; causal slices carry their absolute offset).  Size-independent
+properties run on the full shapes: exact preservation of constant-V heads (c5) and causal
+independence of future V rows (c4).
 """
 
 from __future__ import annotations
@@ -13,53 +18,80 @@ import numpy as np
 import pytest
 import torch
 
-from _parity import assert_attention_close, assert_prep_bit_exact, gpu_attention, gpu_prepare, log, prepared_numpy
+from _parity import (
+    assert_attention_close,
+    assert_prep_bit_exact,
+    gpu_attention,
+    gpu_prepare,
+    log,
+    oracle_attention,
+    prepared_numpy,
+)
 from oracle import piper_oracle as oracle
 from piper_kernels.workloads import WORKLOADS, make_inputs
 
 pytestmark = pytest.mark.gpu
 
+GRANULARITIES = ["per_thread", "per_warp"]
 
-def _oracle_rows(prep: dict, rows: slice, scale: float, causal: bool) -> np.ndarray:
+
+def _row_slice(prep: dict, rows: slice) -> dict:
     sub = dict(prep)
     sub["query_code"] = prep["query_code"][:, :, rows]
     sub["query_scale"] = prep["query_scale"][:, :, rows]
-    return oracle.attention_from_prepared(sub, scale, causal, query_offset=rows.start)
+    return sub
 
 
-def _check_heads(name: str, batches: list[int], heads: list[int], row_slices: list[slice], device) -> None:
+def _oracle_rows(prep: dict, rows: slice, scale: float, causal: bool):
+    """Oracle output and tie-flip bound of query rows ``rows``."""
+    return oracle_attention(_row_slice(prep, rows), scale, causal, query_offset=rows.start)
+
+
+def _check_heads(name: str, batches: list[int], heads: list[int], row_slices: list[slice], device,
+                 granularity: str) -> None:
     w = WORKLOADS[name]
     q, k, v = make_inputs(w, batches=batches, heads=heads)
     scale = w.head_dim**-0.5
-    log(f"[case] {name} batches={batches} heads={heads} shape={tuple(q.shape)}")
-    prep = oracle.prepare(q, k, v, w.is_causal, "per_warp")
-    prepared = gpu_prepare(q, k, v, scale, w.is_causal, device)
-    assert_prep_bit_exact(prepared_numpy(prepared), prep, prepared.shape, w.is_causal)
-    out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
+    log(f"[case] {name} {granularity} batches={batches} heads={heads} shape={tuple(q.shape)}")
+    prep = oracle.prepare(q, k, v, w.is_causal, granularity)
+    two_step = gpu_prepare(q, k, v, scale, w.is_causal, device, qk_granularity=granularity)
+    assert_prep_bit_exact(prepared_numpy(two_step), prep, two_step.shape, w.is_causal)
+    fused = gpu_prepare(q, k, v, scale, w.is_causal, device, quantize_query=False, qk_granularity=granularity)
+    out32 = gpu_attention(fused, torch.float32)
+    assert torch.equal(out32, gpu_attention(two_step, torch.float32)), "fused and two-step paths differ"
+    out32 = out32.cpu().numpy()
     assert np.isfinite(out32).all()
     for rows in row_slices:
-        expected = _oracle_rows(prep, rows, scale, w.is_causal)
-        assert_attention_close(out32[:, :, rows], expected, f"{name} rows {rows.start}:{rows.stop}", key_length=w.key_length)
+        expected, bound = _oracle_rows(prep, rows, scale, w.is_causal)
+        assert_attention_close(out32[:, :, rows], expected, f"{name} {granularity} rows {rows.start}:{rows.stop}",
+                               flip_bound=bound)
 
 
-def test_c1_full(gfx950_device) -> None:
-    _check_heads("c1", [0], list(range(8)), [slice(0, 1024)], gfx950_device)
+@pytest.mark.parametrize("granularity", GRANULARITIES)
+def test_c1_full(gfx950_device, granularity) -> None:
+    _check_heads("c1", [0], list(range(8)), [slice(0, 1024)], gfx950_device, granularity)
 
 
-def test_c2_full_prep_and_row_slices(gfx950_device) -> None:
-    _check_heads("c2", [0], list(range(24)), [slice(0, 256), slice(3840, 4096)], gfx950_device)
+@pytest.mark.parametrize("granularity", GRANULARITIES)
+def test_c2_full_prep_and_row_slices(gfx950_device, granularity) -> None:
+    _check_heads("c2", [0], list(range(24)), [slice(0, 256), slice(3840, 4096)], gfx950_device, granularity)
 
 
-def test_c3_heads(gfx950_device) -> None:
-    _check_heads("c3", [0], [0, 11, 23], [slice(0, 256), slice(8192, 8448), slice(16128, 16384)], gfx950_device)
+@pytest.mark.parametrize("granularity", GRANULARITIES)
+def test_c3_heads(gfx950_device, granularity) -> None:
+    _check_heads("c3", [0], [0, 11, 23], [slice(0, 256), slice(8192, 8448), slice(16128, 16384)], gfx950_device,
+                 granularity)
 
 
-def test_c4_causal_heads(gfx950_device) -> None:
-    _check_heads("c4", [0, 3], [0, 31], [slice(0, 256), slice(4000, 4160), slice(7936, 8192)], gfx950_device)
+@pytest.mark.parametrize("granularity", GRANULARITIES)
+def test_c4_causal_heads(gfx950_device, granularity) -> None:
+    _check_heads("c4", [0, 3], [0, 31], [slice(0, 256), slice(4000, 4160), slice(7936, 8192)], gfx950_device,
+                 granularity)
 
 
-def test_c5_student_t_heads(gfx950_device) -> None:
-    _check_heads("c5", [0, 1], [0, 19, 20, 39], [slice(0, 128), slice(32640, 32768)], gfx950_device)
+@pytest.mark.parametrize("granularity", GRANULARITIES)
+def test_c5_student_t_heads(gfx950_device, granularity) -> None:
+    _check_heads("c5", [0, 1], [0, 19, 20, 39], [slice(0, 128), slice(32640, 32768)], gfx950_device, granularity)
 
 
 def test_c3_full_shape_runs_and_matches_its_head_subset(gfx950_device) -> None:
@@ -125,30 +157,34 @@ def _sdpa_rows_float64(q, k, v, rows: slice, scale: float, causal: bool) -> np.n
 @pytest.mark.parametrize(
     "name,batches,heads,rows",
     [("c1", [0], list(range(8)), slice(0, 1024)), ("c2", [0], [0, 23], slice(0, 512)),
-     ("c4", [2], [5], slice(7680, 8192))],
-    ids=["c1", "c2", "c4"],
+     ("c3", [0], [0, 17], slice(8000, 8256)), ("c4", [2], [5], slice(7680, 8192)),
+     ("c5", [0, 1], [3, 25, 38], slice(20000, 20128))],
+    ids=["c1", "c2", "c3", "c4", "c5"],
 )
 def test_output_against_fp64_sdpa(gfx950_device, name, batches, heads, rows) -> None:
-    """The second correctness level of the task statement, against full-precision attention.
+    """The second correctness level of the task statement, against full-precision attention, on
+    the operator's path (per-thread-group Q/K scales, the kernel quantising the query).
 
     Gate: cosine similarity >= 0.9995 against FP64 SDPA (the stated example tolerance), and a
     max-abs error no larger than the quantized reference's own distance to FP64 SDPA plus 2e-3:
     the stated example max-abs (2e-3) is below what the reference algorithm itself reaches
-    against SDPA (INT8 Q/K/V and UINT8 P quantisation), so the kernel is held to "no further
+    against SDPA (INT8 Q/K/V and UINT8 P quantisation, largest on c5's Student-t inputs, where
+    an outlier sets a whole 32- or 64-row block's scale), so the kernel is held to "no further
     from SDPA than the reference, within the 2e-3 the kernel may differ from the reference".
     """
     w = WORKLOADS[name]
     q, k, v = make_inputs(w, batches=batches, heads=heads)
     scale = w.head_dim**-0.5
     log(f"[case] sdpa envelope {name} batches={batches} heads={heads} rows={rows.start}:{rows.stop}")
-    prepared = gpu_prepare(q, k, v, scale, w.is_causal, device=gfx950_device)
+    prepared = gpu_prepare(q, k, v, scale, w.is_causal, device=gfx950_device, quantize_query=False,
+                           qk_granularity="per_thread")
     got = gpu_attention(prepared, torch.float32).cpu().numpy()[:, :, rows].astype(np.float64)
     expected = _sdpa_rows_float64(q, k, v, rows, scale, w.is_causal)
-    reference = _oracle_rows(oracle.prepare(q, k, v, w.is_causal, "per_warp"), rows, scale, w.is_causal)
-    reference_max = np.abs(reference.astype(np.float64) - expected).max()
+    reference, _ = _oracle_rows(oracle.prepare(q, k, v, w.is_causal, "per_thread"), rows, scale, w.is_causal)
+    reference_err = np.abs(reference.astype(np.float64) - expected)
     err = np.abs(got - expected)
     cosine = (got * expected).sum() / np.sqrt((got * got).sum() * (expected * expected).sum())
-    log(f"[quality] {name} vs fp64 sdpa: max {err.max():.3e} (reference {reference_max:.3e}) mean {err.mean():.3e} "
-        f"cos {cosine:.6f}")
+    log(f"[quality] {name} vs fp64 sdpa: max {err.max():.3e} (reference {reference_err.max():.3e}) mean {err.mean():.3e} "
+        f"(reference {reference_err.mean():.3e}) cos {cosine:.6f}")
     assert cosine >= 0.9995
-    assert err.max() <= reference_max + 2e-3
+    assert err.max() <= reference_err.max() + 2e-3

@@ -162,6 +162,58 @@ def test_per_thread_key_groups_are_rows_8a_2t_c() -> None:
             assert float(scale[0, 0, row]) == exact_scale(float(group_max))
 
 
+def test_group_scale_slots_are_the_per_row_scales_of_each_thread_group() -> None:
+    """query_group_scales_per_thread / key_group_scales_per_thread (the slots the HIP prep stores)
+    against a direct loop over each zero-padded block's thread groups, and against the per-row
+    scales of quantize_*_per_thread (pinned by the interleave tables above), on ragged lengths."""
+    rng = np.random.default_rng(71)
+    for length in (1, 31, 33, 64, 95, 130):
+        x = (rng.standard_normal((1, 2, length, 16)) * rng.uniform(0.1, 8.0, (1, 2, length, 1))).astype(np.float32)
+        q_slots = oracle.query_group_scales_per_thread(x)
+        k_slots = oracle.key_group_scales_per_thread(x)
+        assert q_slots.shape == (1, 2, -(-length // 32), 8) and k_slots.shape == (1, 2, -(-length // 64), 4)
+        for h in range(2):
+            for block in range(q_slots.shape[2]):
+                for t in range(8):
+                    rows = [32 * block + t + 8 * i for i in range(4)]
+                    amax = max((float(np.abs(x[0, h, r]).max()) for r in rows if r < length), default=0.0)
+                    assert float(q_slots[0, h, block, t]) == exact_scale(amax)
+            for block in range(k_slots.shape[2]):
+                for t in range(4):
+                    rows = [64 * block + 8 * a + 2 * t + c for a in range(8) for c in range(2)]
+                    amax = max((float(np.abs(x[0, h, r]).max()) for r in rows if r < length), default=0.0)
+                    assert float(k_slots[0, h, block, t]) == exact_scale(amax)
+        _, q_rows = oracle.quantize_query_per_thread(x)
+        _, k_rows = oracle.quantize_key_per_thread(x)
+        r = np.arange(length)
+        assert np.array_equal(q_rows, q_slots[:, :, r // 32, r % 8])
+        assert np.array_equal(k_rows, k_slots[:, :, r // 64, (r % 8) // 2])
+
+
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_tie_flip_bound_covers_codes_rounded_the_other_way(is_causal: bool) -> None:
+    """attention_from_prepared's flip bound: rounding every near-tie probability code the other
+    way (a planted rounding difference) moves each row by no more than the bound, and rows with
+    no near-tie code are unchanged."""
+    torch.manual_seed(72)
+    q = torch.randn(1, 2, 96, 64, dtype=torch.float16)
+    k = torch.randn(1, 2, 96, 64, dtype=torch.float16) * 2
+    v = torch.randn(1, 2, 96, 64, dtype=torch.float16) + 3
+    prep = oracle.prepare(q, k, v, is_causal, "per_thread")
+    scale = 64**-0.5
+    exact = oracle.attention_from_prepared(prep, scale, is_causal)
+    for window in (1e-5, 2e-2):
+        out, bound = oracle.attention_from_prepared(prep, scale, is_causal, tie_window=window)
+        assert np.array_equal(out, exact) and bound.shape == exact.shape[:3] and (bound >= 0).all()
+        flipped, same_bound = oracle.attention_from_prepared(prep, scale, is_causal, tie_window=window, flip_ties=True)
+        assert np.array_equal(same_bound, bound)
+        moved = np.abs(flipped.astype(np.float64) - exact).max(axis=-1)
+        assert (moved <= bound * (1 + 1e-5) + 1e-6).all()
+        assert not moved[bound == 0].any()
+    # the wide window catches many codes, and flipping them does move the output
+    assert (bound > 0).mean() > 0.5 and moved.max() > 1e-3
+
+
 @pytest.mark.parametrize("granularity", ["per_thread", "per_warp"])
 def test_quantize_query_key_bound_and_centering(granularity: str) -> None:
     """tests/attention/test_qk_quantization.py:10-33 of the reference."""
