@@ -12,13 +12,27 @@ Prints ONE JSON line.  ``value`` = whole-call TOPS (reference op count 4*B*H*Sq*
 call, benchmarks/benchmark_attention.py:184-193).  ``roofline`` prices the dominant
 kernel (the fused attention kernel) against MI355X's dense INT8 MFMA peak, with its
 average duration measured by HIP events recorded on the launch stream inside the timed
-region.  ``mfma_peak_measured`` is the sustained dense INT8 and FP8 MFMA rate of the same GPU
-(the library's back-to-back MFMA probe, results checked), and ``attention_kernel`` also
-reports the kernel's fraction of that measured INT8 rate.  ``mfma_valu_sharing`` times the same
-probe's MFMA-only, FP32-FMA-only and interleaved kinds at the kernel's occupancy (two waves per
-SIMD): how much MFMA execution and VALU issue overlap on this GPU.  ``cpu_baseline`` times the CPU
-oracle (a numpy restatement of the reference's portable path) on a bounded slice of the same
-workload, on one host thread.
+region.  Warm-up runs at least ``--warmup`` steps and at least ``--warmup-ms`` of GPU time, so
+the clock has ramped before timing starts.
+
+Beside the timing (all after the timed region):
+
+* ``quality``: the timed call's output against FP64 softmax attention on a row slice, next to
+  the quantised reference's own distance on the same rows, and against the quantised reference
+  (the CPU oracle's output for every head the CPU baseline computed): max and mean absolute
+  error, SQNR and cosine (the reference harness's quality columns,
+  benchmarks/benchmark_attention.py:249,380);
+* ``cpu_baseline``: the CPU oracle (a numpy restatement of the reference's portable path) on
+  whole heads of the same workload, one head per host thread on all the host threads the run
+  may use, per thread-group Q/K scales (the reference's default) and, on one round of heads,
+  per block;
+* ``mfma_peak_measured``: the sustained dense INT8 and FP8 MFMA rate of the same GPU (the
+  measurement library's back-to-back MFMA probe, results checked), with the kernel's fraction
+  of it in ``attention_kernel``;
+* ``issue_sharing``: the measurement library's issue probe (VALU issue per waves per SIMD,
+  MFMA/VALU overlap across and within waves, the attention loop's mix with and without its
+  MFMAs, LDS bandwidth);
+* ``environment``: GPU, clocks, software versions, host CPU and the source revision.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline] [--two-step]
 """
@@ -28,6 +42,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -48,9 +64,12 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--warmup-ms", type=float, default=300.0, help="minimum GPU time of the warm-up steps")
     parser.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
+    parser.add_argument("--quality-rows", type=int, default=256, help="query rows per head in the FP64 SDPA check")
+    parser.add_argument("--no-probes", action="store_true", help="skip the MFMA-peak and issue probes")
     parser.add_argument(
         "--two-step", action="store_true", help="time the prep of Q, K, V + attention on prepared query codes"
     )
@@ -80,45 +99,206 @@ def traffic_from_profile(workload: str):
         return None
 
 
-def cpu_baseline(workload, seconds: float) -> dict:
-    """Time the CPU oracle on whole (batch 0) heads of the workload until ~`seconds` elapse.
+# ---------------------------------------------------------------------------------------
+# CPU baseline: the oracle, one (batch, head) slice per worker process and host thread
+# ---------------------------------------------------------------------------------------
+def _cpu_worker_ready() -> int:
+    from threadpoolctl import threadpool_limits
 
-    Each head is the full reference computation for that head: prep (means, Q/K/V codes) and
-    the 64-key streaming loop over every query row, numpy on one thread.
-    """
-    import platform
+    from oracle import piper_oracle  # noqa: F401  (import before timing)
+    from piper_kernels import workloads  # noqa: F401
 
-    import numpy as np
+    threadpool_limits(limits=1)
+    return os.getpid()
+
+
+def _cpu_head(task: tuple[str, int, int, str]):
+    """The full reference computation of one (batch, head) slice on one thread: K/V means,
+    Q/K/V codes and the 64-key streaming loop over every query row.  Returns the slice, its
+    wall time (input generation excluded) and the FP32 output [S, D]."""
     from threadpoolctl import threadpool_limits
 
     from oracle import piper_oracle as oracle
+    from piper_kernels.workloads import WORKLOADS, make_inputs
+
+    name, b, h, granularity = task
+    w = WORKLOADS[name]
+    q, k, v = make_inputs(w, heads=[h], batches=[b])
+    with threadpool_limits(limits=1):
+        start = time.perf_counter()
+        out = oracle.piper_attention_reference(q, k, v, w.head_dim**-0.5, w.is_causal, granularity)
+        seconds = time.perf_counter() - start
+    return b, h, granularity, seconds, out[0, 0]
+
+
+def host_threads() -> int:
+    """Host threads the run may use: OMP_NUM_THREADS when set (16 on the GPU box), else the CPU
+    count; at most 16, the box's CPU share per GPU."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+    return max(1, min(16, threads))
+
+
+def _pause(seconds: float) -> int:
+    time.sleep(seconds)
+    return os.getpid()
+
+
+def start_cpu_pool(threads: int):
+    """Worker processes for the CPU baseline, started before this process touches the GPU (so
+    they inherit no GPU state), each with the oracle imported and one numpy thread."""
+    import multiprocessing
+    from concurrent.futures import ProcessPoolExecutor
+
+    pool = ProcessPoolExecutor(max_workers=threads, mp_context=multiprocessing.get_context("spawn"),
+                               initializer=_cpu_worker_ready)
+    pids = set(pool.map(_pause, [0.5] * threads))  # every worker started and initialised
+    log(f"[bench] cpu baseline: {len(pids)} worker processes ready")
+    return pool
+
+
+def cpu_baseline(pool, threads: int, workload, seconds: float) -> tuple[dict, dict]:
+    """Time the CPU oracle on whole (batch, head) slices of the workload, ``threads`` slices at a
+    time in the worker processes (one numpy thread each), until ~``seconds`` of wall time have
+    passed or every slice is done; then one round per block.  Returns the record and the
+    oracle's FP32 outputs by (batch, head)."""
+    import numpy as np
+
     from piper_kernels.measure import attention_operations
+
+    slices = [(b, h) for b in range(workload.batch) for h in range(workload.heads)]
+    outputs: dict[tuple[int, int], np.ndarray] = {}
+    per_thread_wall = 0.0
+    done = 0
+    while done < len(slices) and (done == 0 or per_thread_wall < seconds):
+        batch = slices[done : done + threads]
+        start = time.perf_counter()
+        for b, h, _, _, out in pool.map(_cpu_head, [(workload.name, b, h, "per_thread") for b, h in batch]):
+            outputs[(b, h)] = out
+        per_thread_wall += time.perf_counter() - start
+        done += len(batch)
+        log(f"[bench] cpu baseline: {done} slice(s) per_thread, {per_thread_wall:.1f} s")
+    batch = slices[: min(threads, len(slices))]
+    start = time.perf_counter()
+    list(pool.map(_cpu_head, [(workload.name, b, h, "per_warp") for b, h in batch]))
+    warp_wall = time.perf_counter() - start
+    log(f"[bench] cpu baseline: {len(batch)} slice(s) per_warp, {warp_wall:.1f} s")
+
+    def tops(count: int, wall: float) -> float:
+        ops = attention_operations(1, count, workload.query_length, workload.key_length, workload.head_dim,
+                                   workload.is_causal)
+        return ops / wall / 1e12
+
+    record = {
+        "value": tops(done, per_thread_wall),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "per_warp_value": tops(len(batch), warp_wall),
+        "sample": (
+            f"{workload.name}: {done} of {len(slices)} (batch, head) slices, each the full reference computation "
+            f"(K/V means, per_thread Q/K codes, V codes, 64-key streaming loop over all {workload.query_length} query "
+            f"rows), {threads} at a time in worker processes with one numpy thread each; {per_thread_wall:.1f} s wall; "
+            f"per_warp: {len(batch)} slices in {warp_wall:.1f} s; numpy {np.__version__}; "
+            f"host threads used {threads} of os.cpu_count={os.cpu_count()}"
+        ),
+    }
+    return record, outputs
+
+
+# ---------------------------------------------------------------------------------------
+# quality
+# ---------------------------------------------------------------------------------------
+def sdpa_rows_float64(q, k, v, rows: int, scale: float, is_causal: bool):
+    """FP64 softmax attention of the first ``rows`` query rows of each [B', H', S, D] slice."""
+    import numpy as np
+
+    q64 = q[:, :, :rows].double().cpu().numpy()
+    k64 = k.double().cpu().numpy()
+    v64 = v.double().cpu().numpy()
+    logits = np.matmul(q64, np.swapaxes(k64, -1, -2)) * scale
+    if is_causal:
+        logits = np.where(np.arange(k64.shape[2])[None, :] > np.arange(rows)[:, None], -np.inf, logits)
+    logits -= logits.max(axis=-1, keepdims=True)
+    weights = np.exp(logits)
+    weights /= weights.sum(axis=-1, keepdims=True)
+    return np.matmul(weights, v64)
+
+
+def quality_block(workload, output, reference_outputs: dict, rows: int) -> dict:
+    """The timed call's output against FP64 SDPA (first ``rows`` rows of up to two slices) and
+    against the quantised reference (every slice the CPU baseline computed)."""
+    import numpy as np
+    import torch
+
+    from piper_kernels.measure import measure_quality
     from piper_kernels.workloads import make_inputs
 
-    scale = workload.head_dim**-0.5
-    heads = 0
-    elapsed = 0.0
-    with threadpool_limits(limits=1):
-        while heads < workload.heads and (heads == 0 or elapsed < seconds):
-            q, k, v = make_inputs(workload, heads=[heads], batches=[0])
-            start = time.perf_counter()
-            oracle.piper_attention_reference(q, k, v, scale, workload.is_causal, "per_thread")
-            elapsed += time.perf_counter() - start
-            heads += 1
-            log(f"[bench] cpu baseline: {heads} head(s), {elapsed:.1f} s")
-    ops = attention_operations(1, heads, workload.query_length, workload.key_length, workload.head_dim,
-                               workload.is_causal)
+    def metrics(actual, expected) -> dict:
+        m = measure_quality(torch.as_tensor(actual), torch.as_tensor(expected))
+        return {"max_abs": m.max_absolute_error, "mean_abs": m.mean_absolute_error, "sqnr_db": round(m.sqnr_db, 2),
+                "cosine": m.cosine_similarity}
+
+    heads = list(range(min(2, workload.heads)))
+    rows = min(rows, workload.query_length)
+    q, k, v = make_inputs(workload, batches=[0], heads=heads)
+    sdpa = sdpa_rows_float64(q, k, v, rows, workload.head_dim**-0.5, workload.is_causal)
+    got = output[:1, heads, :rows].float().cpu().numpy()
+    result = {
+        "vs_fp64_sdpa": {
+            "sample": f"batch 0, heads {heads}, query rows 0..{rows - 1}",
+            "output_dtype": str(output.dtype).removeprefix("torch."),
+            **metrics(got, sdpa),
+        }
+    }
+    if all((0, h) in reference_outputs for h in heads):
+        ref = np.stack([reference_outputs[(0, h)][:rows] for h in heads])[None]
+        result["vs_fp64_sdpa"]["reference_fp32"] = metrics(ref, sdpa)
+        cast = torch.from_numpy(ref).to(output.dtype).float().numpy()
+        result["vs_fp64_sdpa"]["reference_cast_to_output_dtype"] = metrics(cast, sdpa)
+    if reference_outputs:
+        keys = sorted(reference_outputs)
+        actual = torch.stack([output[b, h].float().cpu() for b, h in keys])
+        ref32 = torch.stack([torch.from_numpy(reference_outputs[key]) for key in keys])
+        result["vs_quantized_reference"] = {
+            "sample": f"{len(keys)} whole (batch, head) slices (the CPU baseline's)",
+            "fp32_reference": metrics(actual, ref32),
+            "reference_cast_to_output_dtype": metrics(actual, ref32.to(output.dtype).float()),
+        }
+    return result
+
+
+# ---------------------------------------------------------------------------------------
+# environment
+# ---------------------------------------------------------------------------------------
+def environment(device) -> dict:
+    import numpy as np
+    import torch
+
+    props = torch.cuda.get_device_properties(device)
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), cpu)
+    except OSError:
+        pass
+    try:
+        revision = subprocess.run(["git", "-C", str(REPO), "rev-parse", "HEAD"], capture_output=True, text=True,
+                                  timeout=10).stdout.strip() or None
+    except (OSError, subprocess.SubprocessError):
+        revision = None
     return {
-        "value": ops / elapsed / 1e12,
-        "unit": "TOPS",
-        "cores": 1,
-        "kind": "port",
-        "sample": (
-            f"{workload.name}: {heads} of {workload.batch * workload.heads} (batch, head) slices, each the full "
-            f"reference computation (K/V means, per_thread Q/K codes, V codes, 64-key streaming loop over all "
-            f"{workload.query_length} query rows); {elapsed:.1f} s wall; numpy {np.__version__} on 1 thread; "
-            f"cpu={platform.processor() or platform.machine()} os.cpu_count={os.cpu_count()}"
-        ),
+        "gpu": props.name,
+        "arch": props.gcnArchName,
+        "compute_units": props.multi_processor_count,
+        "max_sclk_mhz": getattr(props, "clock_rate", 0) // 1000 or None,
+        "torch": torch.__version__,
+        "hip": torch.version.hip,
+        "numpy": np.__version__,
+        "python": platform.python_version(),
+        "host_cpu": cpu,
+        "host_cpu_count": os.cpu_count(),
+        "source_revision": revision,
     }
 
 
@@ -131,6 +311,11 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+
+    sage = args.operator == "sage_attention_2pp"
+    with_cpu_baseline = not args.no_cpu_baseline and not sage
+    threads = host_threads()
+    pool = start_cpu_pool(threads) if with_cpu_baseline else None  # before any GPU call
 
     import torch
 
@@ -146,7 +331,6 @@ def main() -> int:
     b, h, sq, sk, d = workload.shape
     ops = attention_operations(b, h, sq, sk, d, workload.is_causal)
 
-    sage = args.operator == "sage_attention_2pp"
     if sage:
         from piper_kernels.attention.sage_attention_2pp.hip import _launch_sage_attention_2pp as launch
         from piper_kernels.attention.sage_attention_2pp.hip import _prepare_sage_attention_2pp
@@ -174,16 +358,26 @@ def main() -> int:
         return out
 
     with torch.no_grad():
-        log(f"[bench] warmup {args.warmup}")
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
+        # warm-up: at least --warmup steps and at least --warmup-ms of GPU time (the clock ramps)
+        warm_steps = 0
+        warm_begin = torch.cuda.Event(enable_timing=True)
+        warm_begin.record()
+        while True:
+            for _ in range(max(1, args.warmup) if warm_steps == 0 else 5):
+                step()
+                warm_steps += 1
+            warm_end = torch.cuda.Event(enable_timing=True)
+            warm_end.record()
+            warm_end.synchronize()
+            if warm_steps >= args.warmup and warm_begin.elapsed_time(warm_end) >= args.warmup_ms:
+                break
+        log(f"[bench] warmup {warm_steps} steps, {warm_begin.elapsed_time(warm_end):.0f} ms")
         events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
         log(f"[bench] timing {args.steps} steps")
         torch.cuda.synchronize()
         start = time.perf_counter()
         for i in range(args.steps):
-            step(events[i])
+            out = step(events[i])
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
@@ -212,7 +406,7 @@ def main() -> int:
         "unit": "TOPS",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warm_steps,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -251,6 +445,7 @@ def main() -> int:
             "traffic": traffic_from_profile(workload.name),
         },
         "cpu_baseline": None,
+        "quality": None,
     }
     from piper_kernels.attention.piper_attention._plan import select_plan
 
@@ -263,25 +458,31 @@ def main() -> int:
     else:
         result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
         result["config"]["qk_granularity"] = args.qk_granularity
-    # the sustained dense MFMA rate of this GPU (library probe, after the timed region)
-    from piper_kernels._hip import library as native
-    from piper_kernels.measure import measure_mfma_peak
+    result["environment"] = environment(device)
+    if not args.no_probes:
+        # the sustained dense MFMA rate of this GPU and the issue probe (after the timed region)
+        from piper_kernels._hip import library as native
+        from piper_kernels.measure import measure_issue_sharing, measure_mfma_peak
 
-    log("[bench] MFMA probe")
-    measured = {
-        "int8": measure_mfma_peak(native.MFMA_PROBE_I8, device),
-        "fp8": measure_mfma_peak(native.MFMA_PROBE_F8, device),
-    }
-    result["mfma_peak_measured"] = measured
-    # how MFMA execution and VALU issue share a SIMD at the attention kernels' occupancy
-    from piper_kernels.measure import measure_mfma_valu_sharing
-
-    log("[bench] MFMA/VALU sharing probe")
-    result["mfma_valu_sharing"] = measure_mfma_valu_sharing(device)
-    result["attention_kernel"]["percent_of_measured_int8_peak"] = round(100 * attn_tops / measured["int8"]["tops"], 2)
-    if not args.no_cpu_baseline and not sage:
+        log("[bench] MFMA probe")
+        measured = {
+            "int8": measure_mfma_peak(native.MFMA_PROBE_I8, device),
+            "fp8": measure_mfma_peak(native.MFMA_PROBE_F8, device),
+        }
+        result["mfma_peak_measured"] = measured
+        result["attention_kernel"]["percent_of_measured_int8_peak"] = round(
+            100 * attn_tops / measured["int8"]["tops"], 2
+        )
+        log("[bench] issue probe")
+        result["issue_sharing"] = measure_issue_sharing(device)
+    reference_outputs: dict = {}
+    if pool is not None:
         log("[bench] cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(workload, args.cpu_seconds)
+        with pool:
+            result["cpu_baseline"], reference_outputs = cpu_baseline(pool, threads, workload, args.cpu_seconds)
+    if not sage:
+        log("[bench] quality")
+        result["quality"] = quality_block(workload, out, reference_outputs, args.quality_rows)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -318,44 +318,6 @@ int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layo
 int piper_sage_prepare(const piper_sage_prepare_args* args, void* stream);
 int piper_sage_attention_forward(const piper_sage_attention_args* args, void* stream);
 
-/* Roofline calibration; no counterpart in the reference (whose benchmarks price kernels
- * against published peaks only).  Runs `workgroups` x 512 threads of back-to-back dense MFMAs
- * of one kind on `stream`: each wave issues 4 * `iterations` MFMAs with all-ones operands
- * (INT8 1, FP8 E4M3 1.0), so that events around the launch give the sustained matrix-core rate
- * at the running clock.  Per wave: 4 * iterations * PIPER_MFMA_PROBE_OPS(kind) operations.
- * `sink` receives one 32-bit word per thread (workgroups * 512 words): the sum of the thread's
- * 64 accumulator registers, iterations * 2048 modulo 2^32 for PIPER_MFMA_PROBE_I8 and the FP32
- * bits of iterations * 4096 for PIPER_MFMA_PROBE_F8 (exact for iterations <= 4096). */
-#define PIPER_MFMA_PROBE_I8 0 /* v_mfma_i32_32x32x32_i8 */
-#define PIPER_MFMA_PROBE_F8 1 /* v_mfma_f32_32x32x64_f8f6f4 on FP8 E4M3 */
-/* How MFMA execution and VALU issue share a SIMD: kind VALU issues 64 FP32 FMAs per round
- * (16 chains f = f * 1 + 1) and no MFMA, storing the FP32 bits of 64 * iterations (exact for
- * iterations <= 2^18); kind I8_VALU issues the INT8 kind's 4 MFMAs per round with 16 of those
- * FMAs after each, storing iterations * 2112 modulo 2^32.  Launched with one workgroup per
- * compute unit (two waves per SIMD, like the attention kernels), t(I8_VALU) lies between
- * max(t(I8), t(VALU)) (full overlap) and t(I8) + t(VALU) (serialised). */
-#define PIPER_MFMA_PROBE_VALU 2
-#define PIPER_MFMA_PROBE_I8_VALU 3
-/* Issue rates of two more VALU classes, 64 per round on 16 chains and no MFMA: v_max3_f32
- * (f = max(f, 1, 0) from 1; stores the FP32 bits of 16.0) and v_exp_f32 (f = 2^-f from 0,
- * which converges to 0.641186; stores the FP32 bits of the 16-chain sum). */
-#define PIPER_MFMA_PROBE_MAX3 4
-#define PIPER_MFMA_PROBE_EXP 5
-/* Kind VALU with one wave-wide ds_read_b128 (of zeros) after every 8 FMAs: stores the same word
- * as kind VALU; t(VALU_LDS) - t(VALU) is the issue cost of 8 * iterations LDS reads. */
-#define PIPER_MFMA_PROBE_VALU_LDS 6
-/* Conversion checks of the attention kernels' probability codes (`iterations` is not used).  On
- * entry the 512 words of each workgroup's part of `sink` hold FP32 values; thread t packs values
- * 4 (t % 128) .. 4 (t % 128) + 3 with the kernel's own packer, the first value in byte 0, and
- * stores the word over word t.  P_CODES_U8: Piper Attention's UINT8 codes (round half to even,
- * saturated to [0, 255]; the replaced reference rule is reference.py:104-107), each byte holding
- * u - 128 as the PV MFMA's signed operand.  P_CODES_FP8: SageAttention2++'s FP8 E4M3 codes. */
-#define PIPER_MFMA_PROBE_P_CODES_U8 7
-#define PIPER_MFMA_PROBE_P_CODES_FP8 8
-#define PIPER_MFMA_PROBE_THREADS 512
-#define PIPER_MFMA_PROBE_OPS(kind) ((kind) == PIPER_MFMA_PROBE_F8 ? 131072 : 65536)
-int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream);
-
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* piper_last_error(void);
 

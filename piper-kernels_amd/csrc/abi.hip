@@ -20,7 +20,6 @@ static_assert(PIPER_KV_LOG2_OFFSET(64) == piper::kv_log_offset(64), "log2 offset
 static_assert(PIPER_SAGE_TILE_BYTES(64) == piper::sage_tile_bytes(64), "SageAttention2++ record size (D = 64)");
 static_assert(PIPER_SAGE_TILE_BYTES(128) == piper::sage_tile_bytes(128), "SageAttention2++ record size (D = 128)");
 static_assert(PIPER_SAGE_V_OFFSET(128) == piper::sage_v_offset(128), "SageAttention2++ V^T offset");
-static_assert(PIPER_MFMA_PROBE_THREADS == piper::kProbeThreads, "probe workgroup size");
 static_assert(PIPER_QUERY_SCALE_SLOTS == piper::kQueryScaleSlots && PIPER_KEY_SCALE_SLOTS == piper::kKeyScaleSlots,
               "scale slots per block");
 
@@ -437,21 +436,6 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   const hipError_t err = piper::launch_sage_attention(static_cast<int>(s.head_dim), a->is_causal != 0,
                                                       a->output_dtype, waves, sp, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "attention launch failed: %s", hipGetErrorString(err));
-  g_last_error[0] = '\0';
-  return PIPER_OK;
-}
-
-int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream) {
-  if (kind < PIPER_MFMA_PROBE_I8 || kind > PIPER_MFMA_PROBE_P_CODES_FP8)
-    return fail(PIPER_ERROR_UNSUPPORTED, "unknown MFMA probe kind %d", kind);
-  if (workgroups < 1 || workgroups > 65536 || iterations < 1 || iterations > (1 << 24))
-    return fail(PIPER_ERROR_INVALID_ARGUMENT, "probe needs 1..65536 workgroups and 1..2^24 iterations, got %d and %d",
-                workgroups, iterations);
-  if (sink == nullptr || (reinterpret_cast<uintptr_t>(sink) & 3u) != 0)
-    return fail(PIPER_ERROR_INVALID_ARGUMENT, "sink must be a non-NULL 4-byte aligned buffer of workgroups * %d words",
-                PIPER_MFMA_PROBE_THREADS);
-  const hipError_t err = piper::launch_mfma_probe(kind, workgroups, iterations, sink, static_cast<hipStream_t>(stream));
-  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "probe launch failed: %s", hipGetErrorString(err));
   g_last_error[0] = '\0';
   return PIPER_OK;
 }

@@ -180,13 +180,8 @@ hipError_t launch_sage_prep(bool bf16, int head_dim, const MeanParams& mp, const
 hipError_t launch_sage_attention(int head_dim, bool causal, int out_dtype, int waves, const SageParams& sp,
                                  hipStream_t stream);
 
-// out_dtype: 0 = fp16, 1 = bf16, 2 = fp32.  waves: 4 or 8 query waves per workgroup.
-// kind 0: v_mfma_i32_32x32x32_i8, 1: v_mfma_f32_32x32x64_f8f6f4 (FP8 E4M3), 2: FP32 FMAs only,
-// 3: kind 0 interleaved with kind 2's FMAs, 4: v_max3_f32 only, 5: v_exp_f32 only, 6: kind 2 with
-// a ds_read_b128 after every 8 FMAs, 7/8: the UINT8/FP8 probability-code packers on FP32 values
-// read from the sink; kProbeThreads per workgroup
-constexpr int kProbeThreads = 512;  // 8 waves: two per SIMD
-hipError_t launch_mfma_probe(int kind, int workgroups, int iterations, uint32_t* sink, hipStream_t stream);
+// out_dtype: 0 = fp16, 1 = bf16, 2 = fp32.  waves: 8 or 4 query waves per workgroup (two waves per
+// SIMD), or 3 for three 4-wave workgroups per CU.
 hipError_t launch_attention(int head_dim, bool causal, int out_dtype, int waves, const AttnParams& ap,
                             hipStream_t stream);
 

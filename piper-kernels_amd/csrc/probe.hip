@@ -1,53 +1,41 @@
-// Roofline calibration: dense MFMAs issued back to back on every SIMD, for measuring the
-// sustained matrix-core rate of this GPU at its running clock (the attention kernels are
-// priced against it next to the published peak).
+// libpiper_probe.so: measurement kernels beside the Piper Attention backend (C ABI in
+// include/piper_probe.h).  Nothing here is part of the operator.
 //
-// Each wave keeps four independent accumulator chains so the MFMA pipe never waits on a
-// result, and runs `iterations` rounds of four MFMAs on constant operands: every A and B
-// element is 1 (INT8 1, or FP8 E4M3 1.0 = 0x38), so after the loop every accumulator element
-// is exactly iterations * K (K = 32 for the INT8 instruction, 64 for the FP8 one).  Each lane
-// then stores the 32-bit sum of its 64 accumulator registers to sink[global thread index]:
-// iterations * 2048 (INT8, modulo 2^32) or iterations * 4096 (FP8, as FP32 bits), a value a
-// caller can check so that a fast time cannot come from work the compiler removed.
-//
-// Two more kinds measure how MFMA execution and VALU issue share a SIMD.  Kind 2 runs 64
-// FP32 FMAs per round (16 independent chains f = f * 1 + 1, every result an exact integer)
-// and no MFMA; kind 3 runs the INT8 kind's four MFMAs per round with 16 of those FMAs issued
-// after each one (scheduling barriers keep the interleave).  Launched like the attention
-// kernel (one 8-wave workgroup per compute unit, two waves per SIMD), the three times give
-// t(MFMA), t(VALU) and t(both): t(both) = max of the two if the units overlap, their sum if
-// they serialise.  Kind 2 stores the FP32 bits of 64 * iterations; kind 3 stores
-// iterations * 2048 + 64 * iterations modulo 2^32.  Kinds 4 and 5 time two other instruction
-// classes the same way (64 per round on 16 chains): v_max3_f32 (f = max(f, 1, 0), which stays 1;
-// stores the bits of 16.0) and v_exp_f32 (f = 2^-f from 0, which converges to the root of
-// x = 2^-x, 0.641186; stores the bits of the 16-chain sum).  Kind 6 is kind 2 with a wave-wide
-// ds_read_b128 of zeros after every 8 FMAs (the FMA result word, 64 * iterations, is unchanged):
-// t(6) - t(2) is what 8 * iterations LDS reads add to a VALU-bound wave.
-//
-// Kinds 7 and 8 check conversions rather than time them: on entry, the 512 words of each
-// workgroup's part of `sink` hold FP32 values; thread t packs values 4 (t % 128) .. + 3 with the
-// attention kernels' own probability-code packers (kind 7: Piper Attention's UINT8 codes,
-// stored as u - 128 per byte; kind 8: SageAttention2++'s FP8 E4M3 codes) and stores the word
-// over word t.  `iterations` is not used.
+// * piper_mfma_probe: dense MFMAs issued back to back on every SIMD (the sustained matrix-core
+//   rate of this GPU at its running clock), and two conversion checks that run the attention
+//   kernels' own probability-code packers (quant.h) on caller values.
+// * piper_issue_probe: per-wave roles on shared SIMDs, each a fixed inline-assembly loop timed by
+//   s_memtime, to measure how MFMA execution, VALU issue and LDS reads of different waves share
+//   a SIMD (the issue bound of the attention kernels).
+#include <cstdarg>
+#include <cstdio>
+
 #include "common.h"
-#include "kernels.h"
+#include "piper_probe.h"
 #include "quant.h"
 
 namespace piper {
+namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
+constexpr int kProbeThreads = PIPER_MFMA_PROBE_THREADS;  // 8 waves: two per SIMD
+
+// Kinds I8 and F8: four accumulator chains per wave, `iterations` rounds of four MFMAs on
+// all-ones operands; each lane stores the 32-bit sum of its 64 accumulator registers.
+// Kinds P_CODES_U8 / P_CODES_FP8: thread t packs four of its workgroup's values with the
+// kernels' packer and stores the word over word t.
 template <int kKind>
 __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* sink, int iterations) {
   uint32_t total = 0;
-  if constexpr (kKind == 7 || kKind == 8) {
+  if constexpr (kKind == PIPER_MFMA_PROBE_P_CODES_U8 || kKind == PIPER_MFMA_PROBE_P_CODES_FP8) {
     const float* values = reinterpret_cast<const float*>(sink) + static_cast<long>(blockIdx.x) * kProbeThreads;
     const int i = 4 * (threadIdx.x % (kProbeThreads / 4));
     const float a = values[i], b = values[i + 1], c = values[i + 2], d = values[i + 3];
     __syncthreads();  // every read of this workgroup's words precedes every store over them
-    total = kKind == 7 ? pack_codes(a, b, c, d) : pack_fp8(a, b, c, d);
-  } else if constexpr (kKind == 0) {
+    total = kKind == PIPER_MFMA_PROBE_P_CODES_U8 ? pack_codes(a, b, c, d) : pack_fp8(a, b, c, d);
+  } else if constexpr (kKind == PIPER_MFMA_PROBE_I8) {
     v4i a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     asm volatile("" : "+v"(a));  // opaque: the products cannot be folded
     v16i acc[4];
@@ -61,92 +49,6 @@ __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* 
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) total += static_cast<uint32_t>(acc[c][r]);
-  } else if constexpr (kKind == 4 || kKind == 5) {
-    // instruction-class issue rates: 64 v_max3_f32 (kind 4) or v_exp_f32 (kind 5) per round
-    float one = 1.0f, zero = 0.0f;
-    asm volatile("" : "+v"(one), "+v"(zero));
-    float f[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) f[i] = kKind == 4 ? 1.0f : 0.0f;
-    for (int it = 0; it < iterations; ++it) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if constexpr (kKind == 4) f[i] = fmaxf(fmaxf(f[i], one), zero);  // stays 1
-          else f[i] = __builtin_amdgcn_exp2f(-f[i]);  // converges to the root of x = 2^-x
-        }
-      }
-    }
-    float fsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) fsum += f[i];
-    total = __builtin_bit_cast(uint32_t, fsum);
-  } else if constexpr (kKind == 6) {
-    // kind 2's FMAs with one wave-wide ds_read_b128 after every 8 of them (8 per round, the
-    // attention kernel's ratio of LDS reads to VALU work); the LDS words are zero
-    __shared__ __attribute__((aligned(16))) float lds[4 * kProbeThreads];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lds[4 * threadIdx.x + i] = 0.0f;
-    __syncthreads();
-    const uint32_t address = static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) float*)(lds + 4 * (threadIdx.x & 63))));
-    float one = 1.0f, addend = 1.0f;
-    asm volatile("" : "+v"(one), "+v"(addend));
-    float f[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) f[i] = 0.0f;
-    v4i word = {0, 0, 0, 0};
-    for (int it = 0; it < iterations; ++it) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        // explicit reads (the compiler would hoist or merge loop-invariant loads); their words
-        // are waited for once after the loop
-        asm volatile("ds_read_b128 %0, %1" : "=v"(word) : "v"(address) : "memory");
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) f[(8 * c + i) & 15] = fmaf(f[(8 * c + i) & 15], one, addend);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(word) : : "memory");
-    float fsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) fsum += f[i];
-    total = __builtin_bit_cast(uint32_t, fsum) + static_cast<uint32_t>(word[0] | word[1] | word[2] | word[3]);
-  } else if constexpr (kKind == 2 || kKind == 3) {
-    v4i a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-    asm volatile("" : "+v"(a));
-    float one = 1.0f, addend = 1.0f;  // two registers: an FMA reading one VGPR twice issues slower
-    asm volatile("" : "+v"(one), "+v"(addend));  // opaque: the FMAs cannot be folded
-    float f[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) f[i] = 0.0f;
-    v16i acc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = v16i{};
-    for (int it = 0; it < iterations; ++it) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if constexpr (kKind == 3) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, acc[c], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) f[i] = fmaf(f[i], one, addend);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    float fsum = 0.0f;  // 16 chains of 4 * iterations: exact while 64 * iterations < 2^24
-#pragma unroll
-    for (int i = 0; i < 16; ++i) fsum += f[i];
-    if constexpr (kKind == 2) {
-      total = __builtin_bit_cast(uint32_t, fsum);
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) total += static_cast<uint32_t>(acc[c][r]);
-      total += static_cast<uint32_t>(fsum);
-    }
   } else {
     v8i a = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
     asm volatile("" : "+v"(a));
@@ -168,21 +70,311 @@ __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* 
   sink[static_cast<long>(blockIdx.x) * kProbeThreads + threadIdx.x] = total;
 }
 
-hipError_t launch_mfma_probe(int kind, int workgroups, int iterations, uint32_t* sink, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(workgroups));
-  const dim3 block(kProbeThreads);
-  switch (kind) {
-    case 0: hipLaunchKernelGGL(mfma_probe_kernel<0>, grid, block, 0, stream, sink, iterations); break;
-    case 1: hipLaunchKernelGGL(mfma_probe_kernel<1>, grid, block, 0, stream, sink, iterations); break;
-    case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, grid, block, 0, stream, sink, iterations); break;
-    case 3: hipLaunchKernelGGL(mfma_probe_kernel<3>, grid, block, 0, stream, sink, iterations); break;
-    case 4: hipLaunchKernelGGL(mfma_probe_kernel<4>, grid, block, 0, stream, sink, iterations); break;
-    case 5: hipLaunchKernelGGL(mfma_probe_kernel<5>, grid, block, 0, stream, sink, iterations); break;
-    case 6: hipLaunchKernelGGL(mfma_probe_kernel<6>, grid, block, 0, stream, sink, iterations); break;
-    case 7: hipLaunchKernelGGL(mfma_probe_kernel<7>, grid, block, 0, stream, sink, iterations); break;
-    default: hipLaunchKernelGGL(mfma_probe_kernel<8>, grid, block, 0, stream, sink, iterations); break;
-  }
-  return hipGetLastError();
+// ---------------------------------------------------------------------------------------
+// Issue probe.  Loop bodies are inline assembly on independent chains, so the instruction
+// stream is fixed: FMA chains f = f * 1 + 1, exp chains x = 2^-x, conversion chains that keep
+// writing byte lanes of a word, MFMA chains on AGPR accumulators.
+// ---------------------------------------------------------------------------------------
+constexpr int kIssueLdsBytes = 100 * 1024;  // more than half of a CU's 160 KiB: one workgroup per CU
+constexpr int kInner = 8;                    // rounds between clock reads
+
+__device__ __forceinline__ void fma16(float (&f)[16], float one, float add) {
+  asm volatile(
+      "v_fma_f32 %0, %0, %16, %17\n\t"
+      "v_fma_f32 %1, %1, %16, %17\n\t"
+      "v_fma_f32 %2, %2, %16, %17\n\t"
+      "v_fma_f32 %3, %3, %16, %17\n\t"
+      "v_fma_f32 %4, %4, %16, %17\n\t"
+      "v_fma_f32 %5, %5, %16, %17\n\t"
+      "v_fma_f32 %6, %6, %16, %17\n\t"
+      "v_fma_f32 %7, %7, %16, %17\n\t"
+      "v_fma_f32 %8, %8, %16, %17\n\t"
+      "v_fma_f32 %9, %9, %16, %17\n\t"
+      "v_fma_f32 %10, %10, %16, %17\n\t"
+      "v_fma_f32 %11, %11, %16, %17\n\t"
+      "v_fma_f32 %12, %12, %16, %17\n\t"
+      "v_fma_f32 %13, %13, %16, %17\n\t"
+      "v_fma_f32 %14, %14, %16, %17\n\t"
+      "v_fma_f32 %15, %15, %16, %17\n\t"
+      : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]), "+v"(f[15])
+      : "v"(one), "v"(add));
 }
 
+__device__ __forceinline__ void exp16(float (&f)[16]) {
+  asm volatile(
+      "v_exp_f32 %0, -%0\n\t"
+      "v_exp_f32 %1, -%1\n\t"
+      "v_exp_f32 %2, -%2\n\t"
+      "v_exp_f32 %3, -%3\n\t"
+      "v_exp_f32 %4, -%4\n\t"
+      "v_exp_f32 %5, -%5\n\t"
+      "v_exp_f32 %6, -%6\n\t"
+      "v_exp_f32 %7, -%7\n\t"
+      "v_exp_f32 %8, -%8\n\t"
+      "v_exp_f32 %9, -%9\n\t"
+      "v_exp_f32 %10, -%10\n\t"
+      "v_exp_f32 %11, -%11\n\t"
+      "v_exp_f32 %12, -%12\n\t"
+      "v_exp_f32 %13, -%13\n\t"
+      "v_exp_f32 %14, -%14\n\t"
+      "v_exp_f32 %15, -%15\n\t"
+      : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]), "+v"(f[15]));
+}
+
+__device__ __forceinline__ void cvt16(uint32_t (&w)[16], float one) {
+  asm volatile(
+      "v_cvt_pk_u8_f32 %0, %16, 0, %0\n\t"
+      "v_cvt_pk_u8_f32 %1, %16, 1, %1\n\t"
+      "v_cvt_pk_u8_f32 %2, %16, 2, %2\n\t"
+      "v_cvt_pk_u8_f32 %3, %16, 3, %3\n\t"
+      "v_cvt_pk_u8_f32 %4, %16, 0, %4\n\t"
+      "v_cvt_pk_u8_f32 %5, %16, 1, %5\n\t"
+      "v_cvt_pk_u8_f32 %6, %16, 2, %6\n\t"
+      "v_cvt_pk_u8_f32 %7, %16, 3, %7\n\t"
+      "v_cvt_pk_u8_f32 %8, %16, 0, %8\n\t"
+      "v_cvt_pk_u8_f32 %9, %16, 1, %9\n\t"
+      "v_cvt_pk_u8_f32 %10, %16, 2, %10\n\t"
+      "v_cvt_pk_u8_f32 %11, %16, 3, %11\n\t"
+      "v_cvt_pk_u8_f32 %12, %16, 0, %12\n\t"
+      "v_cvt_pk_u8_f32 %13, %16, 1, %13\n\t"
+      "v_cvt_pk_u8_f32 %14, %16, 2, %14\n\t"
+      "v_cvt_pk_u8_f32 %15, %16, 3, %15\n\t"
+      : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7]), "+v"(w[8]), "+v"(w[9]), "+v"(w[10]), "+v"(w[11]), "+v"(w[12]), "+v"(w[13]), "+v"(w[14]), "+v"(w[15])
+      : "v"(one));
+}
+
+// 16 v_fma_f32, 4 v_cvt_pk_u8_f32 and 2 v_exp_f32, interleaved (the attention loop's proportions)
+__device__ __forceinline__ void mix22(float (&f)[16], uint32_t (&w)[16], float (&e)[2], float one, float add) {
+  asm volatile(
+      "v_fma_f32 %0, %0, %22, %23\n\t"
+      "v_fma_f32 %1, %1, %22, %23\n\t"
+      "v_fma_f32 %2, %2, %22, %23\n\t"
+      "v_cvt_pk_u8_f32 %16, %22, 0, %16\n\t"
+      "v_fma_f32 %3, %3, %22, %23\n\t"
+      "v_fma_f32 %4, %4, %22, %23\n\t"
+      "v_fma_f32 %5, %5, %22, %23\n\t"
+      "v_exp_f32 %20, -%20\n\t"
+      "v_fma_f32 %6, %6, %22, %23\n\t"
+      "v_fma_f32 %7, %7, %22, %23\n\t"
+      "v_cvt_pk_u8_f32 %17, %22, 1, %17\n\t"
+      "v_fma_f32 %8, %8, %22, %23\n\t"
+      "v_fma_f32 %9, %9, %22, %23\n\t"
+      "v_fma_f32 %10, %10, %22, %23\n\t"
+      "v_cvt_pk_u8_f32 %18, %22, 2, %18\n\t"
+      "v_fma_f32 %11, %11, %22, %23\n\t"
+      "v_fma_f32 %12, %12, %22, %23\n\t"
+      "v_exp_f32 %21, -%21\n\t"
+      "v_fma_f32 %13, %13, %22, %23\n\t"
+      "v_fma_f32 %14, %14, %22, %23\n\t"
+      "v_cvt_pk_u8_f32 %19, %22, 3, %19\n\t"
+      "v_fma_f32 %15, %15, %22, %23\n\t"
+      : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]), "+v"(f[15]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(e[0]), "+v"(e[1])
+      : "v"(one), "v"(add));
+}
+
+__device__ __forceinline__ void mfma_agpr(v16i& acc, v4i a) {
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %1, %0" : "+a"(acc) : "v"(a));
+}
+
+template <int R>
+__device__ __forceinline__ uint32_t issue_loop(uint64_t t0, uint64_t budget, const char* lds, uint32_t& rounds,
+                                               uint64_t& t1) {
+  constexpr bool kMfma = R == PIPER_ISSUE_MFMA || R == PIPER_ISSUE_MIX || R == PIPER_ISSUE_MFMA_FMA;
+  v4i a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  asm volatile("" : "+v"(a));
+  float one = 1.0f, add = 1.0f;
+  asm volatile("" : "+v"(one), "+v"(add));
+  float f[16];
+  uint32_t w[16];
+  float e[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    f[i] = 0.0f;
+    w[i] = 0u;
+  }
+  v16i acc0 = {}, acc1 = {};
+  if constexpr (kMfma) asm volatile("" : "+a"(acc0), "+a"(acc1));
+  // LDS reads: lane l reads the 16 bytes at 16 l + 1024 (i % 8), inside the first 8 KiB
+  const uint32_t lds_base = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)lds)) + 16u * (threadIdx.x & 63);
+  v4i words[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) words[i] = v4i{0, 0, 0, 0};
+  do {
+    for (int r = 0; r < kInner; ++r) {
+      if constexpr (R == PIPER_ISSUE_MFMA) {
+        mfma_agpr(acc0, a);
+        mfma_agpr(acc1, a);
+      } else if constexpr (R == PIPER_ISSUE_FMA) {
+        fma16(f, one, add);
+        fma16(f, one, add);
+      } else if constexpr (R == PIPER_ISSUE_EXP) {
+        exp16(f);
+        exp16(f);
+      } else if constexpr (R == PIPER_ISSUE_CVT) {
+        cvt16(w, one);
+        cvt16(w, one);
+      } else if constexpr (R == PIPER_ISSUE_MIX) {
+        mfma_agpr(acc0, a);
+        mix22(f, w, e, one, add);
+        mfma_agpr(acc1, a);
+        mix22(f, w, e, one, add);
+      } else if constexpr (R == PIPER_ISSUE_VALU_MIX) {
+        mix22(f, w, e, one, add);
+        mix22(f, w, e, one, add);
+      } else if constexpr (R == PIPER_ISSUE_LDS) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(words[i]) : "v"(lds_base), "i"(1024 * i) : "memory");
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+      } else if constexpr (R == PIPER_ISSUE_MFMA_FMA) {
+        mfma_agpr(acc0, a);
+        fma16(f, one, add);
+        mfma_agpr(acc1, a);
+        fma16(f, one, add);
+      }
+    }
+    rounds += kInner;
+    t1 = __builtin_amdgcn_s_memtime();
+  } while (t1 - t0 < budget);
+  uint32_t check = 0;
+  if constexpr (kMfma) {
+    v16i r0, r1;
+    asm volatile("" : "=v"(r0) : "0"(acc0));
+    asm volatile("" : "=v"(r1) : "0"(acc1));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) check += static_cast<uint32_t>(r0[i] + r1[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) check += __float_as_uint(f[i]) + w[i];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) check += static_cast<uint32_t>(words[i].x ^ words[i].w);
+  return check + __float_as_uint(e[0]) + __float_as_uint(e[1]);
+}
+
+struct IssueParams {
+  piper_issue_record* records;
+  uint64_t budget;
+  int roles[PIPER_ISSUE_MAX_WAVES_PER_SIMD];
+};
+
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 1024))) issue_probe_kernel(const IssueParams p) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ uint32_t slots[4];  // waves of this workgroup that reached each SIMD's counter
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (threadIdx.x < 4) slots[threadIdx.x] = 0;
+  __syncthreads();
+  const uint32_t hw_id = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_REG_HW_ID, 32 bits
+  const uint32_t xcc_id = __builtin_amdgcn_s_getreg((15 << 11) | 20);  // HW_REG_XCC_ID, 16 bits
+  uint32_t slot = 0;
+  if ((threadIdx.x & 63) == 0) slot = atomicAdd(&slots[(hw_id >> 4) & 3], 1u);
+  slot = __builtin_amdgcn_readfirstlane(slot);
+  const int role = slot < PIPER_ISSUE_MAX_WAVES_PER_SIMD ? p.roles[slot] : PIPER_ISSUE_IDLE;
+  __syncthreads();
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  uint64_t t1 = t0;
+  uint32_t rounds = 0, check = 0;
+  switch (role) {
+    case PIPER_ISSUE_MFMA: check = issue_loop<PIPER_ISSUE_MFMA>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_FMA: check = issue_loop<PIPER_ISSUE_FMA>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_EXP: check = issue_loop<PIPER_ISSUE_EXP>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_CVT: check = issue_loop<PIPER_ISSUE_CVT>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_MIX: check = issue_loop<PIPER_ISSUE_MIX>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_VALU_MIX: check = issue_loop<PIPER_ISSUE_VALU_MIX>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_LDS: check = issue_loop<PIPER_ISSUE_LDS>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_MFMA_FMA: check = issue_loop<PIPER_ISSUE_MFMA_FMA>(t0, p.budget, lds, rounds, t1); break;
+    default: break;
+  }
+  if ((threadIdx.x & 63) == 0) {
+    piper_issue_record rec;
+    rec.hw_id = hw_id;
+    rec.xcc_id = xcc_id;
+    rec.role = static_cast<uint32_t>(role);
+    rec.slot = slot;
+    rec.cycles = t1 - t0;
+    rec.rounds = rounds;
+    rec.check = check;
+    p.records[static_cast<long>(blockIdx.x) * PIPER_ISSUE_RECORDS_PER_WORKGROUP + wave] = rec;
+  }
+}
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, args);
+  va_end(args);
+  return status;
+}
+
+}  // namespace
 }  // namespace piper
+
+extern "C" {
+
+int piper_probe_abi_version(void) { return PIPER_PROBE_ABI_VERSION; }
+
+const char* piper_probe_last_error(void) { return piper::g_last_error; }
+
+int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream) {
+  using namespace piper;
+  if (kind < PIPER_MFMA_PROBE_I8 || kind > PIPER_MFMA_PROBE_P_CODES_FP8)
+    return fail(2, "unknown MFMA probe kind %d", kind);
+  if (workgroups < 1 || workgroups > 65536 || iterations < 1 || iterations > (1 << 24))
+    return fail(1, "probe needs 1..65536 workgroups and 1..2^24 iterations, got %d and %d", workgroups, iterations);
+  if (sink == nullptr || (reinterpret_cast<uintptr_t>(sink) & 3u) != 0)
+    return fail(1, "sink must be a non-NULL 4-byte aligned buffer of workgroups * %d words", PIPER_MFMA_PROBE_THREADS);
+  const dim3 grid(static_cast<unsigned>(workgroups));
+  const dim3 block(kProbeThreads);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (kind) {
+    case PIPER_MFMA_PROBE_I8: hipLaunchKernelGGL(mfma_probe_kernel<PIPER_MFMA_PROBE_I8>, grid, block, 0, s, sink, iterations); break;
+    case PIPER_MFMA_PROBE_F8: hipLaunchKernelGGL(mfma_probe_kernel<PIPER_MFMA_PROBE_F8>, grid, block, 0, s, sink, iterations); break;
+    case PIPER_MFMA_PROBE_P_CODES_U8:
+      hipLaunchKernelGGL(mfma_probe_kernel<PIPER_MFMA_PROBE_P_CODES_U8>, grid, block, 0, s, sink, iterations);
+      break;
+    default:
+      hipLaunchKernelGGL(mfma_probe_kernel<PIPER_MFMA_PROBE_P_CODES_FP8>, grid, block, 0, s, sink, iterations);
+      break;
+  }
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(3, "probe launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return 0;
+}
+
+int piper_issue_probe(const piper_issue_probe_args* a, void* stream) {
+  using namespace piper;
+  if (a == nullptr) return fail(1, "args is NULL");
+  if (a->waves_per_simd < 1 || a->waves_per_simd > PIPER_ISSUE_MAX_WAVES_PER_SIMD)
+    return fail(1, "waves_per_simd must be 1..%d, got %d", PIPER_ISSUE_MAX_WAVES_PER_SIMD, a->waves_per_simd);
+  if (a->workgroups < 1 || a->workgroups > 65536) return fail(1, "workgroups must be 1..65536, got %d", a->workgroups);
+  if (a->cycle_budget < 1000 || a->cycle_budget > 100000000)
+    return fail(1, "cycle_budget must be 1000..10^8, got %lld", (long long)a->cycle_budget);
+  if (a->records == nullptr || (reinterpret_cast<uintptr_t>(a->records) & 7u) != 0)
+    return fail(1, "records must be a non-NULL 8-byte aligned buffer of workgroups * %d records",
+                PIPER_ISSUE_RECORDS_PER_WORKGROUP);
+  IssueParams p{};
+  p.records = a->records;
+  p.budget = static_cast<uint64_t>(a->cycle_budget);
+  for (int s = 0; s < PIPER_ISSUE_MAX_WAVES_PER_SIMD; ++s) {
+    const int role = s < a->waves_per_simd ? a->roles[s] : PIPER_ISSUE_IDLE;
+    if (role < 0 || role >= PIPER_ISSUE_ROLES) return fail(2, "unknown role %d in slot %d", role, s);
+    p.roles[s] = role;
+  }
+  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(issue_probe_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kIssueLdsBytes);
+  if (err != hipSuccess) return fail(3, "hipFuncSetAttribute failed: %s", hipGetErrorString(err));
+  hipLaunchKernelGGL(issue_probe_kernel, dim3(static_cast<unsigned>(a->workgroups)), dim3(256 * a->waves_per_simd),
+                     kIssueLdsBytes, static_cast<hipStream_t>(stream), p);
+  err = hipGetLastError();
+  if (err != hipSuccess) return fail(3, "issue probe launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return 0;
+}
+
+}  // extern "C"

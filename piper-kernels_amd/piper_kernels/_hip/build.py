@@ -1,8 +1,9 @@
-"""Compile ``libpiper_mi355x.so`` (gfx950) from ``piper-kernels_amd/csrc`` with hipcc.
+"""Compile the gfx950 libraries from ``piper-kernels_amd/csrc`` with hipcc.
 
-The library is a plain C-ABI shared object (no torch headers); it is built in-tree next
-to this file so it travels with the repository.  ``python -m piper_kernels._hip.build``
-rebuilds it.
+``libpiper_mi355x.so`` is the operator's C ABI (``include/piper_mi355x.h``); ``libpiper_probe.so``
+holds the measurement probes (``include/piper_probe.h``), which only bench.py and the tests load.
+Both are plain C-ABI shared objects (no torch headers), built in-tree next to this file so they
+travel with the repository.  ``python -m piper_kernels._hip.build`` rebuilds them.
 """
 
 from __future__ import annotations
@@ -19,7 +20,9 @@ CSRC = PACKAGE_ROOT / "csrc"
 INCLUDE = PACKAGE_ROOT.parent / "include"
 BUILD_DIR = PACKAGE_ROOT / "_build"
 LIBRARY_PATH = Path(__file__).resolve().parent / "libpiper_mi355x.so"
-SOURCES = ("abi.hip", "prep.hip", "attention.hip", "sage2pp.hip", "probe.hip")
+PROBE_LIBRARY_PATH = Path(__file__).resolve().parent / "libpiper_probe.so"
+SOURCES = ("abi.hip", "prep.hip", "attention.hip", "sage2pp.hip")
+PROBE_SOURCES = ("probe.hip",)
 OFFLOAD_ARCH = "gfx950"
 
 COMPILE_FLAGS = (
@@ -56,22 +59,28 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(messages, file=sys.stderr)
 
 
+def _link(compiler: str, objects: list[Path], target: Path, verbose: bool) -> None:
+    tmp = target.with_suffix(f".so.tmp{os.getpid()}")
+    _run([compiler, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)], verbose)
+    os.replace(tmp, target)
+
+
 def build_library(verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 and link the shared library; returns its path."""
+    """Compile every HIP source for gfx950 and link both libraries; returns the operator
+    library's path (the probe library is ``PROBE_LIBRARY_PATH``)."""
     compiler = hipcc()
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     includes = [f"-I{INCLUDE}", f"-I{CSRC}"]
-    objects = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
+    sources = SOURCES + PROBE_SOURCES
+    objects = {s: BUILD_DIR / (Path(s).stem + ".o") for s in sources}
 
-    def compile_one(pair: tuple[str, Path]) -> None:
-        source, obj = pair
-        _run([compiler, *COMPILE_FLAGS, *includes, "-c", str(CSRC / source), "-o", str(obj)], verbose)
+    def compile_one(source: str) -> None:
+        _run([compiler, *COMPILE_FLAGS, *includes, "-c", str(CSRC / source), "-o", str(objects[source])], verbose)
 
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        list(pool.map(compile_one, zip(SOURCES, objects)))
-    tmp = LIBRARY_PATH.with_suffix(f".so.tmp{os.getpid()}")
-    _run([compiler, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)], verbose)
-    os.replace(tmp, LIBRARY_PATH)
+    with ThreadPoolExecutor(max_workers=len(sources)) as pool:
+        list(pool.map(compile_one, sources))
+    _link(compiler, [objects[s] for s in SOURCES], LIBRARY_PATH, verbose)
+    _link(compiler, [objects[s] for s in PROBE_SOURCES], PROBE_LIBRARY_PATH, verbose)
     return LIBRARY_PATH
 
 

@@ -1,4 +1,6 @@
-"""ctypes binding of ``libpiper_mi355x.so`` (C ABI in ``include/piper_mi355x.h``).
+"""ctypes bindings of ``libpiper_mi355x.so`` (the operator's C ABI, ``include/piper_mi355x.h``)
+and of ``libpiper_probe.so`` (measurement probes, ``include/piper_probe.h``; loaded only by
+bench.py and the tests).
 
 The structures below mirror the header field for field.  torch is imported before the
 library is opened: torch ships its own HIP runtime with the same SONAME
@@ -14,7 +16,7 @@ from pathlib import Path
 
 import torch  # noqa: F401  (load torch's HIP runtime first; see module docstring)
 
-from .build import LIBRARY_PATH
+from .build import LIBRARY_PATH, PROBE_LIBRARY_PATH
 
 ABI_VERSION = 2
 QUERY_BLOCK = 32
@@ -36,7 +38,6 @@ EXPORTED_SYMBOLS = (
     "piper_sage_prepared_layout",
     "piper_sage_prepare",
     "piper_sage_attention_forward",
-    "piper_mfma_probe",
     "piper_last_error",
 )
 
@@ -44,19 +45,6 @@ STATIC_SCRATCH_BYTES = 16 << 20  # PIPER_STATIC_SCRATCH_BYTES: piper_prepare_sta
 PREPARE_SKIP_QUERY = 1  # piper_prepare_args.flags
 PREPARE_QK_PER_THREAD = 2
 ATTENTION_QK_PER_THREAD = 1  # piper_attention_args.flags / piper_attention_fused_args.flags
-
-# piper_mfma_probe kinds, workgroup size and operations per MFMA (PIPER_MFMA_PROBE_* in the header)
-MFMA_PROBE_I8 = 0
-MFMA_PROBE_F8 = 1
-MFMA_PROBE_VALU = 2  # FP32 FMAs only
-MFMA_PROBE_I8_VALU = 3  # the INT8 MFMAs interleaved with the FP32 FMAs
-MFMA_PROBE_MAX3 = 4  # v_max3_f32 only
-MFMA_PROBE_EXP = 5  # v_exp_f32 only
-MFMA_PROBE_VALU_LDS = 6  # the FP32 FMAs with a ds_read_b128 after every 8
-MFMA_PROBE_P_CODES_U8 = 7  # Piper Attention's UINT8 probability-code packer on FP32 values from the sink
-MFMA_PROBE_P_CODES_FP8 = 8  # SageAttention2++'s FP8 E4M3 probability-code packer, the same way
-MFMA_PROBE_THREADS = 512
-MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -251,8 +239,6 @@ class NativeLibrary:
         lib.piper_sage_prepare.restype = ctypes.c_int
         lib.piper_sage_attention_forward.argtypes = [ctypes.POINTER(PiperSageAttentionArgs), _ptr]
         lib.piper_sage_attention_forward.restype = ctypes.c_int
-        lib.piper_mfma_probe.argtypes = [_i32, _i32, _i32, _ptr, _ptr]
-        lib.piper_mfma_probe.restype = ctypes.c_int
         version = lib.piper_abi_version()
         if version != ABI_VERSION:
             raise LibraryUnavailableError(
@@ -307,8 +293,6 @@ class NativeLibrary:
             self._lib.piper_sage_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_sage_attention_forward"
         )
 
-    def mfma_probe(self, kind: int, workgroups: int, iterations: int, sink: int, stream: int) -> None:
-        self._check(self._lib.piper_mfma_probe(kind, workgroups, iterations, _ptr(sink), _ptr(stream)), "piper_mfma_probe")
 
 
 _lock = threading.Lock()
@@ -341,3 +325,103 @@ def library_available() -> bool:
     except LibraryUnavailableError:
         return False
     return True
+
+
+# ---------------------------------------------------------------------------------------
+# libpiper_probe.so (include/piper_probe.h)
+# ---------------------------------------------------------------------------------------
+PROBE_ABI_VERSION = 1
+PROBE_EXPORTED_SYMBOLS = ("piper_probe_abi_version", "piper_probe_last_error", "piper_mfma_probe", "piper_issue_probe")
+
+# piper_mfma_probe kinds, workgroup size and operations per MFMA (PIPER_MFMA_PROBE_*)
+MFMA_PROBE_I8 = 0
+MFMA_PROBE_F8 = 1
+MFMA_PROBE_P_CODES_U8 = 2  # Piper Attention's UINT8 probability-code packer on FP32 values from the sink
+MFMA_PROBE_P_CODES_FP8 = 3  # SageAttention2++'s FP8 E4M3 probability-code packer, the same way
+MFMA_PROBE_THREADS = 512
+MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
+
+# piper_issue_probe roles (PIPER_ISSUE_*)
+ISSUE_ROLES = ("idle", "mfma", "fma", "exp", "cvt", "mix", "valu_mix", "lds", "mfma_fma")
+ISSUE_MAX_WAVES_PER_SIMD = 4
+ISSUE_RECORDS_PER_WORKGROUP = 16
+
+
+class PiperIssueRecord(ctypes.Structure):
+    _fields_ = [
+        ("hw_id", ctypes.c_uint32),
+        ("xcc_id", ctypes.c_uint32),
+        ("role", ctypes.c_uint32),
+        ("slot", ctypes.c_uint32),
+        ("cycles", ctypes.c_uint64),
+        ("rounds", ctypes.c_uint32),
+        ("check", ctypes.c_uint32),
+    ]
+
+
+class PiperIssueProbeArgs(ctypes.Structure):
+    _fields_ = [
+        ("waves_per_simd", _i32),
+        ("workgroups", _i32),
+        ("roles", _i32 * ISSUE_MAX_WAVES_PER_SIMD),
+        ("cycle_budget", _i64),
+        ("records", _ptr),
+    ]
+
+
+class ProbeLibrary:
+    """Typed wrapper over libpiper_probe.so; non-zero status raises RuntimeError."""
+
+    def __init__(self, path: Path) -> None:
+        self.path = Path(path)
+        self._lib = ctypes.CDLL(str(self.path))
+        lib = self._lib
+        lib.piper_probe_abi_version.argtypes = []
+        lib.piper_probe_abi_version.restype = ctypes.c_int
+        lib.piper_probe_last_error.argtypes = []
+        lib.piper_probe_last_error.restype = ctypes.c_char_p
+        lib.piper_mfma_probe.argtypes = [_i32, _i32, _i32, _ptr, _ptr]
+        lib.piper_mfma_probe.restype = ctypes.c_int
+        lib.piper_issue_probe.argtypes = [ctypes.POINTER(PiperIssueProbeArgs), _ptr]
+        lib.piper_issue_probe.restype = ctypes.c_int
+        version = lib.piper_probe_abi_version()
+        if version != PROBE_ABI_VERSION:
+            raise LibraryUnavailableError(f"{self.path} has ABI version {version}, this package expects {PROBE_ABI_VERSION}")
+
+    def has_symbol(self, name: str) -> bool:
+        return hasattr(self._lib, name)
+
+    def last_error(self) -> str:
+        return (self._lib.piper_probe_last_error() or b"").decode("utf-8", "replace")
+
+    def _check(self, status: int, what: str) -> None:
+        if status != 0:
+            raise RuntimeError(f"{what} failed (status {status}): {self.last_error()}")
+
+    def mfma_probe(self, kind: int, workgroups: int, iterations: int, sink: int, stream: int) -> None:
+        self._check(self._lib.piper_mfma_probe(kind, workgroups, iterations, _ptr(sink), _ptr(stream)), "piper_mfma_probe")
+
+    def issue_probe(self, args: PiperIssueProbeArgs, stream: int) -> None:
+        self._check(self._lib.piper_issue_probe(ctypes.byref(args), _ptr(stream)), "piper_issue_probe")
+
+
+_probe_library: ProbeLibrary | None = None
+
+
+def load_probe_library(path: Path | None = None) -> ProbeLibrary:
+    """Open the in-tree measurement library (once); raise :class:`LibraryUnavailableError` if absent."""
+    global _probe_library
+    with _lock:
+        if path is None and _probe_library is not None:
+            return _probe_library
+        target = Path(path) if path is not None else PROBE_LIBRARY_PATH
+        if not target.exists():
+            raise LibraryUnavailableError(f"{target} is not built; run __graft_entry__.build()")
+        try:
+            library = ProbeLibrary(target)
+        except OSError as error:
+            raise LibraryUnavailableError(f"cannot open {target}: {error}") from error
+        if path is None:
+            _probe_library = library
+        return library
+

@@ -8,15 +8,17 @@
   non-finite values counted separately), evaluated in float64 on the host.
 
 ``measure_mfma_peak`` has no counterpart in the reference (whose benchmarks quote published
-peaks only): it times the library's back-to-back MFMA probe to give the sustained dense
-matrix-core rate of the GPU at hand, which the attention kernels are priced against next to
-the published 5.0 P/s.  ``measure_mfma_valu_sharing`` (no counterpart either) times the
-same probe's MFMA-only, FMA-only and interleaved kinds at the attention kernels' occupancy, to
-show how much MFMA execution and VALU issue overlap on a SIMD.
+peaks only): it times the measurement library's back-to-back MFMA probe to give the sustained
+dense matrix-core rate of the GPU at hand, which the attention kernels are priced against next
+to the published 5.0 P/s.  ``measure_issue_sharing`` (no counterpart either) runs the issue
+probe's per-wave roles side by side on shared SIMDs, to show how VALU issue scales with waves
+per SIMD and how much MFMA execution, VALU issue and LDS reads of different waves overlap --
+the issue bound of the attention kernels.
 """
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import asdict, dataclass
 
@@ -162,29 +164,9 @@ def mfma_probe_expected(kind: int, iterations: int) -> int:
 
     if kind == native.MFMA_PROBE_I8:
         return (iterations * 2048) % (1 << 32)
-    if kind in (native.MFMA_PROBE_VALU, native.MFMA_PROBE_VALU_LDS):  # 16 chains of 4 * iterations + 1.0
-        return struct.unpack("<I", struct.pack("<f", float(iterations * 64)))[0]
-    if kind == native.MFMA_PROBE_I8_VALU:
-        return (iterations * 2048 + iterations * 64) % (1 << 32)
-    if kind == native.MFMA_PROBE_MAX3:  # 16 chains that stay at 1.0
-        return struct.unpack("<I", struct.pack("<f", 16.0))[0]
-    if kind == native.MFMA_PROBE_EXP:
-        raise ValueError("the exp probe converges to an irrational value: check it with exp_probe_ok")
-    if kind in (native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8):
-        raise ValueError("the conversion kinds store codes of their input values: use probability_codes")
-    return struct.unpack("<I", struct.pack("<f", float(iterations * 4096)))[0]
-
-
-EXP_PROBE_FIXED_POINT = 0.6411857445049859  # the root of x = 2^-x
-
-
-def exp_probe_ok(words) -> bool:
-    """Every thread of the exp probe converged to the same 16-chain sum, 16 * the root of
-    x = 2^-x to within v_exp_f32's accuracy."""
-    import numpy as np
-
-    values = np.asarray(words, dtype=np.uint32).view(np.float32)
-    return bool((values == values[0]).all() and abs(float(values[0]) - 16 * EXP_PROBE_FIXED_POINT) < 1e-4)
+    if kind == native.MFMA_PROBE_F8:
+        return struct.unpack("<I", struct.pack("<f", float(iterations * 4096)))[0]
+    raise ValueError("the conversion kinds store codes of their input values: use probability_codes")
 
 
 def probability_codes(values, codes: str, device: torch.device):
@@ -207,7 +189,7 @@ def probability_codes(values, codes: str, device: torch.device):
     sink = torch.from_numpy(host.view(np.int32)).to(device)
     stream = torch.cuda.current_stream(device)
     with torch.cuda.device(device):
-        native.load_library().mfma_probe(kinds[codes], workgroups, 1, sink.data_ptr(), stream.cuda_stream)
+        native.load_probe_library().mfma_probe(kinds[codes], workgroups, 1, sink.data_ptr(), stream.cuda_stream)
         stream.synchronize()
     words = sink.cpu().numpy().view(np.uint32).reshape(workgroups, 4, per_group // 4)
     if not (words == words[:, :1]).all():  # thread t and t + 128k pack the same four values
@@ -237,18 +219,14 @@ def _time_probe(lib, kind: int, workgroups: int, iterations: int, launches: int,
             end.synchronize()
             times.append(begin.elapsed_time(end))
     words = sink.cpu().numpy().view("uint32")
-    if kind == native.MFMA_PROBE_EXP:
-        if not exp_probe_ok(words):
-            raise RuntimeError("MFMA probe kind exp returned wrong results")
-    else:
-        expected = mfma_probe_expected(kind, iterations)
-        if not (words == expected).all():
-            raise RuntimeError(f"MFMA probe kind {kind} returned wrong results ({int((words != expected).sum())} threads)")
+    expected = mfma_probe_expected(kind, iterations)
+    if not (words == expected).all():
+        raise RuntimeError(f"MFMA probe kind {kind} returned wrong results ({int((words != expected).sum())} threads)")
     return sorted(times)[len(times) // 2]
 
 
 def measure_mfma_peak(kind: int, device: torch.device, *, iterations: int = 4096, launches: int = 5) -> dict:
-    """Sustained dense MFMA rate (tera-ops/s) of the library's probe on ``device``.
+    """Sustained dense MFMA rate (tera-ops/s) of the measurement library's probe on ``device``.
 
     Four workgroups of 8 waves per compute unit, four independent accumulator chains per wave;
     the median of ``launches`` timed launches (HIP events on the launch stream) after two
@@ -257,7 +235,7 @@ def measure_mfma_peak(kind: int, device: torch.device, *, iterations: int = 4096
     """
     from ._hip import library as native
 
-    lib = native.load_library()
+    lib = native.load_probe_library()
     workgroups = 4 * torch.cuda.get_device_properties(device).multi_processor_count
     ms = _time_probe(lib, kind, workgroups, iterations, launches, device)
     ops = workgroups * (native.MFMA_PROBE_THREADS // 64) * 4 * iterations * native.MFMA_PROBE_OPS[kind]
@@ -270,43 +248,146 @@ def measure_mfma_peak(kind: int, device: torch.device, *, iterations: int = 4096
     }
 
 
-def measure_mfma_valu_sharing(device: torch.device, *, iterations: int = 2048, launches: int = 5) -> dict:
-    """How INT8 MFMA execution and FP32 VALU issue share a SIMD at the attention kernels'
-    occupancy (one 8-wave workgroup per compute unit: two waves per SIMD).
+# instructions per round of each issue-probe role (include/piper_probe.h)
+ISSUE_ROUND = {
+    "mfma": {"mfma": 2},
+    "fma": {"valu": 32},
+    "exp": {"valu": 32},
+    "cvt": {"valu": 32},
+    "mix": {"mfma": 2, "valu": 44},
+    "valu_mix": {"valu": 44},
+    "lds": {"lds": 16},
+    "mfma_fma": {"mfma": 2, "valu": 32},
+}
 
-    Times the probe's MFMA-only, FMA-only and interleaved kinds (4 MFMAs and 64 FMAs per
-    wave-round).  ``overlap`` = (t_mfma + t_valu - t_both) / min(t_mfma, t_valu): 1 when the
-    units run concurrently, 0 when MFMA execution and VALU issue serialise.  The cycle figures
-    convert per-SIMD time at the 2.4 GHz peak clock: per MFMA, per FMA (two waves issuing), and
-    the VALU cycles one interleaved MFMA costs (its share of t_both - t_valu); and, from the
-    max3 and exp kinds, the per-SIMD cycles of a v_max3_f32 and a v_exp_f32 issued by two waves;
-    and, from the LDS kind, the VALU cycles one interleaved wave-wide ds_read_b128 costs.
-    """
+
+def run_issue_probe(device: torch.device, roles: list[str], *, cycle_budget: int = 400_000) -> dict:
+    """One launch of the issue probe (after a warm-up launch) with ``roles[s]`` for slot s of every
+    SIMD (len(roles) waves per SIMD, one workgroup per CU).  Per role: ticks per round, the
+    s_memtime ticks one SIMD takes for one round of that role (a wave's ticks divided by the rounds
+    all of that role's waves on its SIMD completed, the median over SIMDs), and the fewest and most
+    rounds a single wave completed (an uneven split shows starvation).  Every SIMD must hold
+    exactly len(roles) waves of the workgroup."""
+    import numpy as np
+
     from ._hip import library as native
 
-    if iterations > 1 << 18:
-        raise ValueError("iterations must be <= 2^18 for the exact FMA check")
-    lib = native.load_library()
+    if not 1 <= len(roles) <= native.ISSUE_MAX_WAVES_PER_SIMD:
+        raise ValueError("one to four roles")
+    codes = [native.ISSUE_ROLES.index(r) for r in roles]
+    lib = native.load_probe_library()
     workgroups = torch.cuda.get_device_properties(device).multi_processor_count
-    kinds = (native.MFMA_PROBE_I8, native.MFMA_PROBE_VALU, native.MFMA_PROBE_I8_VALU, native.MFMA_PROBE_MAX3,
-             native.MFMA_PROBE_EXP, native.MFMA_PROBE_VALU_LDS)
-    t = {k: _time_probe(lib, k, workgroups, iterations, launches, device) for k in kinds}
-    t_m, t_v, t_b = t[native.MFMA_PROBE_I8], t[native.MFMA_PROBE_VALU], t[native.MFMA_PROBE_I8_VALU]
-    cycles = 2.4e9 * 1e-3  # cycles per millisecond at the peak clock
-    waves_per_simd = native.MFMA_PROBE_THREADS // 64 // 4
-    mfmas = waves_per_simd * 4 * iterations  # per SIMD
-    fmas = waves_per_simd * 64 * iterations
+    count = workgroups * native.ISSUE_RECORDS_PER_WORKGROUP
+    records = torch.full((count * ctypes.sizeof(native.PiperIssueRecord),), 255, dtype=torch.uint8, device=device)
+    args = native.PiperIssueProbeArgs(waves_per_simd=len(roles), workgroups=workgroups, cycle_budget=cycle_budget,
+                                      records=records.data_ptr())
+    for i, c in enumerate(codes):
+        args.roles[i] = c
+    stream = torch.cuda.current_stream(device)
+    with torch.cuda.device(device):
+        for _ in range(2):
+            lib.issue_probe(args, stream.cuda_stream)
+        stream.synchronize()
+    raw = records.cpu().numpy().view(
+        np.dtype([("hw_id", "<u4"), ("xcc_id", "<u4"), ("role", "<u4"), ("slot", "<u4"), ("cycles", "<u8"),
+                  ("rounds", "<u4"), ("check", "<u4")])
+    ).reshape(workgroups, native.ISSUE_RECORDS_PER_WORKGROUP)[:, : 4 * len(roles)].reshape(-1)
+    if (raw["hw_id"] == 0xFFFFFFFF).any():
+        raise RuntimeError("issue probe: a wave wrote no record")
+    hw = raw["hw_id"].astype(np.int64)
+    simd_key = ((raw["xcc_id"].astype(np.int64) & 15) << 20) | (((hw >> 12) & 15) << 12) | (((hw >> 8) & 15) << 4) | ((hw >> 4) & 3)
+    per_role: dict[str, list[float]] = {r: [] for r in set(roles) if r != "idle"}
+    spread: dict[str, list[int]] = {r: [] for r in per_role}
+    keys, inverse, counts = np.unique(simd_key, return_inverse=True, return_counts=True)
+    if (counts != len(roles)).any():
+        raise RuntimeError(f"issue probe: SIMDs hold {sorted(set(counts.tolist()))} waves, expected {len(roles)}")
+    for simd in range(len(keys)):
+        waves = raw[inverse == simd]
+        for role in per_role:
+            mine = waves[waves["role"] == native.ISSUE_ROLES.index(role)]
+            if len(mine) == 0 or mine["rounds"].sum() == 0:
+                continue
+            per_role[role].append(float(mine["cycles"].max()) / float(mine["rounds"].sum()))
+            spread[role].extend(mine["rounds"].tolist())
     return {
-        "workgroups": workgroups,
-        "iterations": iterations,
-        "mfma_ms": round(t_m, 4),
-        "valu_ms": round(t_v, 4),
-        "both_ms": round(t_b, 4),
-        "overlap": round((t_m + t_v - t_b) / min(t_m, t_v), 3),
-        "cycles_per_mfma": round(t_m * cycles / mfmas, 1),
-        "cycles_per_fma": round(t_v * cycles / fmas, 2),
-        "cycles_per_max3": round(t[native.MFMA_PROBE_MAX3] * cycles / fmas, 2),
-        "cycles_per_exp": round(t[native.MFMA_PROBE_EXP] * cycles / fmas, 2),
-        "valu_cycles_per_lds_read": round((t[native.MFMA_PROBE_VALU_LDS] - t_v) * cycles / (fmas / 8), 1),
-        "valu_cycles_per_interleaved_mfma": round((t_b - t_v) * cycles / mfmas, 1),
+        "roles": roles,
+        "simds": int(len(keys)),
+        **{
+            role: {"ticks_per_round": round(float(np.median(v)), 2), "wave_rounds": [min(spread[role]), max(spread[role])]}
+            for role, v in per_role.items()
+        },
+    }
+
+
+def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) -> dict:
+    """How the SIMD shares issue between waves (the issue probe; s_memtime ticks, which count at
+    the shader clock):
+
+    * ``valu_ticks_per_instruction``: FP32 FMA, v_cvt_pk_u8_f32 and v_exp_f32 throughput of a SIMD
+      with 1-4 waves issuing only that class (a single wave issues at most one instruction per
+      ~6 ticks; the pipes take 2, 4 and 8 ticks per wave-wide instruction);
+    * ``mfma_ticks``: one v_mfma_i32_32x32x32_i8 of a wave issuing only MFMAs;
+    * ``cross_wave``: an MFMA-only wave beside one or three FMA-only waves: both rates next to
+      their rates alone (the verdict's wave-specialised probe A);
+    * ``in_wave``: MFMA and FMA interleaved in one wave (AGPR accumulators), one and two waves
+      per SIMD (probe B);
+    * ``attention_mix``: three waves per SIMD of the attention loop's mix (per MFMA 16 FMA,
+      4 cvt_pk_u8, 2 exp) with and without its MFMAs; ``mfma_cost_ticks`` is what one MFMA adds
+      to the SIMD's time, against its ``mfma_ticks`` duration (0: fully overlapped, equal:
+      serialised);
+    * ``lds``: wave-wide ds_read_b128 throughput of a CU (four waves per SIMD reading) in bytes
+      per tick, and the attention mix with an LDS-reading wave beside it.
+    """
+
+    def run(*roles: str) -> dict:
+        return run_issue_probe(device, list(roles), cycle_budget=cycle_budget)
+
+    def per_instr(result: dict, role: str, kind: str) -> float:
+        return round(result[role]["ticks_per_round"] / ISSUE_ROUND[role][kind], 2)
+
+    valu = {}
+    for role in ("fma", "cvt", "exp"):
+        valu[role] = {str(n): per_instr(run(*([role] * n)), role, "valu") for n in (1, 2, 3, 4)}
+    mfma_alone = run("mfma")
+    fma_alone = run("fma")
+    mfma_ticks = per_instr(mfma_alone, "mfma", "mfma")
+    pair = run("mfma", "fma")
+    quad = run("mfma", "fma", "fma", "fma")
+    fma3 = run("fma", "fma", "fma")
+    in1 = run("mfma_fma")
+    in2 = run("mfma_fma", "mfma_fma")
+    fma2 = run("fma", "fma")
+    mix3 = run("mix", "mix", "mix")
+    vmix3 = run("valu_mix", "valu_mix", "valu_mix")
+    lds4 = run("lds", "lds", "lds", "lds")
+    vmix_lds = run("valu_mix", "valu_mix", "valu_mix", "lds")
+    return {
+        "ticks": "s_memtime",
+        "cycle_budget": cycle_budget,
+        "valu_ticks_per_instruction": valu,
+        "mfma_ticks": mfma_ticks,
+        "cross_wave": {
+            "mfma_plus_fma": {"mfma_ticks": per_instr(pair, "mfma", "mfma"), "fma_ticks": per_instr(pair, "fma", "valu"),
+                              "fma_alone_ticks": per_instr(fma_alone, "fma", "valu")},
+            "mfma_plus_3_fma": {"mfma_ticks": per_instr(quad, "mfma", "mfma"),
+                                "fma_ticks": per_instr(quad, "fma", "valu"),
+                                "fma_alone_ticks": per_instr(fma3, "fma", "valu")},
+        },
+        "in_wave": {
+            "one_wave_round_ticks": in1["mfma_fma"]["ticks_per_round"],
+            "one_wave_fma_alone_ticks": fma_alone["fma"]["ticks_per_round"],
+            "two_waves_round_ticks": in2["mfma_fma"]["ticks_per_round"],
+            "two_waves_fma_alone_ticks": fma2["fma"]["ticks_per_round"],
+            "mfma_only_round_ticks": mfma_alone["mfma"]["ticks_per_round"],
+        },
+        "attention_mix": {
+            "mix_round_ticks": mix3["mix"]["ticks_per_round"],
+            "valu_mix_round_ticks": vmix3["valu_mix"]["ticks_per_round"],
+            "mfma_cost_ticks": round((mix3["mix"]["ticks_per_round"] - vmix3["valu_mix"]["ticks_per_round"]) / 2, 2),
+            "mfma_ticks": mfma_ticks,
+        },
+        "lds": {
+            "bytes_per_tick_per_cu": round(4 * 16 * 1024 / lds4["lds"]["ticks_per_round"], 1),
+            "valu_mix_round_ticks_beside_lds_wave": vmix_lds["valu_mix"]["ticks_per_round"],
+        },
     }

@@ -316,40 +316,100 @@ def test_sage_attention_validates_before_launching(lib) -> None:
         lib.sage_attention_forward(args, 0)
 
 
-def test_mfma_probe_constants_match_the_header(tmp_path) -> None:
+# ---- the measurement library (libpiper_probe.so, include/piper_probe.h) --------------------
+PROBE_HEADER = REPO / "include" / "piper_probe.h"
+
+
+@pytest.fixture(scope="module")
+def probe() -> native.ProbeLibrary:
+    return native.load_probe_library()
+
+
+def test_operator_library_exports_no_probe(lib) -> None:
+    """The probes live in their own library: the operator's ABI exports only what its header
+    declares (a test and measurement probe is no part of the product)."""
+    for name in native.PROBE_EXPORTED_SYMBOLS:
+        assert not lib.has_symbol(name), name
+    assert "mfma_probe" not in HEADER.read_text()
+
+
+def test_probe_library_exports_exactly_its_header(probe) -> None:
+    text = PROBE_HEADER.read_text()
+    declared = set(re.findall(r"^\s*(?:int|const char\*)\s+(piper_\w+)\s*\(", text, re.MULTILINE))
+    assert declared == set(native.PROBE_EXPORTED_SYMBOLS)
+    assert all(probe.has_symbol(name) for name in declared)
+
+
+def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
     source = tmp_path / "probe.c"
-    source.write_text('#include <stdio.h>\n#include "piper_mi355x.h"\nint main(void) {\n'
-                      '  printf("%d %d %d %d %d %d %d\\n", PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8, PIPER_MFMA_PROBE_THREADS,\n'
-                      '         PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8),\n'
-                      '         PIPER_MFMA_PROBE_VALU, PIPER_MFMA_PROBE_I8_VALU);\n'
-                      '  printf("%d %d %d %d %d\\n", PIPER_MFMA_PROBE_MAX3, PIPER_MFMA_PROBE_EXP, PIPER_MFMA_PROBE_VALU_LDS,\n'
-                      '         PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8);\n'
-                      '  return 0; }\n')
+    roles = ["IDLE", "MFMA", "FMA", "EXP", "CVT", "MIX", "VALU_MIX", "LDS", "MFMA_FMA"]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "piper_probe.h"', "int main(void) {",
+             '  printf("%d %d %d %d %d %d %d %d\\n", PIPER_PROBE_ABI_VERSION, PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8,'
+             ' PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8, PIPER_MFMA_PROBE_THREADS,'
+             ' PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8));']
+    lines.append('  printf("' + " ".join(["%d"] * (len(roles) + 3)) + '\\n", '
+                 + ", ".join(f"PIPER_ISSUE_{r}" for r in roles)
+                 + ", PIPER_ISSUE_ROLES, PIPER_ISSUE_MAX_WAVES_PER_SIMD, PIPER_ISSUE_RECORDS_PER_WORKGROUP);")
+    for cname, cls in (("piper_issue_record", native.PiperIssueRecord), ("piper_issue_probe_args", native.PiperIssueProbeArgs)):
+        lines.append(f'  printf("%zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("%zu\\n", offsetof({cname}, {field}));')
+    lines.append("  return 0; }")
+    source.write_text("\n".join(lines) + "\n")
     exe = tmp_path / "probe"
     subprocess.run(["gcc", f"-I{REPO / 'include'}", str(source), "-o", str(exe)], check=True)
-    values = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
-    assert values == [native.MFMA_PROBE_I8, native.MFMA_PROBE_F8, native.MFMA_PROBE_THREADS,
-                      native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8],
-                      native.MFMA_PROBE_VALU, native.MFMA_PROBE_I8_VALU, native.MFMA_PROBE_MAX3,
-                      native.MFMA_PROBE_EXP, native.MFMA_PROBE_VALU_LDS, native.MFMA_PROBE_P_CODES_U8,
-                      native.MFMA_PROBE_P_CODES_FP8]
+    values = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()))
+    assert values[:8] == [native.PROBE_ABI_VERSION, native.MFMA_PROBE_I8, native.MFMA_PROBE_F8,
+                          native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8, native.MFMA_PROBE_THREADS,
+                          native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8]]
+    assert values[8:17] == list(range(len(native.ISSUE_ROLES)))
+    assert [r.upper() for r in native.ISSUE_ROLES] == roles
+    assert values[17:20] == [len(native.ISSUE_ROLES), native.ISSUE_MAX_WAVES_PER_SIMD, native.ISSUE_RECORDS_PER_WORKGROUP]
+    offsets = values[20:]
+    expected = []
+    for cls in (native.PiperIssueRecord, native.PiperIssueProbeArgs):
+        expected.append(ctypes.sizeof(cls))
+        expected.extend(getattr(cls, field).offset for field, _ in cls._fields_)
+    assert offsets == expected
     # 32x32x32 INT8 and 32x32x64 FP8: two operations per multiply-add
     assert native.MFMA_PROBE_OPS == {native.MFMA_PROBE_I8: 2 * 32 * 32 * 32, native.MFMA_PROBE_F8: 2 * 32 * 32 * 64}
 
 
-def test_mfma_probe_validates_before_launching(lib) -> None:
+def test_mfma_probe_validates_before_launching(probe) -> None:
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
-        lib.mfma_probe(9, 1, 1, 0x1000, 0)
+        probe.mfma_probe(4, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
-        lib.mfma_probe(-1, 1, 1, 0x1000, 0)
+        probe.mfma_probe(-1, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="workgroups and"):
-        lib.mfma_probe(native.MFMA_PROBE_I8, 0, 1, 0x1000, 0)
+        probe.mfma_probe(native.MFMA_PROBE_I8, 0, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="workgroups and"):
-        lib.mfma_probe(native.MFMA_PROBE_F8, 1, 0, 0x1000, 0)
+        probe.mfma_probe(native.MFMA_PROBE_F8, 1, 0, 0x1000, 0)
     with pytest.raises(RuntimeError, match="sink must be"):
-        lib.mfma_probe(native.MFMA_PROBE_I8, 1, 1, 0, 0)
+        probe.mfma_probe(native.MFMA_PROBE_I8, 1, 1, 0, 0)
     with pytest.raises(RuntimeError, match="sink must be"):
-        lib.mfma_probe(native.MFMA_PROBE_I8, 1, 1, 0x1002, 0)
+        probe.mfma_probe(native.MFMA_PROBE_I8, 1, 1, 0x1002, 0)
+
+
+def test_issue_probe_validates_before_launching(probe) -> None:
+    args = native.PiperIssueProbeArgs(waves_per_simd=0, workgroups=1, cycle_budget=10000, records=0x1000)
+    with pytest.raises(RuntimeError, match="waves_per_simd"):
+        probe.issue_probe(args, 0)
+    args.waves_per_simd = 5
+    with pytest.raises(RuntimeError, match="waves_per_simd"):
+        probe.issue_probe(args, 0)
+    args.waves_per_simd, args.workgroups = 2, 0
+    with pytest.raises(RuntimeError, match="workgroups"):
+        probe.issue_probe(args, 0)
+    args.workgroups, args.cycle_budget = 1, 10
+    with pytest.raises(RuntimeError, match="cycle_budget"):
+        probe.issue_probe(args, 0)
+    args.cycle_budget, args.records = 10000, 0x1004
+    with pytest.raises(RuntimeError, match="records"):
+        probe.issue_probe(args, 0)
+    args.records = 0x1000
+    args.roles[1] = len(native.ISSUE_ROLES)
+    with pytest.raises(RuntimeError, match="unknown role"):
+        probe.issue_probe(args, 0)
 
 
 def test_mfma_probe_expected_words() -> None:
@@ -358,11 +418,7 @@ def test_mfma_probe_expected_words() -> None:
     assert mfma_probe_expected(native.MFMA_PROBE_I8, 4096) == 4096 * 64 * 32
     assert mfma_probe_expected(native.MFMA_PROBE_I8, 1 << 21) == (64 * 32 << 21) % (1 << 32)
     assert mfma_probe_expected(native.MFMA_PROBE_F8, 4096) == 0x4B800000  # 2^24 as FP32
-    # 16 FMA chains, each 4 * iterations increments of 1.0: 64 * 2048 = 2^17 as FP32
-    assert mfma_probe_expected(native.MFMA_PROBE_VALU, 2048) == 0x48000000
-    assert mfma_probe_expected(native.MFMA_PROBE_I8_VALU, 2048) == 2048 * 2048 + 64 * 2048
-    assert mfma_probe_expected(native.MFMA_PROBE_MAX3, 7) == 0x41800000  # 16.0
-    for kind in (native.MFMA_PROBE_EXP, native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8):
+    for kind in (native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8):
         with pytest.raises(ValueError):
             mfma_probe_expected(kind, 1)
 
@@ -373,21 +429,3 @@ def test_probability_codes_rejects_unknown_codes() -> None:
 
     with pytest.raises(ValueError, match="'u8' or 'fp8'"):
         probability_codes([0.5], "int4", torch.device("cpu"))
-
-
-def test_exp_probe_check() -> None:
-    import math
-
-    import numpy as np
-    from piper_kernels.measure import EXP_PROBE_FIXED_POINT, exp_probe_ok
-
-    assert abs(EXP_PROBE_FIXED_POINT - 2.0 ** -EXP_PROBE_FIXED_POINT) < 1e-15
-    x = 0.0  # the chain the probe runs, in float32 with a correctly rounded 2^-x
-    for _ in range(64):
-        x = float(np.float32(math.pow(2.0, -x)))
-    good = np.full(8, np.float32(16 * x)).view(np.uint32)
-    assert exp_probe_ok(good)
-    bad = good.copy()
-    bad[3] ^= 1
-    assert not exp_probe_ok(bad)
-    assert not exp_probe_ok(np.full(8, np.float32(16.0)).view(np.uint32))
