@@ -328,9 +328,9 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
       ~6 ticks; the pipes take 2, 4 and 8 ticks per wave-wide instruction);
     * ``mfma_ticks``: one v_mfma_i32_32x32x32_i8 of a wave issuing only MFMAs;
     * ``cross_wave``: an MFMA-only wave beside one or three FMA-only waves: both rates next to
-      their rates alone (the verdict's wave-specialised probe A);
+      their rates alone;
     * ``in_wave``: MFMA and FMA interleaved in one wave (AGPR accumulators), one and two waves
-      per SIMD (probe B);
+      per SIMD;
     * ``attention_mix``: three waves per SIMD of the attention loop's mix (per MFMA 16 FMA,
       4 cvt_pk_u8, 2 exp) with and without its MFMAs; ``mfma_cost_ticks`` is what one MFMA adds
       to the SIMD's time, against its ``mfma_ticks`` duration (0: fully overlapped, equal:
