@@ -12,95 +12,103 @@
 #include "kernels.h"
 #include "quant.h"
 
+#include <type_traits>
+
 namespace piper {
 
 // ---------------------------------------------------------------------------------------
-// Means, pass 1: one thread owns a column pair of one chunk of L^2 rows of K (tensor 0) or V
-// (tensor 1).  It sums each L-row block in row order and the chunk's complete blocks in block
-// order (the first two cascade levels); the thread of the last chunk also sums the trailing
-// length % L rows.  SageAttention2++'s V statistic is the per-column max |v| instead (exact in
-// any order).
+// Means, pass 1: one workgroup per chunk of L^2 rows of K (tensor 0) or V (tensor 1) of one
+// batch-head.  Thread (slot, column group) sums L-row blocks slot, slot + kSlots, ... of eight
+// columns, each block's rows in row order from +0.0 (cascade level 0), with 16-byte loads of
+// all the block's rows in flight; the block sums meet in LDS, and one thread per column adds
+// the chunk's complete blocks in block order (level 1).  A short last chunk's trailing
+// length % L rows are its last, incomplete block: their sum goes to slot `chunks`.
+// SageAttention2++'s V statistic is the per-column max |v| instead (exact in any order).
 // ---------------------------------------------------------------------------------------
-template <bool kBf16>
-__device__ __forceinline__ float2 widen_pair(uint32_t bits) {
-  if constexpr (kBf16) return make_float2(__uint_as_float(bits << 16), __uint_as_float(bits & 0xffff0000u));
-  return make_float2(half_bits_to_float(bits & 0xffffu), half_bits_to_float(bits >> 16));
+template <bool kBf16, bool kAbsMax, bool kGuard>
+__device__ __forceinline__ void sum_block_rows(const uint16_t* rows, long stride, int n, float (&acc)[8]) {
+  constexpr int kUnroll = 16;  // rows in flight (16 B each); L is a power of two >= 16
+  for (int r = 0; r < (kGuard ? n : kUnroll); r += kUnroll) {
+    uint4 raw[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      raw[u] = !kGuard || r + u < n ? *reinterpret_cast<const uint4*>(rows + static_cast<long>(r + u) * stride)
+                                    : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (!kGuard || r + u < n) {
+        float f[8];
+        widen8<kBf16>(raw[u], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = kAbsMax ? fmaxf(acc[i], fabsf(f[i])) : acc[i] + f[i];
+      }
+    }
+  }
+}
+
+template <bool kBf16, int D, bool kAbsMax>
+__device__ __forceinline__ void chunk_block_sums(const uint16_t* base, long stride, int L, int full, int blocks,
+                                                 int tail, int slot, int group, float* block_sums) {
+  constexpr int kSlots = 256 / (D / 8);
+  for (int blk = slot; blk < blocks; blk += kSlots) {
+    const uint16_t* rows = base + static_cast<long>(blk) * L * stride;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (blk < full) {
+      for (int r = 0; r < L; r += 16) sum_block_rows<kBf16, kAbsMax, false>(rows + r * stride, stride, 16, acc);
+    } else {
+      sum_block_rows<kBf16, kAbsMax, true>(rows, stride, tail, acc);
+    }
+    float4* dst = reinterpret_cast<float4*>(block_sums + blk * D + 8 * group);
+    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
+// One chunk's partial sums into p.partials; `block_sums` is LDS of L * D floats.  Every thread of
+// the workgroup takes part (a barrier inside).
+template <bool kBf16, int D>
+__device__ __forceinline__ void mean_chunk(const MeanParams& p, int tensor, int bh, int chunk, float* block_sums) {
+  constexpr int kGroups = D / 8;
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  const InputTensor& t = tensor == 0 ? p.key : p.value;
+  const bool absmax = tensor == 1 && p.value_absmax;
+  const int L = p.block_rows;
+  const long row0 = static_cast<long>(chunk) * L * L;
+  const int rows = static_cast<int>(min(static_cast<long>(L) * L, p.length - row0));
+  const int full = rows / L;
+  const int tail = rows - full * L;
+  const int blocks = full + (tail > 0 ? 1 : 0);
+  const int group = threadIdx.x % kGroups;
+  const uint16_t* base =
+      static_cast<const uint16_t*>(t.data) + b * t.stride_batch + h * t.stride_head + row0 * t.stride_seq + 8 * group;
+  if (absmax)
+    chunk_block_sums<kBf16, D, true>(base, t.stride_seq, L, full, blocks, tail, threadIdx.x / kGroups, group,
+                                     block_sums);
+  else
+    chunk_block_sums<kBf16, D, false>(base, t.stride_seq, L, full, blocks, tail, threadIdx.x / kGroups, group,
+                                      block_sums);
+  __syncthreads();
+  if (threadIdx.x >= D) return;
+  const int col = threadIdx.x;
+  float s = 0.0f;  // level 1: the complete blocks, in order
+  for (int blk = 0; blk < full; ++blk) {
+    const float v = block_sums[blk * D + col];
+    s = absmax ? fmaxf(s, v) : s + v;
+  }
+  float* out = p.partials + ((static_cast<long>(tensor) * p.batch_heads + bh) * (p.chunks + 1) + chunk) * D + col;
+  out[0] = s;
+  if (chunk == p.chunks - 1) out[D] = tail > 0 ? block_sums[full * D + col] : 0.0f;  // slot `chunks`
 }
 
 template <bool kBf16, int D>
 __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
-  constexpr int kPairs = D / 2;
-  constexpr int kUnroll = 16;  // loads in flight; L is a power of two >= 16
-  const long gid = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-  const long per_tensor = static_cast<long>(p.batch_heads) * p.chunks * kPairs;
-  if (gid >= per_tensor * p.tensors) return;
-  const int tensor = static_cast<int>(gid / per_tensor);
-  const long rem = gid - tensor * per_tensor;
-  const int pair = static_cast<int>(rem % kPairs);
-  const int chunk = static_cast<int>((rem / kPairs) % p.chunks);
-  const int bh = static_cast<int>(rem / (static_cast<long>(kPairs) * p.chunks));
-  const int b = bh / p.heads;
-  const int h = bh - b * p.heads;
-
-  const InputTensor& t = tensor == 0 ? p.key : p.value;
-  // two adjacent 16-bit elements per 4-byte load (rows are 16-byte aligned, so the pair is too)
-  const uint16_t* base = static_cast<const uint16_t*>(t.data) + b * t.stride_batch + h * t.stride_head + 2 * pair;
-  const int block = p.block_rows;
-  const long chunk_rows = static_cast<long>(block) * block;
-  const int row0 = static_cast<int>(chunk * chunk_rows);
-  const int row1 = static_cast<int>(min(row0 + chunk_rows, static_cast<long>(p.length)));
-  const int blocks = (row1 - row0) / block;
-  const bool absmax = tensor == 1 && p.value_absmax;
-
-  float s0 = 0.0f, s1 = 0.0f;  // level 1: complete blocks of this chunk, in order
-  int row = row0;
-  for (int blk = 0; blk < blocks; ++blk) {
-    float b0 = 0.0f, b1 = 0.0f;  // level 0: the block's rows, in order
-    for (int r = 0; r < block; r += kUnroll) {
-      uint32_t raw[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        raw[u] = *reinterpret_cast<const uint32_t*>(base + static_cast<long>(row + u) * t.stride_seq);
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const float2 f = widen_pair<kBf16>(raw[u]);
-        if (absmax) {
-          b0 = fmaxf(b0, fabsf(f.x));
-          b1 = fmaxf(b1, fabsf(f.y));
-        } else {
-          b0 += f.x;
-          b1 += f.y;
-        }
-      }
-      row += kUnroll;
-    }
-    if (absmax) {
-      s0 = fmaxf(s0, b0);
-      s1 = fmaxf(s1, b1);
-    } else {
-      s0 += b0;
-      s1 += b1;
-    }
-  }
-  float* out = p.partials + ((static_cast<long>(tensor) * p.batch_heads + bh) * (p.chunks + 1) + chunk) * D + 2 * pair;
-  out[0] = s0;
-  out[1] = s1;
-  if (chunk == p.chunks - 1) {  // the trailing rows, summed in order from +0.0 (slot `chunks`)
-    float a0 = 0.0f, a1 = 0.0f;
-    for (; row < row1; ++row) {
-      const float2 f = widen_pair<kBf16>(*reinterpret_cast<const uint32_t*>(base + static_cast<long>(row) * t.stride_seq));
-      if (absmax) {
-        a0 = fmaxf(a0, fabsf(f.x));
-        a1 = fmaxf(a1, fabsf(f.y));
-      } else {
-        a0 += f.x;
-        a1 += f.y;
-      }
-    }
-    out[D] = a0;
-    out[D + 1] = a1;
-  }
+  extern __shared__ float block_sums[];  // [L][D]
+  const int chunk = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.chunks));
+  const int rest = static_cast<int>(blockIdx.x / static_cast<unsigned>(p.chunks));
+  mean_chunk<kBf16, D>(p, rest / p.batch_heads, rest % p.batch_heads, chunk, block_sums);
 }
+
 
 // Means, pass 2, one thread per (tensor, batch-head, column): the complete chunks' level-1 sums
 // are added in groups of L (level 2), the group sums in order (level 3); then
@@ -108,19 +116,13 @@ __global__ void __launch_bounds__(256) mean_partial_kernel(const MeanParams p) {
 // in FP32.  Causal calls write a zero V mean.  SageAttention2++ (value_absmax): the V column's
 // max |v| over the chunks gives its FP8 scale amax / 2.25 + 1e-7
 // (sage_attention_2pp/reference.py:22-23: FP32 division, FP32 add).
-__global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, int head_dim) {
-  const int gid = blockIdx.x * 64 + threadIdx.x;
-  const int per_tensor = p.batch_heads * head_dim;
-  if (gid >= 2 * per_tensor) return;
-  const int tensor = gid / per_tensor;
-  const int rem = gid - tensor * per_tensor;
+__device__ __forceinline__ void finalize_column(const MeanParams& p, int tensor, int bh, int d, int head_dim) {
+  const int rem = bh * head_dim + d;
   float* dst = tensor == 0 ? p.key_mean : p.value_mean;
   if (tensor >= p.tensors) {
     dst[rem] = 0.0f;
     return;
   }
-  const int bh = rem / head_dim;
-  const int d = rem - bh * head_dim;
   const float* src =
       p.partials + (static_cast<long>(tensor) * p.batch_heads + bh) * (p.chunks + 1) * head_dim + d;
   if (tensor == 1 && p.value_absmax) {
@@ -160,6 +162,15 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
   dst[rem] = total / static_cast<float>(p.length);
 }
 
+__global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, int head_dim) {
+  const int gid = blockIdx.x * 64 + threadIdx.x;
+  const int per_tensor = p.batch_heads * head_dim;
+  if (gid >= 2 * per_tensor) return;
+  const int tensor = gid / per_tensor;
+  const int rem = gid - tensor * per_tensor;
+  finalize_column(p, tensor, rem / head_dim, rem % head_dim, head_dim);
+}
+
 // ---------------------------------------------------------------------------------------
 // Quantisation.  Each wave owns one unit: a 32-row Q block, a 64-row K block or a 64-key V
 // tile (a workgroup of 4 waves holds units of one kind only).  No LDS: V tiles are written
@@ -172,7 +183,7 @@ __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, i
 // go to scale_out (per block: the one scale repeated), and key tiles carry them in the padding
 // of K row 0 as well (bytes [D, D + 4 * kSlots)).  Codes go to rows of kStride bytes (D for
 // query codes, the padded tile stride for keys).
-template <bool kBf16, int D, int kRows, bool kCenter, int kStride, int kSlots>
+template <bool kBf16, int D, int kRows, bool kCenter, int kStride, int kSlots, bool kGuard>
 __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int h, int row0, int length,
                                                const float* __restrict__ mean, int8_t* __restrict__ codes,
                                                float* __restrict__ scale_out, bool per_thread) {
@@ -194,8 +205,8 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
     const int row = row0 + it * kRowsPerIter + sub;
-    raw[it] = row < length ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * in.stride_seq)
-                           : make_uint4(0, 0, 0, 0);
+    raw[it] = !kGuard || row < length ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * in.stride_seq)
+                                      : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
@@ -205,7 +216,7 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       // padded rows are zero after centring (sage/reference.py:13-20 pads the centred K)
-      const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
+      const float x = !kGuard || row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
       amax[it & 1] = fmaxf(amax[it & 1], fabsf(x));
     }
   }
@@ -228,6 +239,11 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
     scale[1] = scale_from_amax(amax[1]);
   }
   const Divisor divisor[2] = {Divisor(scale[0]), Divisor(scale[1])};
+  // The second pass widens and centres again from the packed rows: an empty asm "redefines"
+  // them, so the compiler cannot keep the first pass's 8 floats per row live instead (64 more
+  // VGPRs, which would halve the waves per SIMD).
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) asm volatile("" : "+v"(raw[it].x), "+v"(raw[it].y), "+v"(raw[it].z), "+v"(raw[it].w));
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
     const int row = row0 + it * kRowsPerIter + sub;
@@ -236,7 +252,7 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
     uint32_t c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float x = row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
+      const float x = !kGuard || row < length ? (kCenter ? f[i] - mu[i] : f[i]) : 0.0f;
       c[i] = code_word(x, divisor[it & 1]);
     }
     uint2 packed = make_uint2(pack_low_bytes(c[0], c[1], c[2], c[3]), pack_low_bytes(c[4], c[5], c[6], c[7]));
@@ -259,52 +275,51 @@ __device__ __forceinline__ void quantize_block(const InputTensor& in, int b, int
   }
 }
 
-template <bool kBf16, int D>
-__global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int block = blockIdx.x;
-
-  if (block < p.q_blocks_wg) {
-    const int unit = block * 4 + wave;
-    if (unit >= p.batch_heads * p.nqb) return;
-    const int bh = unit / p.nqb;
-    const int qb = unit - bh * p.nqb;
-    const int b = bh / p.heads;
-    const int h = bh - b * p.heads;
-    quantize_block<kBf16, D, kQueryBlock, false, D, kQueryScaleSlots>(
-        p.query, b, h, qb * kQueryBlock, p.query_length, nullptr,
-        p.query_code + (static_cast<long>(bh) * p.sq32 + qb * kQueryBlock) * D,
-        p.query_scale + static_cast<long>(unit) * kQueryScaleSlots, p.per_thread);
-    return;
+// V tile: per-key scales, codes written transposed from registers, tile column sums.  Lane
+// (group, sub) owns columns [8 group, +8) of the kKeys consecutive keys [kKeys sub, +kKeys): its
+// codes, packed four keys to a word, are the 16-byte (D = 128) or 8-byte (D = 64) pieces of its
+// eight V^T rows -- no transpose through LDS.  A key's |v| maximum is reduced over the kGroups
+// lanes of its row of lanes with DPP.  The code words fill the registers the raw rows free, so
+// the kernel fits four waves per SIMD, which overlap one another's loads with their arithmetic.
+template <int kLanes>
+__device__ __forceinline__ float row_group_max(float v) {  // max over aligned groups of kLanes lanes (8 or 16)
+  v = fmaxf(v, dpp<0xB1>(v));  // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp<0x4E>(v));  // quad_perm [2,3,0,1]
+  if constexpr (kLanes == 8) {
+    v = fmaxf(v, dpp<0x141>(v));  // row_half_mirror: lane i and 7 - i of each half row
+  } else {
+    static_assert(kLanes == 16, "8 or 16 lanes");
+    v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
+    v = fmaxf(v, dpp<0x128>(v));  // row_ror:8
   }
-  if (block < p.q_blocks_wg + p.k_blocks_wg) {
-    const int unit = (block - p.q_blocks_wg) * 4 + wave;
-    if (unit >= p.batch_heads * p.nkb) return;
-    const int bh = unit / p.nkb;
-    const int kb = unit - bh * p.nkb;
-    const int b = bh / p.heads;
-    const int h = bh - b * p.heads;
-    int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * kv_tile_bytes(D);
-    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots>(
-        p.key, b, h, kb * kKeyBlock, p.key_length, p.key_mean + static_cast<long>(bh) * D, tile,
-        p.key_scale + static_cast<long>(unit) * kKeyScaleSlots, p.per_thread);
-    return;
-  }
+  return v;
+}
 
-  // ---- V tile: per-key scales, codes written transposed from registers, tile column sums ----
-  const int unit = (block - p.q_blocks_wg - p.k_blocks_wg) * 4 + wave;
-  if (unit >= p.batch_heads * p.nkb) return;
+template <int kN, int kI = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {  // f(integral_constant<int, i>) for i = 0 .. kN - 1
+  if constexpr (kI < kN) {
+    f(std::integral_constant<int, kI>{});
+    static_for<kN, kI + 1>(f);
+  }
+}
+
+// `word`'s low byte placed at byte kByte of `packed` (v_perm_b32 selectors: 0-3 pick bytes of
+// the second operand, 4 the first operand's byte 0)
+template <int kByte>
+__device__ __forceinline__ uint32_t insert_byte(uint32_t packed, uint32_t word) {
+  constexpr uint32_t kSel = (0x03020100u & ~(0xffu << (8 * kByte))) | (0x04u << (8 * kByte));
+  return __builtin_amdgcn_perm(word, packed, kSel);
+}
+
+template <bool kBf16, int D, bool kGuard>
+__device__ __forceinline__ void quantize_value_tile(const QuantParams& p, int unit, int lane) {
+  constexpr int kGroups = D / 8;
+  constexpr int kSubs = kWave / kGroups;
+  constexpr int kKeys = kKeyBlock / kSubs;
   const int bh = unit / p.nkb;
   const int kb = unit - bh * p.nkb;
   const int b = bh / p.heads;
   const int h = bh - b * p.heads;
-  // lane (group, sub) owns columns [8 group, +8) of the kKeys consecutive keys
-  // [kKeys sub, +kKeys): its codes, packed four keys to a word, are the 16-byte (D = 128) or
-  // 8-byte (D = 64) pieces of its eight V^T rows -- no transpose through LDS.
-  constexpr int kGroups = D / 8;
-  constexpr int kSubs = kWave / kGroups;
-  constexpr int kKeys = kKeyBlock / kSubs;
   const int group = lane % kGroups;
   const int sub = lane / kGroups;
   const int key0 = sub * kKeys;  // first key of this lane in the tile
@@ -314,45 +329,46 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
 #pragma unroll
   for (int j = 0; j < kKeys; ++j) {
     const int row = kb * kKeyBlock + key0 + j;
-    raw[j] = row < p.key_length ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
-                                : make_uint4(0, 0, 0, 0);
+    raw[j] = !kGuard || row < p.key_length
+                 ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
+                 : make_uint4(0, 0, 0, 0);
   }
   float mu[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) mu[i] = p.center_value ? p.value_mean[static_cast<long>(bh) * D + group * 8 + i] : 0.0f;
+
   uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D);
-  float* meta = reinterpret_cast<float*>(tile + kv_log_offset(D));
-  uint32_t packed[8][kKeys / 4];  // [column][four keys]
   int colsum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  float own_scale = 0.0f;  // the scale of key key0 + group (lane group < kKeys), for the metadata
+  float own_scale = 0.0f;  // the scale of key key0 + group (lanes with group < kKeys), for the metadata
+  uint32_t packed[8][kKeys / 4];  // [column][four keys]: filled as raw[] empties, so the two share registers
 #pragma unroll
   for (int j4 = 0; j4 < kKeys / 4; ++j4) {
-    uint32_t word[4][8];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    static_for<4>([&](auto u) {
       const int j = 4 * j4 + u;
-      const int row = kb * kKeyBlock + key0 + j;
-      const bool valid = row < p.key_length;
-      float f[8];
-      widen8<kBf16>(raw[j], f);
-      float amax = 0.0f;
+      const bool valid = !kGuard || kb * kKeyBlock + key0 + j < p.key_length;
+      float x[8];
+      widen8<kBf16>(raw[j], x);
+      float m = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        f[i] = valid ? f[i] - mu[i] : 0.0f;
-        amax = fmaxf(amax, fabsf(f[i]));
+        x[i] = valid ? x[i] - mu[i] : 0.0f;
+        m = fmaxf(m, fabsf(x[i]));
       }
-      amax = group_max<kGroups>(amax);
-      const float scale = scale_from_amax(amax);
+      const float scale = scale_from_amax(row_group_max<kGroups>(m));
       const Divisor divisor(scale);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) word[u][i] = code_word(f[i], divisor);
       if (group == j) own_scale = scale;
-    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      packed[i][j4] = pack_low_bytes(word[0][i], word[1][i], word[2][i], word[3][i]);
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t word = code_word(x[i], divisor);
+        if constexpr (u == 0)
+          packed[i][j4] = word;  // bytes 1-3 are replaced by the next three keys
+        else
+          packed[i][j4] = insert_byte<u>(packed[i][j4], word);
+      }
+    });
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
       colsum[i] = __builtin_amdgcn_sdot4(static_cast<int>(packed[i][j4]), 0x01010101, colsum[i], false);
-    }
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -363,9 +379,10 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
       *reinterpret_cast<uint2*>(dst) = make_uint2(packed[i][0], packed[i][1]);
   }
   // per-key metadata, one key per lane: lane (group, sub) with group < kKeys owns key key0 + group
+  float* meta = reinterpret_cast<float*>(tile + kv_log_offset(D));
   if (group < kKeys) {
     const int row = kb * kKeyBlock + key0 + group;
-    const bool valid = row < p.key_length;
+    const bool valid = !kGuard || row < p.key_length;
     p.value_scale[static_cast<long>(bh) * p.sk64 + row] = valid ? own_scale : 0.0f;
     meta[key0 + group] = valid ? log2f(own_scale) : -__builtin_inff();
     meta[kKeyBlock + key0 + group] = valid ? 1.0f / (255.0f * own_scale) : 0.0f;
@@ -381,6 +398,71 @@ __global__ void __launch_bounds__(256) quantize_kernel(const QuantParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) correction[i] = 128 * colsum[i] + kAccBias;
   }
+}
+
+template <bool kBf16, int D>
+__device__ __forceinline__ void quantize_query_unit(const QuantParams& p, int unit) {  // one 32-row Q block
+  const int bh = unit / p.nqb;
+  const int qb = unit - bh * p.nqb;
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  int8_t* codes = p.query_code + (static_cast<long>(bh) * p.sq32 + qb * kQueryBlock) * D;
+  float* scales = p.query_scale + static_cast<long>(unit) * kQueryScaleSlots;
+  if ((qb + 1) * kQueryBlock <= p.query_length)
+    quantize_block<kBf16, D, kQueryBlock, false, D, kQueryScaleSlots, false>(
+        p.query, b, h, qb * kQueryBlock, p.query_length, nullptr, codes, scales, p.per_thread);
+  else
+    quantize_block<kBf16, D, kQueryBlock, false, D, kQueryScaleSlots, true>(
+        p.query, b, h, qb * kQueryBlock, p.query_length, nullptr, codes, scales, p.per_thread);
+}
+
+template <bool kBf16, int D>
+__device__ __forceinline__ void quantize_key_unit(const QuantParams& p, int unit) {  // one 64-row K block
+  const int bh = unit / p.nkb;
+  const int kb = unit - bh * p.nkb;
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * kv_tile_bytes(D);
+  const float* mean = p.key_mean + static_cast<long>(bh) * D;
+  float* scales = p.key_scale + static_cast<long>(unit) * kKeyScaleSlots;
+  if ((kb + 1) * kKeyBlock <= p.key_length)
+    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots, false>(
+        p.key, b, h, kb * kKeyBlock, p.key_length, mean, tile, scales, p.per_thread);
+  else
+    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots, true>(
+        p.key, b, h, kb * kKeyBlock, p.key_length, mean, tile, scales, p.per_thread);
+}
+
+template <bool kBf16, int D>
+__device__ __forceinline__ void quantize_value_unit(const QuantParams& p, int unit, int lane) {  // one 64-key V tile
+  if ((unit % p.nkb + 1) * kKeyBlock <= p.key_length)
+    quantize_value_tile<kBf16, D, false>(p, unit, lane);
+  else
+    quantize_value_tile<kBf16, D, true>(p, unit, lane);
+}
+
+// One wave per unit, four units of one kind per workgroup: Q blocks (two-step path), K blocks,
+// V tiles.  Four waves per SIMD (at most 128 VGPRs) overlap one another's loads with their
+// arithmetic.  Causal calls take the K blocks last-read-first: the mean pass has just read K (and
+// only K), so the most recently read rows are still in the last-level cache.
+template <bool kBf16, int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) quantize_kernel(const QuantParams p) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int block = blockIdx.x;
+  if (block < p.q_blocks_wg) {
+    const int unit = block * 4 + wave;
+    if (unit < p.batch_heads * p.nqb) quantize_query_unit<kBf16, D>(p, unit);
+    return;
+  }
+  block -= p.q_blocks_wg;
+  if (block < p.k_blocks_wg) {
+    const int unit = (p.center_value ? block : p.k_blocks_wg - 1 - block) * 4 + wave;
+    if (unit < p.batch_heads * p.nkb) quantize_key_unit<kBf16, D>(p, unit);
+    return;
+  }
+  const int unit = (block - p.k_blocks_wg) * 4 + wave;
+  if (unit < p.batch_heads * p.nkb) quantize_value_unit<kBf16, D>(p, unit, lane);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -405,9 +487,14 @@ __global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParam
     const int b = bh / p.heads;
     const int h = bh - b * p.heads;
     int8_t* tile = reinterpret_cast<int8_t*>(p.kv_tiles) + static_cast<long>(unit) * sage_tile_bytes(D);
-    quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots>(
-        p.key, b, h, kb * kKeyBlock, p.key_length, p.key_mean + static_cast<long>(bh) * D, tile,
-        p.key_scale + static_cast<long>(unit) * kKeyScaleSlots, p.per_thread);
+    const float* mean = p.key_mean + static_cast<long>(bh) * D;
+    float* scales = p.key_scale + static_cast<long>(unit) * kKeyScaleSlots;
+    if ((kb + 1) * kKeyBlock <= p.key_length)
+      quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots, false>(
+          p.key, b, h, kb * kKeyBlock, p.key_length, mean, tile, scales, p.per_thread);
+    else
+      quantize_block<kBf16, D, kKeyBlock, true, kv_k_stride(D), kKeyScaleSlots, true>(
+          p.key, b, h, kb * kKeyBlock, p.key_length, mean, tile, scales, p.per_thread);
     return;
   }
 
@@ -470,11 +557,18 @@ __global__ void __launch_bounds__(256) sage_quantize_kernel(const SageQuantParam
 // host launchers
 // ---------------------------------------------------------------------------------------
 template <bool kBf16, int D>
+static hipError_t launch_mean_partials(const MeanParams& mp, hipStream_t stream) {
+  // one workgroup per (tensor, batch-head, chunk); LDS holds the chunk's L block sums of D columns
+  const long workgroups = static_cast<long>(mp.tensors) * mp.batch_heads * mp.chunks;
+  const size_t lds = static_cast<size_t>(mp.block_rows) * D * sizeof(float);
+  hipLaunchKernelGGL((mean_partial_kernel<kBf16, D>), dim3(static_cast<unsigned>(workgroups)), dim3(256), lds, stream,
+                     mp);
+  return hipGetLastError();
+}
+
+template <bool kBf16, int D>
 static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {
-  const long mean_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 2) * mp.tensors;
-  hipLaunchKernelGGL((mean_partial_kernel<kBf16, D>), dim3(static_cast<unsigned>((mean_threads + 255) / 256)),
-                     dim3(256), 0, stream, mp);
-  hipError_t err = hipGetLastError();
+  hipError_t err = launch_mean_partials<kBf16, D>(mp, stream);
   if (err != hipSuccess) return err;
   const int fin_threads = 2 * mp.batch_heads * D;
   hipLaunchKernelGGL(mean_finalize_kernel, dim3((fin_threads + 63) / 64), dim3(64), 0, stream, mp, D);
@@ -487,10 +581,7 @@ static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp,
 
 template <bool kBf16, int D>
 static hipError_t launch_sage_prep_typed(const MeanParams& mp, const SageQuantParams& qp, hipStream_t stream) {
-  const long stat_threads = static_cast<long>(mp.batch_heads) * mp.chunks * (D / 2) * mp.tensors;
-  hipLaunchKernelGGL((mean_partial_kernel<kBf16, D>), dim3(static_cast<unsigned>((stat_threads + 255) / 256)),
-                     dim3(256), 0, stream, mp);
-  hipError_t err = hipGetLastError();
+  hipError_t err = launch_mean_partials<kBf16, D>(mp, stream);
   if (err != hipSuccess) return err;
   const int fin_threads = 2 * mp.batch_heads * D;
   hipLaunchKernelGGL(mean_finalize_kernel, dim3((fin_threads + 63) / 64), dim3(64), 0, stream, mp, D);
