@@ -150,7 +150,9 @@ typedef struct piper_layout {
   int64_t kv_tiles_bytes; /* all tile records */
   int64_t workspace_bytes; /* scratch for piper_prepare: FP32 partial sums of the K/V means
                               (torch's CPU summation order, so the means and every K/V code
-                              equal the reference's torch.mean(dim=2) path bit for bit) */
+                              equal the reference's torch.mean(dim=2) path bit for bit), then
+                              4 * (4 * B * H + 4) bytes of arrival counters and a status
+                              word; the library clears what it needs on the stream */
 } piper_layout;
 
 /* piper_prepare_args.flags */

@@ -193,7 +193,7 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
   layout->mean_bytes = bh * d * 4;
   layout->kv_tile_bytes = PIPER_KV_TILE_BYTES(d);
   layout->kv_tiles_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * PIPER_KV_TILE_BYTES(d);
-  layout->workspace_bytes = 2 * bh * (chunks + 1) * d * 4;
+  layout->workspace_bytes = 2 * bh * (chunks + 1) * d * 4 + 4 * piper::prep_sync_words(bh);
   g_last_error[0] = '\0';
   return PIPER_OK;
 }

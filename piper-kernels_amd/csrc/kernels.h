@@ -26,6 +26,14 @@ __host__ __device__ inline int cascade_chunks(int length) {  // chunks of L^2 ro
   return static_cast<int>((length + rows - 1) / rows);
 }
 
+// Workspace of piper_prepare: the mean partials ([2][batch_heads][chunks + 1][D] floats), then
+// the single-pass prep's sync words (an arrival counter per batch-head tensor, a status word;
+// the rest is spare, padding to 16 bytes).
+inline long prep_partial_bytes(long batch_heads, int length, int head_dim) {
+  return 2 * batch_heads * (cascade_chunks(length) + 1) * head_dim * 4;
+}
+inline long prep_sync_words(long batch_heads) { return 4 * batch_heads + 4; }
+
 // One 64-key tile record is byte for byte the attention kernel's LDS stage, so it is copied
 // with direct global -> LDS loads in 1 KiB pieces: K codes [64][D] in rows of D + 16 bytes,
 // V^T codes [D][64] in rows of 80 bytes (the 16 spare bytes per row spread LDS banks), 64

@@ -311,31 +311,61 @@ __device__ __forceinline__ uint32_t insert_byte(uint32_t packed, uint32_t word) 
   return __builtin_amdgcn_perm(word, packed, kSel);
 }
 
+// Rows [16 sub, +16) of a 64-row K block or V tile (8 rows at D = 64), columns [8 group, +8):
+// lane (group, sub)'s share of the unit, every load in flight before any arithmetic.  Rows past
+// the end read as zero.
+template <int D, bool kGuard>
+__device__ __forceinline__ void load_unit_rows(const InputTensor& in, int b, int h, int kb, int length, int lane,
+                                               uint4 (&raw)[kKeyBlock / (kWave / (D / 8))]) {
+  constexpr int kGroups = D / 8;
+  constexpr int kKeys = kKeyBlock / (kWave / kGroups);
+  const int group = lane % kGroups;
+  const int key0 = (lane / kGroups) * kKeys;
+  const uint16_t* base =
+      static_cast<const uint16_t*>(in.data) + b * in.stride_batch + h * in.stride_head + group * 8;
+#pragma unroll
+  for (int j = 0; j < kKeys; ++j) {
+    const int row = kb * kKeyBlock + key0 + j;
+    raw[j] = !kGuard || row < length ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * in.stride_seq)
+                                     : make_uint4(0, 0, 0, 0);
+  }
+}
+
+template <bool kBf16, int D, bool kGuard>
+__device__ __forceinline__ void quantize_value_rows(const QuantParams& p, int unit, int lane,
+                                                    uint4 (&raw)[kKeyBlock / (kWave / (D / 8))],
+                                                    const float (&mu)[8]);
+
 template <bool kBf16, int D, bool kGuard>
 __device__ __forceinline__ void quantize_value_tile(const QuantParams& p, int unit, int lane) {
   constexpr int kGroups = D / 8;
-  constexpr int kSubs = kWave / kGroups;
-  constexpr int kKeys = kKeyBlock / kSubs;
   const int bh = unit / p.nkb;
   const int kb = unit - bh * p.nkb;
   const int b = bh / p.heads;
   const int h = bh - b * p.heads;
   const int group = lane % kGroups;
-  const int sub = lane / kGroups;
-  const int key0 = sub * kKeys;  // first key of this lane in the tile
-  const uint16_t* base = static_cast<const uint16_t*>(p.value.data) + b * p.value.stride_batch +
-                         h * p.value.stride_head + group * 8;
-  uint4 raw[kKeys];  // every row in flight before any arithmetic
-#pragma unroll
-  for (int j = 0; j < kKeys; ++j) {
-    const int row = kb * kKeyBlock + key0 + j;
-    raw[j] = !kGuard || row < p.key_length
-                 ? *reinterpret_cast<const uint4*>(base + static_cast<long>(row) * p.value.stride_seq)
-                 : make_uint4(0, 0, 0, 0);
-  }
+  uint4 raw[kKeyBlock / (kWave / kGroups)];
+  load_unit_rows<D, kGuard>(p.value, b, h, kb, p.key_length, lane, raw);
   float mu[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) mu[i] = p.center_value ? p.value_mean[static_cast<long>(bh) * D + group * 8 + i] : 0.0f;
+  quantize_value_rows<kBf16, D, kGuard>(p, unit, lane, raw, mu);
+}
+
+// The V tile `unit` from lane (group, sub)'s rows `raw` (load_unit_rows) centred by `mu` (its
+// eight columns' means, zeros when uncentred).
+template <bool kBf16, int D, bool kGuard>
+__device__ __forceinline__ void quantize_value_rows(const QuantParams& p, int unit, int lane,
+                                                    uint4 (&raw)[kKeyBlock / (kWave / (D / 8))],
+                                                    const float (&mu)[8]) {
+  constexpr int kGroups = D / 8;
+  constexpr int kSubs = kWave / kGroups;
+  constexpr int kKeys = kKeyBlock / kSubs;
+  const int bh = unit / p.nkb;
+  const int kb = unit - bh * p.nkb;
+  const int group = lane % kGroups;
+  const int sub = lane / kGroups;
+  const int key0 = sub * kKeys;  // first key of this lane in the tile
 
   uint8_t* tile = p.kv_tiles + static_cast<long>(unit) * kv_tile_bytes(D);
   int colsum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -466,6 +496,316 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) q
 }
 
 // ---------------------------------------------------------------------------------------
+// Single-pass prep (D = 128, cascade blocks of L = 16 rows, at most kSinglePassChunks chunks per
+// sequence): K and V are read from HBM once.  One workgroup per 256-row chunk of one batch-head's
+// K or V: wave w holds rows [64 w, +64) of the chunk (the chunk's K block or V tile 4 c + w) in
+// registers, lane (group, sub) the columns [8 group, +8) of rows [16 sub, +16) -- exactly one
+// cascade level-0 block, which it sums in row order.  The chunk's level-1 sums are published
+// (write-through stores) and counted on the batch-head tensor's arrival counter; the chunk that
+// arrives last computes the mean (levels 2 and 3, the torch order of the mean pass above) and
+// writes it over the pending marks the launch left in the mean buffer; the other chunks poll
+// their columns until the marks are gone.  Every chunk then quantises its rows from registers.
+// Causal V needs no mean and does not wait.
+//
+// Progress: a chunk waits only for chunks of its own batch-head tensor, whose workgroup ids are
+// consecutive; ids are remapped so that each XCD runs a consecutive range, and an XCD dispatches
+// its workgroups in order, so once the first chunk of a tensor runs, the rest are dispatched as
+// soon as slots free up -- and a tensor's kSinglePassChunks chunks fit in one XCD's slots (32 CUs
+// x 4 workgroups).  Every wait is bounded: past kSpinLimit polls it gives up, records a status
+// and quantises with a NaN mean, so the kernel always ends.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float load_coherent(const float* p) {  // agent-scope relaxed: bypasses L2
+  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ void store_coherent(float* p, float v) {  // agent-scope relaxed: written through
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// K block from registers (load_unit_rows at D = 128): centred by `mu`, per-thread-group scales
+// (group of row r: (r % 8) / 2, i.e. (j % 8) / 2 for this lane's row 16 sub + j) or one per
+// block, codes into the tile's K rows, scales to scale_out and to the padding of K row 0 --
+// the same values as quantize_block, which takes the rows in another lane order.
+template <bool kBf16, bool kGuard>
+__device__ __forceinline__ void quantize_key_rows(uint4 (&raw)[16], const float (&mu)[8], int valid_rows,
+                                                  int8_t* __restrict__ tile, float* __restrict__ scale_out,
+                                                  bool per_thread, int lane) {
+  constexpr int D = 128;
+  constexpr int kStride = kv_k_stride(D);
+  const int group = lane & 15;
+  const int sub = lane >> 4;
+  float am[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float f[8];
+    widen8<kBf16>(raw[j], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = !kGuard || j < valid_rows ? f[i] - mu[i] : 0.0f;
+      am[(j & 7) >> 1] = fmaxf(am[(j & 7) >> 1], fabsf(x));
+    }
+  }
+  float scale[4];
+  if (per_thread) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) scale[t] = scale_from_amax(wave_max(am[t]));
+  } else {
+    scale[0] = scale_from_amax(wave_max(fmaxf(fmaxf(am[0], am[1]), fmaxf(am[2], am[3]))));
+    scale[1] = scale[2] = scale[3] = scale[0];
+  }
+  const Divisor divisor[4] = {Divisor(scale[0]), Divisor(scale[1]), Divisor(scale[2]), Divisor(scale[3])};
+  // widen and centre again from the packed rows (as quantize_block: keeps 128 floats out of VGPRs)
+#pragma unroll
+  for (int j = 0; j < 16; ++j) asm volatile("" : "+v"(raw[j].x), "+v"(raw[j].y), "+v"(raw[j].z), "+v"(raw[j].w));
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float f[8];
+    widen8<kBf16>(raw[j], f);
+    uint32_t c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = !kGuard || j < valid_rows ? f[i] - mu[i] : 0.0f;
+      c[i] = code_word(x, divisor[(j & 7) >> 1]);
+    }
+    *reinterpret_cast<uint2*>(tile + (16 * sub + j) * kStride + 8 * group) =
+        make_uint2(pack_low_bytes(c[0], c[1], c[2], c[3]), pack_low_bytes(c[4], c[5], c[6], c[7]));
+  }
+  if (lane == 0) {
+    const float4 s4 = make_float4(scale[0], scale[1], scale[2], scale[3]);
+    *reinterpret_cast<float4*>(scale_out) = s4;
+    *reinterpret_cast<float4*>(tile + D) = s4;
+  }
+}
+
+struct SinglePassParams {
+  QuantParams q;
+  MeanParams m;
+  uint32_t* arrivals;  // [batch_heads][2] chunks arrived (zero before the launch)
+  uint32_t* status;    // nonzero: a wait gave up (zero before the launch)
+  int kv_workgroups;   // batch_heads * 2 * chunks; Q-block workgroups (4 blocks each) follow
+};
+
+constexpr int kSinglePassChunks = 64;
+constexpr int kSpinLimit = 1 << 20;  // polls (with s_sleep): about a second
+constexpr uint32_t kMeanPending = 0x7fa5a5a5u;  // a signalling NaN: the mean slot before it is published
+
+// The mean of one column from the published partials, torch's cascade order (finalize_column),
+// with two threads per column: thread `half` sums the level-2 groups [2 half, 2 half + 2) of L
+// chunks each (loads in flight together), the groups meet in LDS and thread 0 of the pair
+// combines them in order.
+__device__ __forceinline__ float single_pass_mean(const MeanParams& p, const float* src, int col, int half,
+                                                  float (*group_sums)[128]) {
+  constexpr int L = 16;
+  const int full = p.length / (L * L);  // complete chunks
+  const int groups = (full + L - 1) / L;  // level-2 groups (the last may be unfinished)
+#pragma unroll
+  for (int gg = 0; gg < 2; ++gg) {
+    const int g = 2 * half + gg;
+    if (g < groups) {
+      const int c0 = g * L;
+      const int n = min(L, full - c0);
+      float part[L];
+#pragma unroll
+      for (int i = 0; i < L; ++i) part[i] = i < n ? load_coherent(src + static_cast<long>(c0 + i) * 128) : 0.0f;
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < L; ++i)
+        if (i < n) s += part[i];
+      group_sums[g][col] = s;
+    }
+  }
+  __syncthreads();
+  if (half != 0) return 0.0f;
+  float level3 = 0.0f, level2 = 0.0f;
+  for (int g = 0; g < groups; ++g) {
+    if ((g + 1) * L <= full) level3 += group_sums[g][col];
+    else level2 = group_sums[g][col];
+  }
+  const float level1 = full < p.chunks ? load_coherent(src + static_cast<long>(full) * 128) : 0.0f;
+  const float level0 = load_coherent(src + static_cast<long>(p.chunks) * 128);
+  const float total = ((level0 + level1) + level2) + level3;
+  return total / static_cast<float>(p.length);
+}
+
+// LDS of a single-pass workgroup.
+struct SinglePassShared {
+  float block_sums[16][128];  // the chunk's level-0 sums
+  float group_sums[4][128];
+  float mean[128];
+  int last;
+};
+
+// One chunk of tensor kTensor (0: K, 1: V) of batch-head bh: load, cascade sums, mean, codes.
+// The whole pipeline is inlined once per tensor so that each keeps its 64 VGPRs of rows in
+// registers without the other's code in between; a unit that reaches past the end of the
+// sequence (at most one per batch-head) loads its rows again, guarded, inside its own branch.
+template <bool kBf16, int kTensor>
+__device__ __forceinline__ void single_pass_chunk(const SinglePassParams& p, SinglePassShared& sh, int bh, int chunk,
+                                                  int wave, int lane) {
+  constexpr int D = 128;
+  constexpr int L = 16;
+  const int chunks = p.m.chunks;
+  const int pair = 2 * bh + kTensor;
+  const int b = bh / p.q.heads;
+  const int h = bh - b * p.q.heads;
+  const int length = p.q.key_length;
+  const InputTensor& in = kTensor == 0 ? p.q.key : p.q.value;
+  const int kb = chunk * 4 + wave;  // this wave's K block / V tile
+  const int group = lane & 15;
+  const int sub = lane >> 4;
+  const int first_row = kb * kKeyBlock + sub * 16;  // this lane's rows [first_row, +16)
+  const int valid_rows = max(0, min(16, length - first_row));
+  const bool full_unit = (kb + 1) * kKeyBlock <= length;
+
+  uint4 raw[16];
+  if (full_unit) {
+    load_unit_rows<D, false>(in, b, h, kb, length, lane, raw);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) raw[j] = make_uint4(0, 0, 0, 0);
+  }
+
+  float* mean_out = (kTensor == 0 ? p.m.key_mean : p.m.value_mean) + static_cast<long>(bh) * D;
+  const bool centred = kTensor == 0 || p.q.center_value;
+  if (centred) {
+    // level 0: this lane's block of L rows, in row order from +0.0 (a partial unit reads its
+    // rows here with guards; they are read again for the codes)
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (full_unit) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float f[8];
+        widen8<kBf16>(raw[j], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += f[i];
+      }
+    } else if (valid_rows > 0) {
+      const uint16_t* rows = static_cast<const uint16_t*>(in.data) + b * in.stride_batch + h * in.stride_head +
+                             static_cast<long>(first_row) * in.stride_seq + 8 * group;
+      for (int j = 0; j < valid_rows; ++j) {
+        float f[8];
+        widen8<kBf16>(*reinterpret_cast<const uint4*>(rows + static_cast<long>(j) * in.stride_seq), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += f[i];
+      }
+    }
+    float4* dst = reinterpret_cast<float4*>(&sh.block_sums[4 * wave + sub][8 * group]);
+    dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    // the K codes widen the packed rows again: the 128 floats of this pass stay dead (the V
+    // tile's register reuse needs no such hint)
+    if constexpr (kTensor == 0) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) asm volatile("" : "+v"(raw[j].x), "+v"(raw[j].y), "+v"(raw[j].z), "+v"(raw[j].w));
+    }
+    __syncthreads();
+    // level 1: the chunk's complete blocks in order; a short last chunk's trailing rows go to
+    // slot `chunks` (mean_chunk's layout)
+    const int rows = min(L * L, length - chunk * L * L);
+    const int full = rows / L;
+    const int tail = rows - full * L;
+    float* src = p.m.partials + (static_cast<long>(pair) * (chunks + 1)) * D;
+    if (threadIdx.x < D) {
+      const int col = threadIdx.x;
+      float s = 0.0f;
+      for (int blk = 0; blk < full; ++blk) s += sh.block_sums[blk][col];
+      store_coherent(src + static_cast<long>(chunk) * D + col, s);
+      if (chunk == chunks - 1)
+        store_coherent(src + static_cast<long>(chunks) * D + col, tail > 0 ? sh.block_sums[full][col] : 0.0f);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the stores are complete before the arrival is counted
+    __syncthreads();
+    if (threadIdx.x == 0)
+      sh.last = __hip_atomic_fetch_add(p.arrivals + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                static_cast<uint32_t>(chunks - 1);
+    __syncthreads();
+    if (sh.last) {
+      const int col = threadIdx.x & (D - 1);
+      const float m = single_pass_mean(p.m, src + col, col, threadIdx.x >> 7, sh.group_sums);
+      if (threadIdx.x < D) {
+        sh.mean[col] = m;
+        store_coherent(mean_out + col, m);  // replaces the pending mark: the other chunks go on
+      }
+    } else if (threadIdx.x < D) {
+      // wait for this column's mean to replace the pending mark (kMeanPending, a signalling NaN
+      // that no arithmetic produces)
+      uint32_t bits;
+      int polls = 0;
+      while ((bits = __hip_atomic_load(reinterpret_cast<const uint32_t*>(mean_out) + threadIdx.x, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT)) == kMeanPending) {
+        if (++polls > kSpinLimit) {
+          __hip_atomic_store(p.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          bits = 0x7fc00000u;  // gave up: a NaN mean
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      sh.mean[threadIdx.x] = __builtin_bit_cast(float, bits);
+    }
+    __syncthreads();
+  } else if (chunk == 0 && threadIdx.x < D) {
+    mean_out[threadIdx.x] = 0.0f;  // causal: V is not centred, its mean slot reads zero
+  }
+  if (kb >= p.q.nkb) return;
+
+  float mu[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mu[i] = centred ? sh.mean[8 * group + i] : 0.0f;
+  const int unit = bh * p.q.nkb + kb;
+  if constexpr (kTensor == 0) {
+    int8_t* tile = reinterpret_cast<int8_t*>(p.q.kv_tiles) + static_cast<long>(unit) * kv_tile_bytes(D);
+    float* scales = p.q.key_scale + static_cast<long>(unit) * kKeyScaleSlots;
+    if (full_unit) {
+      quantize_key_rows<kBf16, false>(raw, mu, valid_rows, tile, scales, p.q.per_thread, lane);
+    } else {
+      uint4 rows[16];
+      load_unit_rows<D, true>(in, b, h, kb, length, lane, rows);
+      quantize_key_rows<kBf16, true>(rows, mu, valid_rows, tile, scales, p.q.per_thread, lane);
+    }
+  } else {
+    if (full_unit) {
+      quantize_value_rows<kBf16, D, false>(p.q, unit, lane, raw, mu);
+    } else {
+      uint4 rows[16];
+      load_unit_rows<D, true>(in, b, h, kb, length, lane, rows);
+      quantize_value_rows<kBf16, D, true>(p.q, unit, lane, rows, mu);
+    }
+  }
+}
+
+template <bool kBf16>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+prep_single_pass_kernel(const SinglePassParams p) {
+  __shared__ __attribute__((aligned(16))) SinglePassShared sh;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: index math stays scalar
+  const int lane = threadIdx.x & 63;
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  if (logical >= p.kv_workgroups) {  // the two-step path's Q blocks: no mean, no wait
+    const int unit = (logical - p.kv_workgroups) * 4 + wave;
+    if (unit < p.q.batch_heads * p.q.nqb) quantize_query_unit<kBf16, 128>(p.q, unit);
+    return;
+  }
+  const int pair = logical / p.m.chunks;  // (batch-head, tensor): K and V of a batch-head are neighbours
+  const int chunk = logical - pair * p.m.chunks;
+  if (pair & 1) single_pass_chunk<kBf16, 1>(p, sh, pair >> 1, chunk, wave, lane);
+  else single_pass_chunk<kBf16, 0>(p, sh, pair >> 1, chunk, wave, lane);
+}
+
+// Before the single-pass prep: arrival counters and status word cleared, the means marked
+// pending (the V mean only when V is centred).
+__global__ void __launch_bounds__(256) prep_clear_kernel(uint32_t* words, int count, float* key_mean, float* value_mean,
+                                                         int means, int centre_value) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < count) words[i] = 0u;
+  if (i < means) {
+    key_mean[i] = __builtin_bit_cast(float, kMeanPending);
+    if (centre_value) value_mean[i] = __builtin_bit_cast(float, kMeanPending);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // SageAttention2++ quantisation (sage_attention_2pp/reference.py:22-25, 44-49).  Each wave
 // owns a 64-row K block (the Piper K path, into the SageAttention2++ tile record) or a
 // 64-key V tile: FP8 E4M3 codes of v / scale[channel] (the correctly rounded FP32 quotient,
@@ -568,6 +908,28 @@ static hipError_t launch_mean_partials(const MeanParams& mp, hipStream_t stream)
 
 template <bool kBf16, int D>
 static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {
+  if (D == 128 && mp.block_rows == 16 && mp.chunks <= kSinglePassChunks && !mp.value_absmax) {
+    SinglePassParams sp{};
+    sp.q = qp;
+    sp.m = mp;
+    const int words = static_cast<int>(prep_sync_words(mp.batch_heads));
+    uint32_t* sync = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(mp.partials) +
+                                                 prep_partial_bytes(mp.batch_heads, mp.length, D));
+    sp.arrivals = sync;
+    sp.status = sync + 2 * mp.batch_heads;
+    sp.kv_workgroups = 2 * mp.batch_heads * mp.chunks;
+    // a fill kernel, not hipMemsetAsync: safe to record in a captured graph
+    const int means = mp.batch_heads * D;
+    const int threads = words > means ? words : means;
+    hipLaunchKernelGGL(prep_clear_kernel, dim3((threads + 255) / 256), dim3(256), 0, stream, sync, words, mp.key_mean,
+                       mp.value_mean, means, qp.center_value);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const long workgroups = static_cast<long>(sp.kv_workgroups) + qp.q_blocks_wg;
+    hipLaunchKernelGGL((prep_single_pass_kernel<kBf16>), dim3(static_cast<unsigned>(workgroups)), dim3(256), 0, stream,
+                       sp);
+    return hipGetLastError();
+  }
   hipError_t err = launch_mean_partials<kBf16, D>(mp, stream);
   if (err != hipSuccess) return err;
   const int fin_threads = 2 * mp.batch_heads * D;

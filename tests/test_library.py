@@ -78,6 +78,12 @@ def mean_workspace_bytes(batch_heads: int, key_length: int, head_dim: int) -> in
     return 2 * batch_heads * (chunks + 1) * head_dim * 4
 
 
+def prep_workspace_bytes(batch_heads: int, key_length: int, head_dim: int) -> int:
+    """piper_prepare's workspace: the mean partials, then the single-pass prep's arrival counter
+    and ready flag per batch-head tensor, a status word and padding (4 * B * H + 4 words)."""
+    return mean_workspace_bytes(batch_heads, key_length, head_dim) + 4 * (4 * batch_heads + 4)
+
+
 @pytest.mark.parametrize(
     "shape", [(1, 24, 16384, 16384, 128), (2, 3, 35, 67, 64), (1, 1, 1, 1, 64), (4, 32, 8192, 8192, 128)]
 )
@@ -98,7 +104,7 @@ def test_prepared_layout_sizes(lib, shape) -> None:
     assert layout.kv_tile_bytes == native.kv_tile_bytes(d) == -(-raw // 1024) * 1024
     assert layout.kv_tile_bytes % 1024 == 0 and layout.kv_tile_bytes - raw < 1024
     assert layout.kv_tiles_bytes == b * h * (sk64 // 64) * layout.kv_tile_bytes
-    assert layout.workspace_bytes == mean_workspace_bytes(b * h, sk, d)
+    assert layout.workspace_bytes == prep_workspace_bytes(b * h, sk, d)
 
 
 @pytest.mark.parametrize("bad", [(1, 1, 8, 8, 32), (0, 1, 8, 8, 64), (1, 1, 0, 8, 64)])
