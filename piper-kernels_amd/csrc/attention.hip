@@ -72,13 +72,16 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   }
   if constexpr (kCausal) {
     if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // block crosses this wave's diagonal
-      const int query = q0 + n;
-      const int key_base = t * kKeyBlock + 16 * h;
+      // Register r holds key t * 64 + 16 h + r' (r' = r or r + 16) for query q0 + n: masked when
+      // r' > lim.  The lane id is read here, inside the branch, so that nothing lane-dependent
+      // is kept live across the loop for it (a hoisted value spills at 168 VGPRs, and the
+      // reload's vmcnt wait would also drain the tile copies in flight).
+      int lane_id;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_id));
+      const int lim = q0 - t * kKeyBlock + (lane_id & 31) - 16 * (lane_id >> 5);
 #pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int key = key_base + (r < 16 ? r : 16 + r);
-        if (key > query) x[r] = -__builtin_inff();
-      }
+      for (int r = 0; r < 32; ++r)
+        if ((r < 16 ? r : 16 + r) > lim) x[r] = -__builtin_inff();
     }
   }
   const float mx = cross_half_max(max32(x));
