@@ -65,6 +65,12 @@ int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint3
  *   VALU_MIX    MIX without its MFMAs
  *   LDS         16 wave-wide ds_read_b128 (1 KiB each, distinct addresses) and a wait per round
  *   MFMA_FMA    2 x (1 MFMA + 16 FMA) per round in one wave
+ *   MIX_VGPR    MIX with the MFMA accumulators in VGPRs instead of AGPRs (only beside MIX_VGPR or
+ *               IDLE waves: it runs in a kernel of its own, status 2 otherwise)
+ *   CLUSTER     8 MFMAs back to back (two AGPR chains), then 8 x (16 FMA + 4 cvt_pk_u8 + 2 exp):
+ *               the attention loop's ratio with its MFMAs bunched as the score MFMAs are
+ *   ADD_LIT     32 v_add_f32 per round with a 32-bit literal operand, 16 chains
+ *   ADD_SGPR    32 v_add_f32 per round with an SGPR operand, 16 chains
  *
  * A wave's record: its hardware ids, role, slot, the ticks its loop took and the rounds it
  * completed (rounds / ticks is its rate while the other waves of its SIMD ran theirs).
@@ -78,7 +84,11 @@ int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint3
 #define PIPER_ISSUE_VALU_MIX 6
 #define PIPER_ISSUE_LDS 7
 #define PIPER_ISSUE_MFMA_FMA 8
-#define PIPER_ISSUE_ROLES 9
+#define PIPER_ISSUE_MIX_VGPR 9
+#define PIPER_ISSUE_CLUSTER 10
+#define PIPER_ISSUE_ADD_LIT 11
+#define PIPER_ISSUE_ADD_SGPR 12
+#define PIPER_ISSUE_ROLES 13
 #define PIPER_ISSUE_MAX_WAVES_PER_SIMD 4
 #define PIPER_ISSUE_RECORDS_PER_WORKGROUP 16
 

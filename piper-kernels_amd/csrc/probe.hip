@@ -176,10 +176,31 @@ __device__ __forceinline__ void mfma_agpr(v16i& acc, v4i a) {
   asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %1, %0" : "+a"(acc) : "v"(a));
 }
 
+__device__ __forceinline__ void mfma_vgpr(v16i& acc, v4i a) {
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %1, %0" : "+v"(acc) : "v"(a));
+}
+
+// 16 v_add_f32 (VOP2) on 16 chains whose other operand is a 32-bit literal or an SGPR.
+#define PIPER_ADD16(OPND)                                                                                         \
+  "v_add_f32_e32 %0, " OPND ", %0\n\tv_add_f32_e32 %1, " OPND ", %1\n\tv_add_f32_e32 %2, " OPND ", %2\n\t"       \
+  "v_add_f32_e32 %3, " OPND ", %3\n\tv_add_f32_e32 %4, " OPND ", %4\n\tv_add_f32_e32 %5, " OPND ", %5\n\t"       \
+  "v_add_f32_e32 %6, " OPND ", %6\n\tv_add_f32_e32 %7, " OPND ", %7\n\tv_add_f32_e32 %8, " OPND ", %8\n\t"       \
+  "v_add_f32_e32 %9, " OPND ", %9\n\tv_add_f32_e32 %10, " OPND ", %10\n\tv_add_f32_e32 %11, " OPND ", %11\n\t"   \
+  "v_add_f32_e32 %12, " OPND ", %12\n\tv_add_f32_e32 %13, " OPND ", %13\n\tv_add_f32_e32 %14, " OPND ", %14\n\t" \
+  "v_add_f32_e32 %15, " OPND ", %15\n\t"
+#define PIPER_F16_OUTS                                                                                             \
+  "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), "+v"(f[8]),     \
+      "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]), "+v"(f[15])
+
+__device__ __forceinline__ void add16_literal(float (&f)[16]) { asm volatile(PIPER_ADD16("0xcb400000") : PIPER_F16_OUTS); }
+
+__device__ __forceinline__ void add16_sgpr(float (&f)[16], float b) { asm volatile(PIPER_ADD16("%16") : PIPER_F16_OUTS : "s"(b)); }
+
 template <int R>
 __device__ __forceinline__ uint32_t issue_loop(uint64_t t0, uint64_t budget, const char* lds, uint32_t& rounds,
                                                uint64_t& t1) {
-  constexpr bool kMfma = R == PIPER_ISSUE_MFMA || R == PIPER_ISSUE_MIX || R == PIPER_ISSUE_MFMA_FMA;
+  constexpr bool kMfma = R == PIPER_ISSUE_MFMA || R == PIPER_ISSUE_MIX || R == PIPER_ISSUE_MFMA_FMA || R == PIPER_ISSUE_CLUSTER;
+  constexpr bool kMfmaVgpr = R == PIPER_ISSUE_MIX_VGPR;
   v4i a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
   asm volatile("" : "+v"(a));
   float one = 1.0f, add = 1.0f;
@@ -194,6 +215,9 @@ __device__ __forceinline__ uint32_t issue_loop(uint64_t t0, uint64_t budget, con
   }
   v16i acc0 = {}, acc1 = {};
   if constexpr (kMfma) asm volatile("" : "+a"(acc0), "+a"(acc1));
+  if constexpr (kMfmaVgpr) asm volatile("" : "+v"(acc0), "+v"(acc1));
+  float negb = -12582912.0f;  // the attention kernels' accumulator bias, in an SGPR
+  asm volatile("" : "+s"(negb));
   // LDS reads: lane l reads the 16 bytes at 16 l + 1024 (i % 8), inside the first 8 KiB
   const uint32_t lds_base = static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)lds)) + 16u * (threadIdx.x & 63);
@@ -235,13 +259,32 @@ __device__ __forceinline__ uint32_t issue_loop(uint64_t t0, uint64_t budget, con
         fma16(f, one, add);
         mfma_agpr(acc1, a);
         fma16(f, one, add);
+      } else if constexpr (R == PIPER_ISSUE_MIX_VGPR) {
+        mfma_vgpr(acc0, a);
+        mix22(f, w, e, one, add);
+        mfma_vgpr(acc1, a);
+        mix22(f, w, e, one, add);
+      } else if constexpr (R == PIPER_ISSUE_CLUSTER) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          mfma_agpr(acc0, a);
+          mfma_agpr(acc1, a);
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) mix22(f, w, e, one, add);
+      } else if constexpr (R == PIPER_ISSUE_ADD_LIT) {
+        add16_literal(f);
+        add16_literal(f);
+      } else if constexpr (R == PIPER_ISSUE_ADD_SGPR) {
+        add16_sgpr(f, negb);
+        add16_sgpr(f, negb);
       }
     }
     rounds += kInner;
     t1 = __builtin_amdgcn_s_memtime();
   } while (t1 - t0 < budget);
   uint32_t check = 0;
-  if constexpr (kMfma) {
+  if constexpr (kMfma || kMfmaVgpr) {
     v16i r0, r1;
     asm volatile("" : "=v"(r0) : "0"(acc0));
     asm volatile("" : "=v"(r1) : "0"(acc1));
@@ -261,6 +304,9 @@ struct IssueParams {
   int roles[PIPER_ISSUE_MAX_WAVES_PER_SIMD];
 };
 
+// kVgprOnly: the kernel runs MIX_VGPR waves only (its VGPR accumulators get a register
+// allocation of their own; beside the AGPR roles' state they would be shuffled through AGPRs).
+template <bool kVgprOnly>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 1024))) issue_probe_kernel(const IssueParams p) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   __shared__ uint32_t slots[4];  // waves of this workgroup that reached each SIMD's counter
@@ -277,7 +323,9 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 1024))) issue_pr
   const uint64_t t0 = __builtin_amdgcn_s_memtime();
   uint64_t t1 = t0;
   uint32_t rounds = 0, check = 0;
-  switch (role) {
+  if constexpr (kVgprOnly) {
+    if (role == PIPER_ISSUE_MIX_VGPR) check = issue_loop<PIPER_ISSUE_MIX_VGPR>(t0, p.budget, lds, rounds, t1);
+  } else switch (role) {
     case PIPER_ISSUE_MFMA: check = issue_loop<PIPER_ISSUE_MFMA>(t0, p.budget, lds, rounds, t1); break;
     case PIPER_ISSUE_FMA: check = issue_loop<PIPER_ISSUE_FMA>(t0, p.budget, lds, rounds, t1); break;
     case PIPER_ISSUE_EXP: check = issue_loop<PIPER_ISSUE_EXP>(t0, p.budget, lds, rounds, t1); break;
@@ -286,6 +334,9 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 1024))) issue_pr
     case PIPER_ISSUE_VALU_MIX: check = issue_loop<PIPER_ISSUE_VALU_MIX>(t0, p.budget, lds, rounds, t1); break;
     case PIPER_ISSUE_LDS: check = issue_loop<PIPER_ISSUE_LDS>(t0, p.budget, lds, rounds, t1); break;
     case PIPER_ISSUE_MFMA_FMA: check = issue_loop<PIPER_ISSUE_MFMA_FMA>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_CLUSTER: check = issue_loop<PIPER_ISSUE_CLUSTER>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_ADD_LIT: check = issue_loop<PIPER_ISSUE_ADD_LIT>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_ADD_SGPR: check = issue_loop<PIPER_ISSUE_ADD_SGPR>(t0, p.budget, lds, rounds, t1); break;
     default: break;
   }
   if ((threadIdx.x & 63) == 0) {
@@ -361,16 +412,25 @@ int piper_issue_probe(const piper_issue_probe_args* a, void* stream) {
   IssueParams p{};
   p.records = a->records;
   p.budget = static_cast<uint64_t>(a->cycle_budget);
+  int vgpr_roles = 0, other_roles = 0;
   for (int s = 0; s < PIPER_ISSUE_MAX_WAVES_PER_SIMD; ++s) {
     const int role = s < a->waves_per_simd ? a->roles[s] : PIPER_ISSUE_IDLE;
     if (role < 0 || role >= PIPER_ISSUE_ROLES) return fail(2, "unknown role %d in slot %d", role, s);
     p.roles[s] = role;
+    vgpr_roles += role == PIPER_ISSUE_MIX_VGPR;
+    other_roles += role != PIPER_ISSUE_MIX_VGPR && role != PIPER_ISSUE_IDLE;
   }
-  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(issue_probe_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kIssueLdsBytes);
+  if (vgpr_roles > 0 && other_roles > 0) return fail(2, "MIX_VGPR shares a SIMD only with MIX_VGPR or IDLE waves");
+  const void* kernel = vgpr_roles > 0 ? reinterpret_cast<const void*>(issue_probe_kernel<true>)
+                                      : reinterpret_cast<const void*>(issue_probe_kernel<false>);
+  hipError_t err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kIssueLdsBytes);
   if (err != hipSuccess) return fail(3, "hipFuncSetAttribute failed: %s", hipGetErrorString(err));
-  hipLaunchKernelGGL(issue_probe_kernel, dim3(static_cast<unsigned>(a->workgroups)), dim3(256 * a->waves_per_simd),
-                     kIssueLdsBytes, static_cast<hipStream_t>(stream), p);
+  if (vgpr_roles > 0)
+    hipLaunchKernelGGL(issue_probe_kernel<true>, dim3(static_cast<unsigned>(a->workgroups)),
+                       dim3(256 * a->waves_per_simd), kIssueLdsBytes, static_cast<hipStream_t>(stream), p);
+  else
+    hipLaunchKernelGGL(issue_probe_kernel<false>, dim3(static_cast<unsigned>(a->workgroups)),
+                       dim3(256 * a->waves_per_simd), kIssueLdsBytes, static_cast<hipStream_t>(stream), p);
   err = hipGetLastError();
   if (err != hipSuccess) return fail(3, "issue probe launch failed: %s", hipGetErrorString(err));
   g_last_error[0] = '\0';

@@ -342,7 +342,7 @@ MFMA_PROBE_THREADS = 512
 MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 
 # piper_issue_probe roles (PIPER_ISSUE_*)
-ISSUE_ROLES = ("idle", "mfma", "fma", "exp", "cvt", "mix", "valu_mix", "lds", "mfma_fma")
+ISSUE_ROLES = ("idle", "mfma", "fma", "exp", "cvt", "mix", "valu_mix", "lds", "mfma_fma", "mix_vgpr", "cluster", "add_lit", "add_sgpr")
 ISSUE_MAX_WAVES_PER_SIMD = 4
 ISSUE_RECORDS_PER_WORKGROUP = 16
 

@@ -258,6 +258,10 @@ ISSUE_ROUND = {
     "valu_mix": {"valu": 44},
     "lds": {"lds": 16},
     "mfma_fma": {"mfma": 2, "valu": 32},
+    "mix_vgpr": {"mfma": 2, "valu": 44},
+    "cluster": {"mfma": 8, "valu": 176},
+    "add_lit": {"valu": 32},
+    "add_sgpr": {"valu": 32},
 }
 
 
@@ -336,7 +340,13 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
       to the SIMD's time, against its ``mfma_ticks`` duration (0: fully overlapped, equal:
       serialised);
     * ``lds``: wave-wide ds_read_b128 throughput of a CU (four waves per SIMD reading) in bytes
-      per tick, and the attention mix with an LDS-reading wave beside it.
+      per tick, and the attention mix with an LDS-reading wave beside it;
+    * ``mfma_placement``: the attention mix's MFMA cost with VGPR instead of AGPR accumulators,
+      and with the MFMAs bunched eight at a time (per round 8 MFMAs then 176 VALU instructions)
+      instead of spread one per 22 VALU instructions;
+    * ``operand``: v_add_f32 ticks per instruction with a 32-bit literal and with an SGPR
+      operand, three waves per SIMD (an FP32 VALU instruction reading an SGPR issues at half
+      the rate).
     """
 
     def run(*roles: str) -> dict:
@@ -361,6 +371,11 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
     vmix3 = run("valu_mix", "valu_mix", "valu_mix")
     lds4 = run("lds", "lds", "lds", "lds")
     vmix_lds = run("valu_mix", "valu_mix", "valu_mix", "lds")
+    mixv3 = run("mix_vgpr", "mix_vgpr", "mix_vgpr")
+    cluster3 = run("cluster", "cluster", "cluster")
+    lit3 = run("add_lit", "add_lit", "add_lit")
+    sgpr3 = run("add_sgpr", "add_sgpr", "add_sgpr")
+    vmix_round = vmix3["valu_mix"]["ticks_per_round"]
     return {
         "ticks": "s_memtime",
         "cycle_budget": cycle_budget,
@@ -389,5 +404,14 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
         "lds": {
             "bytes_per_tick_per_cu": round(4 * 16 * 1024 / lds4["lds"]["ticks_per_round"], 1),
             "valu_mix_round_ticks_beside_lds_wave": vmix_lds["valu_mix"]["ticks_per_round"],
+        },
+        "mfma_placement": {
+            "agpr_spread_mfma_cost_ticks": round((mix3["mix"]["ticks_per_round"] - vmix_round) / 2, 2),
+            "vgpr_spread_mfma_cost_ticks": round((mixv3["mix_vgpr"]["ticks_per_round"] - vmix_round) / 2, 2),
+            "agpr_bunched_mfma_cost_ticks": round((cluster3["cluster"]["ticks_per_round"] - 4 * vmix_round) / 8, 2),
+        },
+        "operand": {
+            "add_literal_ticks": per_instr(lit3, "add_lit", "valu"),
+            "add_sgpr_ticks": per_instr(sgpr3, "add_sgpr", "valu"),
         },
     }

@@ -49,3 +49,6 @@ def test_issue_sharing_summary(gfx950_device) -> None:
     assert set(valu) == {"fma", "cvt", "exp"} and all(set(v) == {"1", "2", "3", "4"} for v in valu.values())
     assert valu["exp"]["4"] >= valu["fma"]["4"]  # exp is a quarter-rate instruction
     assert result["mfma_ticks"] >= 31.0 and result["lds"]["bytes_per_tick_per_cu"] > 0
+    placement = result["mfma_placement"]
+    assert all(0.0 < v < 2 * result["mfma_ticks"] for v in placement.values()), placement
+    assert result["operand"]["add_literal_ticks"] > 0 and result["operand"]["add_sgpr_ticks"] > 0

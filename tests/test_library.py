@@ -348,7 +348,8 @@ def test_probe_library_exports_exactly_its_header(probe) -> None:
 
 def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
     source = tmp_path / "probe.c"
-    roles = ["IDLE", "MFMA", "FMA", "EXP", "CVT", "MIX", "VALU_MIX", "LDS", "MFMA_FMA"]
+    roles = ["IDLE", "MFMA", "FMA", "EXP", "CVT", "MIX", "VALU_MIX", "LDS", "MFMA_FMA", "MIX_VGPR", "CLUSTER", "ADD_LIT",
+             "ADD_SGPR"]
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "piper_probe.h"', "int main(void) {",
              '  printf("%d %d %d %d %d %d %d %d\\n", PIPER_PROBE_ABI_VERSION, PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8,'
              ' PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8, PIPER_MFMA_PROBE_THREADS,'
@@ -368,10 +369,12 @@ def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
     assert values[:8] == [native.PROBE_ABI_VERSION, native.MFMA_PROBE_I8, native.MFMA_PROBE_F8,
                           native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8, native.MFMA_PROBE_THREADS,
                           native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8]]
-    assert values[8:17] == list(range(len(native.ISSUE_ROLES)))
+    n = len(roles)
+    assert values[8:8 + n] == list(range(len(native.ISSUE_ROLES)))
     assert [r.upper() for r in native.ISSUE_ROLES] == roles
-    assert values[17:20] == [len(native.ISSUE_ROLES), native.ISSUE_MAX_WAVES_PER_SIMD, native.ISSUE_RECORDS_PER_WORKGROUP]
-    offsets = values[20:]
+    assert values[8 + n:11 + n] == [len(native.ISSUE_ROLES), native.ISSUE_MAX_WAVES_PER_SIMD,
+                                    native.ISSUE_RECORDS_PER_WORKGROUP]
+    offsets = values[11 + n:]
     expected = []
     for cls in (native.PiperIssueRecord, native.PiperIssueProbeArgs):
         expected.append(ctypes.sizeof(cls))
@@ -415,6 +418,10 @@ def test_issue_probe_validates_before_launching(probe) -> None:
     args.records = 0x1000
     args.roles[1] = len(native.ISSUE_ROLES)
     with pytest.raises(RuntimeError, match="unknown role"):
+        probe.issue_probe(args, 0)
+    args.roles[0] = native.ISSUE_ROLES.index("mix_vgpr")  # runs in a kernel of its own
+    args.roles[1] = native.ISSUE_ROLES.index("fma")
+    with pytest.raises(RuntimeError, match="MIX_VGPR"):
         probe.issue_probe(args, 0)
 
 
