@@ -85,6 +85,12 @@ def parse_args() -> argparse.Namespace:
         default="piper_attention",
         help="the operator whose complete call is a step (default: Piper Attention, the headline)",
     )
+    parser.add_argument(
+        "--sage-accumulate",
+        choices=["fp32", "reference"],
+        default="fp32",
+        help="SageAttention2++ only: FP32 accumulation across blocks (default) or the reference's FP16 partials",
+    )
     return parser.parse_args()
 
 
@@ -336,8 +342,11 @@ def main() -> int:
     ops = attention_operations(b, h, sq, sk, d, workload.is_causal)
 
     if sage:
-        from piper_kernels.attention.sage_attention_2pp.hip import _launch_sage_attention_2pp as launch
+        from piper_kernels.attention.sage_attention_2pp.hip import _launch_sage_attention_2pp
         from piper_kernels.attention.sage_attention_2pp.hip import _prepare_sage_attention_2pp
+
+        def launch(prepared):
+            return _launch_sage_attention_2pp(prepared, accumulate=args.sage_accumulate)
 
         def prepare():
             return _prepare_sage_attention_2pp(q, k, v, scale, workload.is_causal)
@@ -420,6 +429,7 @@ def main() -> int:
         "config": {
             **workload.as_dict(),
             "operator": args.operator,
+            **({"sage_accumulate": args.sage_accumulate} if sage else {}),
             "step": (
                 "complete operator call: HIP prep of Q, K, V + fused attention kernel"
                 if args.two_step and not sage

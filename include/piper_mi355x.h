@@ -268,6 +268,12 @@ typedef struct piper_sage_prepare_args {
   int64_t workspace_bytes;
 } piper_sage_prepare_args;
 
+/* piper_sage_attention_args.flags: round each 64-key block's FP8 product to FP16 before it joins
+ * the FP32 accumulator -- the reference's arithmetic (sage_attention_2pp/reference.py:95-98, its
+ * model of an FP16-accumulating FP8 MMA); without it the products of every block accumulate in
+ * the MFMA's FP32 registers (faster and closer to exact). */
+#define PIPER_SAGE_FP16_PARTIALS 2
+
 typedef struct piper_sage_attention_args {
   int32_t abi_version;  /* PIPER_ABI_VERSION */
   int32_t dtype;        /* of query: PIPER_FLOAT16 or PIPER_BFLOAT16 */
@@ -276,7 +282,7 @@ typedef struct piper_sage_attention_args {
   int32_t plan;         /* OR of PIPER_PLAN_* bits (the same launch plans) */
   float scale;          /* softmax scale, finite and > 0 */
   int32_t flags;        /* PIPER_ATTENTION_QK_PER_THREAD after a per-thread-group K prep: the
-                           query is quantised per thread group as well */
+                           query is quantised per thread group as well; PIPER_SAGE_FP16_PARTIALS */
   int32_t reserved;     /* 0 */
   piper_shape shape;
   piper_tensor query;   /* [B, H, Sq, D], the layout rules of piper_prepare_args.query */

@@ -403,7 +403,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
   if (a->plan < 0 || a->plan > PIPER_PLAN_MASK || (a->plan & PIPER_PLAN_THREE_WORKGROUPS))
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
-  if ((a->flags & ~PIPER_ATTENTION_QK_PER_THREAD) != 0)
+  if ((a->flags & ~(PIPER_ATTENTION_QK_PER_THREAD | PIPER_SAGE_FP16_PARTIALS)) != 0)
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   if (int st = check_input("query", a->query)) return st;
   const piper_sage_prepared& o = a->prepared;
@@ -430,6 +430,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   sp.xcd_remap = (a->plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
   sp.causal_interleave = (a->plan & PIPER_PLAN_CAUSAL_INTERLEAVE) ? 1 : 0;
   sp.per_thread = (a->flags & PIPER_ATTENTION_QK_PER_THREAD) ? 1 : 0;
+  sp.fp16_partials = (a->flags & PIPER_SAGE_FP16_PARTIALS) ? 1 : 0;
   if (static_cast<int64_t>(sp.query_tiles) * sp.batch_heads > 0x7fffffff)
     return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
 

@@ -180,6 +180,7 @@ struct SageParams {
   int xcd_remap;
   int causal_interleave;
   int per_thread;  // Q/K scales per thread group (the tile's four K slots, per-row-group Q scales)
+  int fp16_partials;  // round each block's FP8 product to FP16 (the reference's arithmetic)
 };
 
 hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream);

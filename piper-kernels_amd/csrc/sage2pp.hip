@@ -9,11 +9,12 @@
 // + sum(exp2(s - m')), and the epilogue acc * scale_v / max(den, 1e-30).  Scores are in the
 // log2 domain (the softmax scale carries log2 e).
 //
-// The one arithmetic difference from the reference: its 64-key partial products are rounded
-// to FP16 (a model of NVIDIA's FP16-accumulating FP8 MMA, reference.py:95-98).  gfx950's FP8
-// MFMA accumulates in FP32, so the products of every block accumulate in the MFMA's own FP32
+// By default one arithmetic difference from the reference: its 64-key partial products are
+// rounded to FP16 (a model of NVIDIA's FP16-accumulating FP8 MMA, reference.py:95-98).  gfx950's
+// FP8 MFMA accumulates in FP32, so the products of every block accumulate in the MFMA's own FP32
 // registers, rescaled only when the running maximum moves, and the per-channel V scale is
-// applied once at the end.  This removes all per-block VALU work on the D outputs (the
+// applied once at the end.  The kFp16Partials instantiation (PIPER_SAGE_FP16_PARTIALS) keeps the
+// reference's rounding: each block's product is formed on its own, rounded to FP16 and added.  This removes all per-block VALU work on the D outputs (the
 // reference applies a scale per block): per block and lane, the VALU work is the 32 scores'
 // subtraction, max, FMA, exp2, sum and FP8 packing.
 //
@@ -112,7 +113,7 @@ __device__ __forceinline__ void sage_block_head(const v16i (&s)[2], const float 
   }
 }
 
-template <int D, int NW>
+template <int D, int NW, bool kFp16Partials>
 __device__ __forceinline__ void sage_block_tail(const char* stage, const float (&x)[32], const float (&ct)[4], int n,
                                                 int h, v16f (&acc)[D / 32], float& den, float mrun) {
   using L = SageLayout<D, NW>;
@@ -137,18 +138,27 @@ __device__ __forceinline__ void sage_block_tail(const char* stage, const float (
   const v8i p = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]), static_cast<int>(pw[3]),
                  static_cast<int>(pw[4]), static_cast<int>(pw[5]), static_cast<int>(pw[6]), static_cast<int>(pw[7])};
 
-  // ---- O^T += V^T P^T on the FP8 MFMA, accumulating in FP32 ----
+  // ---- O^T += V^T P^T on the FP8 MFMA, accumulating in FP32 (with kFp16Partials, the block's
+  // 64-key product is formed on its own and rounded to FP16 before it is added: the reference's
+  // partial.to(float16), reference.py:95-98; |partial| <= 64 * 448 * 2.25 < 65504) ----
 #pragma unroll
   for (int j = 0; j < kChunksD; ++j) {
     const char* vrow = stage + L::kVOffset + (32 * j + n) * L::kVStride + 16 * h;
     const v4i a0 = *reinterpret_cast<const v4i*>(vrow);
     const v4i a1 = *reinterpret_cast<const v4i*>(vrow + 32);
     const v8i a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-    acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, p, acc[j], 0, 0, 0, 0, 0, 0);
+    if constexpr (kFp16Partials) {
+      const v16f zero = {};
+      const v16f part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, p, zero, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][r] += static_cast<float>(static_cast<_Float16>(part[r]));
+    } else {
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, p, acc[j], 0, 0, 0, 0, 0, 0);
+    }
   }
 }
 
-template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
+template <int D, int NW, bool kCausal, bool kPerThread, bool kFp16Partials, bool kBarrier>
 __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                           int wave, int lane, const v4i (&qf)[D / 32], float cq, int q0, int n,
                                           int h, int krow, const v16i& bias, const v16i (&s_cur)[2],
@@ -177,12 +187,12 @@ __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t
     // but costs register copies and measured 3% slower)
     block_scores<D, L>(smem + ((t + 1) % R::kStages) * L::kStageBytes, qf, h, krow, bias, s_next);
     sage_block_head<D, kCausal, kPerThread>(s_cur, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
-    sage_block_tail<D, NW>(stage, x, ct, n, h, acc, den, mrun);
+    sage_block_tail<D, NW, kFp16Partials>(stage, x, ct, n, h, acc, den, mrun);
   }
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }
 
-template <int D, int NW, bool kCausal, int kOut, bool kPerThread>
+template <int D, int NW, bool kCausal, int kOut, bool kPerThread, bool kFp16Partials>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const SageParams p) {
   using L = SageLayout<D, NW>;
   using R = Ring<NW>;
@@ -249,14 +259,14 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const S
 
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
-    sage_step<D, NW, kCausal, kPerThread, R::kEveryIteration>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
-                                                           h, krow, bias, s_a, s_b, acc, den, mrun);
-    sage_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
-                                    s_b, s_a, acc, den, mrun);
+    sage_step<D, NW, kCausal, kPerThread, kFp16Partials, R::kEveryIteration>(
+        p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias, s_a, s_b, acc, den, mrun);
+    sage_step<D, NW, kCausal, kPerThread, kFp16Partials, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq,
+                                                               q0, n, h, krow, bias, s_b, s_a, acc, den, mrun);
   }
   if (t < tiles)
-    sage_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias,
-                                     s_a, s_b, acc, den, mrun);
+    sage_step<D, NW, kCausal, kPerThread, kFp16Partials, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0,
+                                                                n, h, krow, bias, s_a, s_b, acc, den, mrun);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may outlive the waves
 
   // ---- epilogue: acc * scale_v / max(den, 1e-30); lane (n, h) holds rows d = 32j + 8g + 4h + i ----
@@ -278,22 +288,34 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const S
   }
 }
 
-template <int D, int NW, bool kCausal, bool kPerThread>
+template <int D, int NW, bool kCausal, bool kPerThread, bool kFp16Partials>
 static hipError_t sage_launch_out(int out_dtype, const SageParams& sp, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(sp.query_tiles * sp.batch_heads));
   const dim3 block(NW * 64);
   switch (out_dtype) {
-    case 0: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 0, kPerThread>), grid, block, 0, stream, sp); break;
-    case 1: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 1, kPerThread>), grid, block, 0, stream, sp); break;
-    default: hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 2, kPerThread>), grid, block, 0, stream, sp); break;
+    case 0:
+      hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 0, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
+      break;
+    case 1:
+      hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 1, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
+      break;
+    default:
+      hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 2, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
+      break;
   }
   return hipGetLastError();
 }
 
+template <int D, int NW, bool kCausal, bool kPerThread>
+static hipError_t sage_launch_partials(int out_dtype, const SageParams& sp, hipStream_t stream) {
+  return sp.fp16_partials ? sage_launch_out<D, NW, kCausal, kPerThread, true>(out_dtype, sp, stream)
+                          : sage_launch_out<D, NW, kCausal, kPerThread, false>(out_dtype, sp, stream);
+}
+
 template <int D, int NW, bool kCausal>
 static hipError_t sage_launch_granularity(int out_dtype, const SageParams& sp, hipStream_t stream) {
-  return sp.per_thread ? sage_launch_out<D, NW, kCausal, true>(out_dtype, sp, stream)
-                       : sage_launch_out<D, NW, kCausal, false>(out_dtype, sp, stream);
+  return sp.per_thread ? sage_launch_partials<D, NW, kCausal, true>(out_dtype, sp, stream)
+                       : sage_launch_partials<D, NW, kCausal, false>(out_dtype, sp, stream);
 }
 
 template <int D, int NW>

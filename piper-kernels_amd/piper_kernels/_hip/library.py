@@ -45,6 +45,7 @@ STATIC_SCRATCH_BYTES = 16 << 20  # PIPER_STATIC_SCRATCH_BYTES: piper_prepare_sta
 PREPARE_SKIP_QUERY = 1  # piper_prepare_args.flags
 PREPARE_QK_PER_THREAD = 2
 ATTENTION_QK_PER_THREAD = 1  # piper_attention_args.flags / piper_attention_fused_args.flags
+SAGE_FP16_PARTIALS = 2  # piper_sage_attention_args.flags: FP16-rounded 64-key partial products
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64

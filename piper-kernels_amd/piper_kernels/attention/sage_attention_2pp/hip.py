@@ -137,10 +137,19 @@ def _prepare_sage_attention_2pp(
     return prepared
 
 
+ACCUMULATE_MODES = ("fp32", "reference")
+
+
 def _launch_sage_attention_2pp(
-    prepared: PreparedSageAttention2pp, *, output: torch.Tensor | None = None
+    prepared: PreparedSageAttention2pp, *, output: torch.Tensor | None = None, accumulate: str = "fp32"
 ) -> torch.Tensor:
-    """Run only the fused kernel (query quantisation in its prologue); ``output`` may be FP32."""
+    """Run only the fused kernel (query quantisation in its prologue); ``output`` may be FP32.
+
+    ``accumulate="fp32"`` accumulates every block's FP8 product in the MFMA's FP32 registers;
+    ``accumulate="reference"`` rounds each 64-key block's product to FP16 first, the reference's
+    arithmetic (``sage_attention_2pp/reference.py:95-98``)."""
+    if accumulate not in ACCUMULATE_MODES:
+        raise ValueError(f"accumulate must be one of {ACCUMULATE_MODES}, got {accumulate!r}")
     lib = native.load_library()
     batch, heads, sq, sk, d = prepared.shape
     out = prepared.output if output is None else output
@@ -154,7 +163,8 @@ def _launch_sage_attention_2pp(
         is_causal=int(prepared.is_causal),
         plan=prepared.plan.plan_id,
         scale=ctypes.c_float(prepared.scale).value,
-        flags=native.ATTENTION_QK_PER_THREAD if prepared.qk_granularity == "per_thread" else 0,
+        flags=(native.ATTENTION_QK_PER_THREAD if prepared.qk_granularity == "per_thread" else 0)
+        | (native.SAGE_FP16_PARTIALS if accumulate == "reference" else 0),
         reserved=0,
         shape=native.PiperShape(batch, heads, sq, sk, d),
         query=native.PiperTensor(query.data_ptr(), *query.stride()[:3]),
@@ -178,9 +188,10 @@ def _run_sage_attention_2pp(
     *,
     plan: MI355XPlan | None = None,
     qk_granularity: str = "per_thread",
+    accumulate: str = "fp32",
 ) -> torch.Tensor:
     prepared = _prepare_sage_attention_2pp(query, key, value, scale, is_causal, plan=plan, qk_granularity=qk_granularity)
-    return _launch_sage_attention_2pp(prepared)
+    return _launch_sage_attention_2pp(prepared, accumulate=accumulate)
 
 
 @torch.library.custom_op("piper_kernels::sage_attention_2pp", mutates_args=())

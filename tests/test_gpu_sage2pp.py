@@ -45,12 +45,12 @@ def _prepare(q, k, v, scale, causal, device, plan=None, qk_granularity="per_warp
     return prepared
 
 
-def _launch(prepared, dtype=torch.float32) -> torch.Tensor:
+def _launch(prepared, dtype=torch.float32, accumulate="fp32") -> torch.Tensor:
     from piper_kernels.attention.sage_attention_2pp.hip import _launch_sage_attention_2pp
 
     b, h, sq, _, d = prepared.shape
     out = torch.empty((b, h, sq, d), device=prepared.output.device, dtype=dtype)
-    _launch_sage_attention_2pp(prepared, output=out)
+    _launch_sage_attention_2pp(prepared, output=out, accumulate=accumulate)
     torch.cuda.synchronize(out.device)
     return out
 
@@ -133,6 +133,33 @@ def test_output_against_oracle(gfx950_device, case) -> None:
     assert np.abs(actual - reference).mean() <= np.abs(fp32 - reference).mean() + MEAN_ABS
     # 16-bit outputs are the RNE rounding of the FP32 result
     out16 = _launch(prepared, dtype)
+    assert torch.equal(out16.cpu(), torch.from_numpy(actual).to(dtype))
+
+
+@pytest.mark.parametrize("case", SHAPES, ids=_id)
+def test_fp16_partials_match_the_reference_mode(gfx950_device, case) -> None:
+    """accumulate="reference" (PIPER_SAGE_FP16_PARTIALS) rounds each 64-key block's FP8 product to
+    FP16 as the reference does (reference.py:95-98): against the oracle's reference mode it meets
+    the gates the FP32 mode meets against the FP32 oracle, and it is nearer the reference mode than
+    the FP32-accumulation oracle is wherever the two modes differ measurably."""
+    shape, dtype, causal = case
+    log(f"[sage fp16 partials] {shape} {dtype} causal={causal}")
+    d = shape[-1]
+    q, k, v = _inputs(shape, dtype, seed=86)
+    prepared = _prepare(q, k, v, d**-0.5, causal, gfx950_device)
+    actual = _launch(prepared, accumulate="reference").cpu().numpy()
+    prep = oracle.prepare(q, k, v)
+    reference = oracle.attention_from_prepared(prep, d**-0.5, causal)
+    fp32 = oracle.attention_from_prepared(prep, d**-0.5, causal, accumulate="fp32")
+    err = np.abs(actual - reference)
+    modes = np.abs(fp32 - reference).mean()
+    log(f"   vs reference mode: mean {err.mean():.2e} max {err.max():.2e} cos {_cosine(actual, reference):.7f}; "
+        f"distance between the oracle's modes: mean {modes:.2e}")
+    assert np.isfinite(actual).all()
+    assert err.mean() <= MEAN_ABS and err.max() <= MAX_ABS and _cosine(actual, reference) >= COSINE
+    if modes > 1e-5:
+        assert err.mean() < modes
+    out16 = _launch(prepared, dtype, accumulate="reference")
     assert torch.equal(out16.cpu(), torch.from_numpy(actual).to(dtype))
 
 

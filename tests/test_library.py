@@ -307,10 +307,10 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     args.plan = 32
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.sage_attention_forward(args, 0)
-    args.plan, args.flags = 0, 2
+    args.plan, args.flags = 0, 4
     with pytest.raises(RuntimeError, match="unknown flags"):
         lib.sage_attention_forward(args, 0)
-    args.flags = native.ATTENTION_QK_PER_THREAD
+    args.flags = native.ATTENTION_QK_PER_THREAD | native.SAGE_FP16_PARTIALS  # both known
     with pytest.raises(RuntimeError, match="output pointer is NULL"):
         lib.sage_attention_forward(args, 0)
     args.is_causal = 1

@@ -166,9 +166,13 @@ def test_every_native_call_runs_under_the_input_device_guard(monkeypatch) -> Non
     q, k, v = _inputs()
     hip._run_sage_attention_2pp(q, k, v, q.shape[-1] ** -0.5, False)
     hip._run_sage_attention_2pp(q, k, v, q.shape[-1] ** -0.5, True, qk_granularity="per_warp")
-    assert [c[0] for c in calls] == ["sage_prepare", "sage_attention_forward"] * 2
+    hip._run_sage_attention_2pp(q, k, v, q.shape[-1] ** -0.5, False, accumulate="reference")
+    assert [c[0] for c in calls] == ["sage_prepare", "sage_attention_forward"] * 3
     assert all(c[1] == [q.device] and c[2] == 0x5EED for c in calls)
     assert set(streams) == {q.device}
     assert calls[0][3] == native.PREPARE_QK_PER_THREAD  # the sage prep never quantises Q
     assert calls[1][3] == native.ATTENTION_QK_PER_THREAD
     assert calls[2][3] == 0 and calls[3][3] == 0
+    assert calls[5][3] == native.ATTENTION_QK_PER_THREAD | native.SAGE_FP16_PARTIALS  # the reference's FP16 partials
+    with pytest.raises(ValueError, match="accumulate"):
+        hip._run_sage_attention_2pp(q, k, v, q.shape[-1] ** -0.5, False, accumulate="fp16")
