@@ -61,14 +61,14 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
     const float4 la = lk4[4 * h + q];
     const float4 lb = lk4[8 + 4 * h + q];
     const float c01 = ct[2 * (q & 1)], c23 = ct[2 * (q & 1) + 1];
-    x[4 * q + 0] = fmaf(unbias(s[0][4 * q + 0]), c01, la.x);
-    x[4 * q + 1] = fmaf(unbias(s[0][4 * q + 1]), c01, la.y);
-    x[4 * q + 2] = fmaf(unbias(s[0][4 * q + 2]), c23, la.z);
-    x[4 * q + 3] = fmaf(unbias(s[0][4 * q + 3]), c23, la.w);
-    x[16 + 4 * q + 0] = fmaf(unbias(s[1][4 * q + 0]), c01, lb.x);
-    x[16 + 4 * q + 1] = fmaf(unbias(s[1][4 * q + 1]), c01, lb.y);
-    x[16 + 4 * q + 2] = fmaf(unbias(s[1][4 * q + 2]), c23, lb.z);
-    x[16 + 4 * q + 3] = fmaf(unbias(s[1][4 * q + 3]), c23, lb.w);
+    x[4 * q + 0] = fmaf(unbias_score(s[0][4 * q + 0]), c01, la.x);
+    x[4 * q + 1] = fmaf(unbias_score(s[0][4 * q + 1]), c01, la.y);
+    x[4 * q + 2] = fmaf(unbias_score(s[0][4 * q + 2]), c23, la.z);
+    x[4 * q + 3] = fmaf(unbias_score(s[0][4 * q + 3]), c23, la.w);
+    x[16 + 4 * q + 0] = fmaf(unbias_score(s[1][4 * q + 0]), c01, lb.x);
+    x[16 + 4 * q + 1] = fmaf(unbias_score(s[1][4 * q + 1]), c01, lb.y);
+    x[16 + 4 * q + 2] = fmaf(unbias_score(s[1][4 * q + 2]), c23, lb.z);
+    x[16 + 4 * q + 3] = fmaf(unbias_score(s[1][4 * q + 3]), c23, lb.w);
   }
   if constexpr (kCausal) {
     if (t * kKeyBlock + kKeyBlock - 1 > q0) {  // block crosses this wave's diagonal
@@ -161,7 +161,7 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
 template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                               int wave, int lane, const v4i (&qf)[D / 32], float cq,
-                                              int q0, int n, int h, int krow, const v16i& bias,
+                                              int q0, int n, int h, int krow,
                                               const v16i (&s_cur)[2], v16i (&s_next)[2], float (&num)[D / 32][16],
                                               float& den, float& mref) {
   using L = TileLayout<D, NW>;
@@ -171,7 +171,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
   copy_block<L>(p, smem + ((t + R::kLead) % R::kStages) * L::kStageBytes, bh, min(t + R::kLead, tiles - 1), wave,
                 lane);
   if (t < wave_tiles) {
-    block_scores<D, L>(smem + ((t + 1) % R::kStages) * L::kStageBytes, qf, h, krow, bias, s_next);  // unused past the end
+    block_scores<D, L>(smem + ((t + 1) % R::kStages) * L::kStageBytes, qf, h, krow, s_next);  // unused past the end
     const char* stage = smem + (t % R::kStages) * L::kStageBytes;
     // the K scales of the tile's four thread groups sit in the padding of K row 0
     float ct[4];
@@ -230,7 +230,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
     for (int c = 0; c < kChunksD; ++c) qf[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
     // the scale of this lane's query row: slot n % 8 of its block (every slot, per block)
     cq = p.query_scale[(static_cast<long>(bh) * p.nqb + (q0 >> 5)) * kQueryScaleSlots + (kPerThread ? (n & 7) : 0)] *
-         p.scale_log2e;
+         (p.scale_log2e * kScoreUnit);
     // Settle the prepared Q loads inside this branch: a load the compiler still counts as
     // pending at the loop header would get its wait (in-order vmcnt, so a wait for all direct
     // LDS copies in flight) inside every iteration, and a wait at the join would also drain
@@ -256,7 +256,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLead * (L::kRounds - 1)) : "memory");
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
-    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * p.scale_log2e;
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * (p.scale_log2e * kScoreUnit);
   }
 
   float num[kChunksD][16];
@@ -273,25 +273,21 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
 
   stage_barrier<0>();  // all prologue copies landed
 
-  // QK accumulator bias, kept in registers for the whole loop (opaque, so not rematerialised)
-  v16i bias = {kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias,
-               kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias};
-  asm volatile("" : "+v"(bias));
   v16i s_a[2], s_b[2];  // scores of the current and the next block, alternating
-  if (wave_tiles > 0) block_scores<D, L>(smem, qf, h, krow, bias, s_a);
+  if (wave_tiles > 0) block_scores<D, L>(smem, qf, h, krow, s_a);
 
   // unrolled by two so both score sets keep static names; one barrier per pair (8 waves) or
   // per iteration (4 waves)
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
     pipeline_step<D, NW, kCausal, kPerThread, R::kEveryIteration>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq,
-                                                               q0, n, h, krow, bias, s_a, s_b, num, den, mref);
+                                                               q0, n, h, krow, s_a, s_b, num, den, mref);
     pipeline_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
-                                        h, krow, bias, s_b, s_a, num, den, mref);
+                                        h, krow, s_b, s_a, num, den, mref);
   }
   if (t < tiles)
     pipeline_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
-                                         krow, bias, s_a, s_b, num, den, mref);
+                                         krow, s_a, s_b, num, den, mref);
   // no direct copy may still be writing this workgroup's LDS when its waves end
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -361,7 +357,7 @@ attention_w3_kernel(const AttnParams p) {
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) qf[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
     cq = p.query_scale[(static_cast<long>(bh) * p.nqb + (q0 >> 5)) * kQueryScaleSlots + (kPerThread ? (n & 7) : 0)] *
-         p.scale_log2e;
+         (p.scale_log2e * kScoreUnit);
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) asm volatile("" ::"v"(qf[c]));
     asm volatile("" ::"v"(cq));
@@ -379,7 +375,7 @@ attention_w3_kernel(const AttnParams p) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds - 1) : "memory");
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
-    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * p.scale_log2e;
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * (p.scale_log2e * kScoreUnit);
   }
 
   float num[kChunksD][16];
@@ -390,9 +386,6 @@ attention_w3_kernel(const AttnParams p) {
   float den = 0.0f;
   float mref = -__builtin_inff();
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
-  v16i bias = {kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias,
-               kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias};
-  asm volatile("" : "+v"(bias));
 
   for (int t = 0; t < tiles; ++t) {
     // this wave's copies of tile t landed; after the barrier every wave's have, and every read
@@ -402,7 +395,7 @@ attention_w3_kernel(const AttnParams p) {
     if (t < wave_tiles) {
       const char* stage = smem + (t & 1) * L::kStageBytes;
       v16i sc[2];
-      block_scores<D, L>(stage, qf, h, krow, bias, sc);
+      block_scores<D, L>(stage, qf, h, krow, sc);
       float ct[4];
       if constexpr (kPerThread) {
         const float4 ks = *reinterpret_cast<const float4*>(stage + D);

@@ -58,8 +58,8 @@ __device__ __forceinline__ void sage_block_head(const v16i (&s)[2], const float 
   constexpr int kChunksD = D / 32;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    x[r] = unbias(s[0][r]);
-    x[16 + r] = unbias(s[1][r]);
+    x[r] = unbias_score(s[0][r]);
+    x[16 + r] = unbias_score(s[1][r]);
   }
   // Both masks are scalar branches taken by one tile (and the diagonal tiles); the empty asm
   // keeps the compiler from speculating them into per-element compares in every block.
@@ -161,7 +161,7 @@ __device__ __forceinline__ void sage_block_tail(const char* stage, const float (
 template <int D, int NW, bool kCausal, bool kPerThread, bool kFp16Partials, bool kBarrier>
 __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                           int wave, int lane, const v4i (&qf)[D / 32], float cq, int q0, int n,
-                                          int h, int krow, const v16i& bias, const v16i (&s_cur)[2],
+                                          int h, int krow, const v16i (&s_cur)[2],
                                           v16i (&s_next)[2], v16f (&acc)[D / 32], float& den, float& mrun) {
   using L = SageLayout<D, NW>;
   using R = Ring<NW>;  // the Piper Attention kernel's ring (stream.h)
@@ -185,7 +185,7 @@ __device__ __forceinline__ void sage_step(const SageParams& p, char* smem, int t
     // the frame move, or interleaving them with the softmax, measured 1-5% slower; feeding the
     // biased accumulator bits to the exp FMA with a folded constant saves the 32 subtractions
     // but costs register copies and measured 3% slower)
-    block_scores<D, L>(smem + ((t + 1) % R::kStages) * L::kStageBytes, qf, h, krow, bias, s_next);
+    block_scores<D, L>(smem + ((t + 1) % R::kStages) * L::kStageBytes, qf, h, krow, s_next);
     sage_block_head<D, kCausal, kPerThread>(s_cur, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
     sage_block_tail<D, NW, kFp16Partials>(stage, x, ct, n, h, acc, den, mrun);
   }
@@ -234,7 +234,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const S
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kSageLead * (L::kRounds - 1)) : "memory");
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
-    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * p.scale_log2e;
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * (p.scale_log2e * kScoreUnit);
   } else {
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
@@ -251,22 +251,19 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const S
 
   stage_barrier<0>();  // all prologue copies landed
 
-  v16i bias = {kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias,
-               kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias, kAccBias};
-  asm volatile("" : "+v"(bias));
   v16i s_a[2], s_b[2];
-  if (wave_tiles > 0) block_scores<D, L>(smem, qf, h, krow, bias, s_a);
+  if (wave_tiles > 0) block_scores<D, L>(smem, qf, h, krow, s_a);
 
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
     sage_step<D, NW, kCausal, kPerThread, kFp16Partials, R::kEveryIteration>(
-        p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, bias, s_a, s_b, acc, den, mrun);
+        p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, s_a, s_b, acc, den, mrun);
     sage_step<D, NW, kCausal, kPerThread, kFp16Partials, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq,
-                                                               q0, n, h, krow, bias, s_b, s_a, acc, den, mrun);
+                                                               q0, n, h, krow, s_b, s_a, acc, den, mrun);
   }
   if (t < tiles)
     sage_step<D, NW, kCausal, kPerThread, kFp16Partials, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0,
-                                                                n, h, krow, bias, s_a, s_b, acc, den, mrun);
+                                                                n, h, krow, s_a, s_b, acc, den, mrun);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may outlive the waves
 
   // ---- epilogue: acc * scale_v / max(den, 1e-30); lane (n, h) holds rows d = 32j + 8g + 4h + i ----

@@ -174,6 +174,22 @@ __device__ __forceinline__ void store4(void* out, long index, float a, float b, 
 // subscript reads element 0.)
 __device__ __forceinline__ float unbias(int bits) { return __builtin_bit_cast(float, bits) - kAccBiasValue; }
 
+// Score accumulators start from the bit pattern of 1/(2 pi), which the MFMA takes as an inline
+// constant accumulator operand (no registers hold it).  Its mantissa field 0x22F983 = 2292099
+// exceeds |Q K^T| <= 128 * 127^2 = 2064512, so every result's bits stay in the binade
+// [2^-3, 2^-2), where they read as 1/(2 pi) + score * 2^-26 exactly; subtracting 1/(2 pi) is
+// exact (the two are within a factor of 2) and leaves score * 2^-26.  The kernels' score
+// multipliers carry the compensating 2^26 (kScoreUnit), so score * 2^-26 * (c * 2^26) is the
+// same exact product as score * c: every logit is bit-identical to one from an unbiased score
+// (for multipliers c below 2^101, where c * 2^26 stays finite).
+constexpr int kScoreBias = 0x3E22F983;
+constexpr float kScoreUnit = 67108864.0f;  // 2^26
+static_assert(128 * 127 * 127 < (kScoreBias & 0x7fffff), "a score must not leave the bias's binade");
+
+__device__ __forceinline__ float unbias_score(int bits) {
+  return __builtin_bit_cast(float, bits) - __builtin_bit_cast(float, kScoreBias);
+}
+
 // A 16-byte global load the compiler does not track: the caller waits for it with an explicit
 // s_waitcnt, which lets later direct LDS copies stay in flight.  (A tracked load would get a
 // compiler wait that also drains every copy issued after it: vmcnt completes in order.)
@@ -254,10 +270,13 @@ __device__ __forceinline__ float quantize_query_block(const Params& p, int q0, i
 // lane: its query column, keys 16h + r after the K-row permutation).
 template <int D, class L>
 __device__ __forceinline__ void block_scores(const char* stage, const v4i (&qf)[D / 32], int h, int krow,
-                                             const v16i& bias, v16i (&s)[2]) {
-  // accumulators start from the bias: |K Q^T| <= D * 128 * 128 < 2^22, so each result reads as
-  // FP32 1.5 * 2^23 + score exactly
-  s[0] = s[1] = bias;
+                                             v16i (&s)[2]) {
+  // accumulators start from kScoreBias (an inline constant): each result reads as FP32
+  // 1/(2 pi) + score * 2^-26 exactly (unbias_score)
+  constexpr v16i kInit = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
+                          kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
+                          kScoreBias, kScoreBias};
+  s[0] = s[1] = kInit;
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
     const char* kb = stage + 32 * c + 16 * h;
