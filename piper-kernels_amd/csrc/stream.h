@@ -266,24 +266,37 @@ __device__ __forceinline__ float quantize_query_block(const Params& p, int q0, i
   return scale;
 }
 
+// First MFMA of a score chain, its accumulator operand the inline constant 1/(2 pi)
+// (kScoreBias).  Written as assembly because the compiler does not fold a constant that more
+// than one MFMA uses: it keeps the splat in 16 SGPRs and copies them to VGPRs in every block.
+// The result feeds only the next MFMA of its chain, as that MFMA's full accumulator operand,
+// which the hardware interlocks; the leading s_nop covers a VALU write of a source operand.
+__device__ __forceinline__ v16i score_mfma_first(v4i a, v4i b) {
+  static_assert(kScoreBias == 0x3E22F983, "0.15915494 is the inline constant 1/(2 pi)");
+  v16i r;
+  asm("s_nop 1\n\tv_mfma_i32_32x32x32_i8 %0, %1, %2, 0.15915494" : "=&v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // Integer scores S^T = K Q^T of one 64-key block: s[0] keys 0..31, s[1] keys 32..63 (each
 // lane: its query column, keys 16h + r after the K-row permutation).
 template <int D, class L>
 __device__ __forceinline__ void block_scores(const char* stage, const v4i (&qf)[D / 32], int h, int krow,
                                              v16i (&s)[2]) {
-  // accumulators start from kScoreBias (an inline constant): each result reads as FP32
-  // 1/(2 pi) + score * 2^-26 exactly (unbias_score)
-  constexpr v16i kInit = {kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
-                          kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias, kScoreBias,
-                          kScoreBias, kScoreBias};
-  s[0] = s[1] = kInit;
+  // accumulators start from kScoreBias: each result reads as FP32 1/(2 pi) + score * 2^-26
+  // exactly (unbias_score)
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
     const char* kb = stage + 32 * c + 16 * h;
     const v4i a0 = *reinterpret_cast<const v4i*>(kb + krow * L::kKStride);
     const v4i a1 = *reinterpret_cast<const v4i*>(kb + (32 + krow) * L::kKStride);
-    s[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qf[c], s[0], 0, 0, 0);
-    s[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qf[c], s[1], 0, 0, 0);
+    if (c == 0) {
+      s[0] = score_mfma_first(a0, qf[c]);
+      s[1] = score_mfma_first(a1, qf[c]);
+    } else {
+      s[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qf[c], s[0], 0, 0, 0);
+      s[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qf[c], s[1], 0, 0, 0);
+    }
   }
 }
 
