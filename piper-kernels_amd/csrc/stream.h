@@ -84,13 +84,14 @@ __device__ __forceinline__ TileCoord workgroup_tile(const Params& p) {
   return {bh, kCausal && !p.causal_forward ? qt - 1 - qtile : qtile};
 }
 
-// One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from its global address to
-// LDS byte lds + 16 * i.  Issued as inline assembly so that the compiler's wait insertion does
-// not treat every later LDS read as dependent on it: the waits are explicit (stage_barrier,
-// and a drain before the waves end).
-__device__ __forceinline__ void copy_piece(const void* src, uint32_t lds) {
+// One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from src + off (src
+// wave-uniform, held in SGPRs; off the lane's 32-bit offset) to LDS byte lds + 16 * i.  The
+// scalar-base form keeps the per-piece address arithmetic on the scalar unit.  Issued as inline
+// assembly so that the compiler's wait insertion does not treat every later LDS read as
+// dependent on it: the waits are explicit (stage_barrier, and a drain before the waves end).
+__device__ __forceinline__ void copy_piece(const char* src, uint32_t off, uint32_t lds) {
   // s_nop: one wait state between the SALU write of M0 and the LDS DMA that reads it
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(src), "{m0}"(lds) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_address(const char* p) {
@@ -108,7 +109,7 @@ __device__ __forceinline__ void copy_block(const Params& p, char* stage, int bh,
 #pragma unroll
   for (int r = 0; r < L::kRounds; ++r) {
     const int piece = wave + r * NW;  // wave-uniform: a scalar branch
-    if (piece < L::kPieces) copy_piece(tile + piece * 1024 + lane * 16, base + piece * 1024);
+    if (piece < L::kPieces) copy_piece(tile + piece * 1024, lane * 16, base + piece * 1024);
   }
 }
 
