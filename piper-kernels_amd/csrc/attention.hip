@@ -390,6 +390,7 @@ attention_w3_kernel(const AttnParams p) {
   for (int t = 0; t < tiles; ++t) {
     // this wave's copies of tile t landed; after the barrier every wave's have, and every read
     // of tile t - 1 (stage (t + 1) % 2) is done
+    if constexpr (!kCausal) progress_priority(t, 1, tiles);  // causal: workgroups differ in length
     stage_barrier<0>();
     if (t + 1 < tiles) copy_block<L>(p, smem + ((t + 1) & 1) * L::kStageBytes, bh, t + 1, wave, lane);
     if (t < wave_tiles) {

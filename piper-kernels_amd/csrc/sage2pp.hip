@@ -256,6 +256,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const S
 
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
+    if constexpr (!kCausal) progress_priority(t, 2, tiles);  // causal: workgroups differ in length
     sage_step<D, NW, kCausal, kPerThread, kFp16Partials, R::kEveryIteration>(
         p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h, krow, s_a, s_b, acc, den, mrun);
     sage_step<D, NW, kCausal, kPerThread, kFp16Partials, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq,

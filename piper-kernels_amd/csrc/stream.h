@@ -129,6 +129,20 @@ __device__ __forceinline__ void stage_barrier_keep_last(int wave) {
     stage_barrier<L::kRounds - 1>();
 }
 
+// Wave priority by the workgroup's progress through its tiles: 3 in the first quarter, then 2, 1
+// and 0 in the last, each set at the iteration [t, t + step) that reaches its quarter mark.  The
+// SIMD arbiter otherwise favours the oldest wave, so the workgroups sharing a CU drift apart and,
+// at the end of the grid, slots idle while the youngest workgroups finish alone.  For grids of
+// equal-length workgroups (non-causal); the level is the wave's issue priority (s_setprio), not a
+// stream priority.
+__device__ __forceinline__ void progress_priority(int t, int step, int tiles) {
+  const int q1 = tiles / 4, q2 = tiles / 2, q3 = (3 * tiles) / 4;
+  if (t == 0) __builtin_amdgcn_s_setprio(3);
+  if (t <= q1 && q1 < t + step) __builtin_amdgcn_s_setprio(2);
+  if (t <= q2 && q2 < t + step) __builtin_amdgcn_s_setprio(1);
+  if (t <= q3 && q3 < t + step) __builtin_amdgcn_s_setprio(0);
+}
+
 // Balanced max over 32 values (depth 4 instead of a 16-long v_max3 chain).
 __device__ __forceinline__ float max32(const float (&x)[32]) {
   float t[11];
