@@ -186,7 +186,7 @@ typedef struct piper_prepare_args {
                                           across the heads of each XCD (across all heads with
                                           PIPER_PLAN_NO_XCD_REMAP) instead of head by head */
 #define PIPER_PLAN_THREE_WORKGROUPS 16 /* three 4-wave workgroups per CU (three waves per SIMD, 2-stage LDS
-                                          rings); overrides PIPER_PLAN_FOUR_WAVES.  Piper Attention only */
+                                          rings); overrides PIPER_PLAN_FOUR_WAVES.  Both operators */
 #define PIPER_PLAN_MASK 31
 
 /* piper_attention_args.flags / piper_attention_fused_args.flags */

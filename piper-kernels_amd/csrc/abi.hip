@@ -401,8 +401,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
   if (!(std::isfinite(a->scale) && a->scale > 0.0f))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
-  if (a->plan < 0 || a->plan > PIPER_PLAN_MASK || (a->plan & PIPER_PLAN_THREE_WORKGROUPS))
-    return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
+  if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
   if ((a->flags & ~(PIPER_ATTENTION_QK_PER_THREAD | PIPER_SAGE_FP16_PARTIALS)) != 0)
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   if (int st = check_input("query", a->query)) return st;
@@ -412,7 +411,8 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   if (!aligned16(o.kv_tiles) || !aligned16(o.value_scale) || (reinterpret_cast<uintptr_t>(a->output) & 7u) != 0)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte and the output 8-byte aligned");
 
-  const int waves = (a->plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
+  // 3: three 4-wave workgroups per CU (sage_attention_w3_kernel)
+  const int waves = (a->plan & PIPER_PLAN_THREE_WORKGROUPS) ? 3 : (a->plan & PIPER_PLAN_FOUR_WAVES) ? 4 : 8;
   piper::SageParams sp{};
   sp.kv_tiles = static_cast<const uint8_t*>(o.kv_tiles);
   sp.value_scale = o.value_scale;
@@ -424,7 +424,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   sp.query_length = static_cast<int>(s.query_length);
   sp.key_length = static_cast<int>(s.key_length);
   sp.nkb = static_cast<int>(ceil_div(s.key_length, PIPER_KEY_BLOCK));
-  sp.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * waves));
+  sp.query_tiles = static_cast<int>(ceil_div(s.query_length, 32 * (waves == 3 ? 4 : waves)));
   sp.scale_log2e = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
   sp.causal_forward = (a->plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
   sp.xcd_remap = (a->plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;

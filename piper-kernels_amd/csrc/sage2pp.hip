@@ -286,22 +286,144 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) sage_attention_kernel(const S
   }
 }
 
+// Three 4-wave workgroups per CU (three waves per SIMD, each from another workgroup), as Piper
+// Attention's attention_w3_kernel: a 2-stage LDS ring per workgroup and no score look-ahead, to
+// fit 168 VGPRs.  Iteration t: wait for this wave's copies of tile t, barrier (every copy of
+// tile t landed, every read of tile t - 1 done), start the copy of tile t + 1 into the stage
+// tile t - 1 used, then the scores, head and tail of tile t.  Same per-block arithmetic as
+// sage_attention_kernel, in the same order, so the output is bit-identical to the other plans.
+template <int D, bool kCausal, int kOut, bool kPerThread, bool kFp16Partials>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3, 3)))
+sage_attention_w3_kernel(const SageParams p) {
+  constexpr int NW = 4;
+  using L = SageLayout<D, NW>;
+  constexpr int kChunksD = D / 32;
+  __shared__ __attribute__((aligned(16))) char smem[2 * L::kStageBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5;
+  const int n = lane & 31;
+  const TileCoord tc = workgroup_tile<kCausal>(p);
+  const int bh = __builtin_amdgcn_readfirstlane(tc.bh);
+  const int qtile = __builtin_amdgcn_readfirstlane(tc.qtile);
+  const int q0 = qtile * (NW * 32) + wave * 32;
+  const bool wave_live = q0 < p.query_length;
+
+  int tiles = p.nkb;
+  int wave_tiles = wave_live ? p.nkb : 0;
+  if constexpr (kCausal) {
+    const int last_query = min(p.query_length, (qtile + 1) * NW * 32) - 1;
+    tiles = last_query / kKeyBlock + 1;
+    wave_tiles = wave_live ? (min(p.query_length, q0 + 32) - 1) / kKeyBlock + 1 : 0;
+  }
+
+  // query loads first (untracked), then the copies of tile 0, then a wait for the query only
+  v4i raw[D / 16];
+  if (wave_live) issue_query_loads<D>(p, bh, q0, n, h, raw);
+  copy_block<L>(p, smem, bh, 0, wave, lane);
+  v4i qf[kChunksD];
+  float cq = 0.0f;
+  if (wave_live) {
+    if (wave < L::kFullWaves)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds - 1) : "memory");
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * (p.scale_log2e * kScoreUnit);
+  } else {
+#pragma unroll
+    for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
+  }
+
+  v16f acc[kChunksD];
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  float den = 0.0f;
+  float mrun = -__builtin_inff();
+  const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+
+  for (int t = 0; t < tiles; ++t) {
+    if constexpr (!kCausal) progress_priority(t, 1, tiles);  // causal: workgroups differ in length
+    stage_barrier<0>();
+    if (t + 1 < tiles) copy_block<L>(p, smem + ((t + 1) & 1) * L::kStageBytes, bh, t + 1, wave, lane);
+    if (t < wave_tiles) {
+      const char* stage = smem + (t & 1) * L::kStageBytes;
+      v16i sc[2];
+      block_scores<D, L>(stage, qf, h, krow, sc);
+      float ct[4];
+      if constexpr (kPerThread) {
+        const float4 ks = *reinterpret_cast<const float4*>(stage + D);
+        ct[0] = cq * ks.x;
+        ct[1] = cq * ks.y;
+        ct[2] = cq * ks.z;
+        ct[3] = cq * ks.w;
+      } else {
+        ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
+      }
+      float x[32];
+      sage_block_head<D, kCausal, kPerThread>(sc, ct, t, q0, n, h, p.key_length, x, acc, den, mrun);
+      sage_block_tail<D, NW, kFp16Partials>(stage, x, ct, n, h, acc, den, mrun);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may outlive the waves
+
+  const float total = cross_half_sum(den);
+  const int query = q0 + n;
+  if (!wave_live || query >= p.query_length) return;
+  const float rden = 1.0f / fmaxf(total, 1e-30f);
+  const float* vscale = p.value_scale + static_cast<long>(bh) * D;
+  const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
+#pragma unroll
+  for (int j = 0; j < kChunksD; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * j + 8 * g + 4 * h;
+      const float4 vs = *reinterpret_cast<const float4*>(vscale + d0);
+      store4<kOut>(p.output, out_row + d0, (acc[j][4 * g + 0] * vs.x) * rden, (acc[j][4 * g + 1] * vs.y) * rden,
+                   (acc[j][4 * g + 2] * vs.z) * rden, (acc[j][4 * g + 3] * vs.w) * rden);
+    }
+  }
+}
+
 template <int D, int NW, bool kCausal, bool kPerThread, bool kFp16Partials>
 static hipError_t sage_launch_out(int out_dtype, const SageParams& sp, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(sp.query_tiles * sp.batch_heads));
-  const dim3 block(NW * 64);
-  switch (out_dtype) {
-    case 0:
-      hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 0, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
-      break;
-    case 1:
-      hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 1, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
-      break;
-    default:
-      hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 2, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
-      break;
+  if constexpr (NW == 3) {  // three 4-wave workgroups per CU
+    const dim3 block(256);
+    switch (out_dtype) {
+      case 0:
+        hipLaunchKernelGGL((sage_attention_w3_kernel<D, kCausal, 0, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
+        break;
+      case 1:
+        hipLaunchKernelGGL((sage_attention_w3_kernel<D, kCausal, 1, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
+        break;
+      default:
+        hipLaunchKernelGGL((sage_attention_w3_kernel<D, kCausal, 2, kPerThread, kFp16Partials>), grid, block, 0, stream, sp);
+        break;
+    }
+    return hipGetLastError();
+  } else {
+    const dim3 block(NW * 64);
+    switch (out_dtype) {
+      case 0:
+        hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 0, kPerThread, kFp16Partials>), grid, block, 0, stream,
+                           sp);
+        break;
+      case 1:
+        hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 1, kPerThread, kFp16Partials>), grid, block, 0, stream,
+                           sp);
+        break;
+      default:
+        hipLaunchKernelGGL((sage_attention_kernel<D, NW, kCausal, 2, kPerThread, kFp16Partials>), grid, block, 0, stream,
+                           sp);
+        break;
+    }
+    return hipGetLastError();
   }
-  return hipGetLastError();
 }
 
 template <int D, int NW, bool kCausal, bool kPerThread>
@@ -324,12 +446,16 @@ static hipError_t sage_launch_causal(bool causal, int out_dtype, const SageParam
 
 hipError_t launch_sage_attention(int head_dim, bool causal, int out_dtype, int waves, const SageParams& sp,
                                  hipStream_t stream) {
+  // waves: 8 or 4 query waves per workgroup with two waves per SIMD, or 3 for three 4-wave
+  // workgroups per CU (sage_attention_w3_kernel)
   if (head_dim == 128) {
-    return waves == 4 ? sage_launch_causal<128, 4>(causal, out_dtype, sp, stream)
-                      : sage_launch_causal<128, 8>(causal, out_dtype, sp, stream);
+    return waves == 3   ? sage_launch_causal<128, 3>(causal, out_dtype, sp, stream)
+           : waves == 4 ? sage_launch_causal<128, 4>(causal, out_dtype, sp, stream)
+                        : sage_launch_causal<128, 8>(causal, out_dtype, sp, stream);
   }
-  return waves == 4 ? sage_launch_causal<64, 4>(causal, out_dtype, sp, stream)
-                    : sage_launch_causal<64, 8>(causal, out_dtype, sp, stream);
+  return waves == 3   ? sage_launch_causal<64, 3>(causal, out_dtype, sp, stream)
+         : waves == 4 ? sage_launch_causal<64, 4>(causal, out_dtype, sp, stream)
+                      : sage_launch_causal<64, 8>(causal, out_dtype, sp, stream);
 }
 
 }  // namespace piper

@@ -136,9 +136,10 @@ def piper_heuristic_plan(batch: int, heads: int, query_length: int, is_causal: b
 
 
 def sage_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
-    """The SageAttention2++ operator's plan: 4-wave workgroups, two per CU, on every shape
-    (measured 4-22% faster than 8-wave workgroups at c2-c5: c2 22%, c3 4%, c4 9%, c5 5%)."""
-    return MI355XPlan(waves=4)
+    """The SageAttention2++ operator's plan: three 4-wave workgroups per CU on every shape
+    (same-box A/B against two per CU: c2 14%, c3 8%, c4 7%, c5 8% faster; two per CU had been
+    4-22% faster than one 8-wave workgroup per CU at c2-c5)."""
+    return MI355XPlan(waves=4, three_per_cu=True)
 
 
 def select_plan(batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool) -> MI355XPlan:

@@ -235,7 +235,7 @@ def test_plan_selection() -> None:
     # Piper Attention's untuned shapes: three 4-wave workgroups per CU
     for shape in ((1, 24, 16384, False), (1, 24, 16384, True), (2, 32, 8192, False), (1, 1, 32768, False)):
         assert _plan.piper_heuristic_plan(*shape) == MI355XPlan(waves=4, three_per_cu=True)
-    assert _plan.sage_plan(1, 24, 16384) == MI355XPlan(waves=4)  # SageAttention2++: two per CU everywhere
+    assert _plan.sage_plan(1, 24, 16384) == MI355XPlan(waves=4, three_per_cu=True)  # SageAttention2++: three per CU
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
                                         "causal_interleave": False, "three_per_cu": False, "block_m": 256,

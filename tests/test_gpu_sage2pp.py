@@ -190,7 +190,7 @@ def test_reference_gate(gfx950_device, dtype, head_dim, is_causal) -> None:
 def test_plans_and_reruns_are_bitwise_identical(gfx950_device) -> None:
     q, k, v = _inputs((1, 2, 700, 700, 128), torch.bfloat16, seed=83)
     outs = []
-    for plan in [MI355XPlan.from_id(i) for i in range(16)] + [MI355XPlan()]:
+    for plan in MI355XPlan.all_plans() + [MI355XPlan()]:
         prepared = _prepare(q, k, v, 128**-0.5, True, gfx950_device, plan=plan)
         outs.append(_launch(prepared).cpu())
     assert all(torch.equal(outs[0], o) for o in outs[1:])
@@ -247,15 +247,17 @@ def test_quality_against_fp64_sdpa(gfx950_device) -> None:
 GOLDEN_FIXTURES = sorted((GOLDEN / "sage2pp").glob("*.npz"))
 
 
-@pytest.mark.parametrize("waves", [8, 4])
+@pytest.mark.parametrize(
+    "plan", [MI355XPlan(waves=8), MI355XPlan(waves=4), MI355XPlan(waves=4, three_per_cu=True)], ids=["w8", "w4", "w3"]
+)
 @pytest.mark.parametrize("fixture", GOLDEN_FIXTURES, ids=[p.stem for p in GOLDEN_FIXTURES])
-def test_golden_fixture(gfx950_device, fixture, waves) -> None:
+def test_golden_fixture(gfx950_device, fixture, plan) -> None:
     """Prep bit for bit and the output within the gates of the committed oracle fixtures."""
     g = load_golden(fixture)
-    log(f"[sage golden] {fixture.stem} waves={waves}")
+    log(f"[sage golden] {fixture.stem} plan={plan.plan_id}")
     q, k, v = g["query"], g["key"], g["value"]
     sk, d = k.shape[2], k.shape[3]
-    prepared = _prepare(q, k, v, g["scale"], g["is_causal"], gfx950_device, plan=MI355XPlan(waves=waves))
+    prepared = _prepare(q, k, v, g["scale"], g["is_causal"], gfx950_device, plan=plan)
     assert _bits_equal(prepared.key_mean.cpu().numpy(), g["key_mean"])
     assert _bits_equal(prepared.key_scale.cpu().numpy(), np.repeat(g["key_block_scale"][..., None], 4, axis=-1))
     assert _bits_equal(prepared.value_scale.cpu().numpy(), g["value_scale"])
