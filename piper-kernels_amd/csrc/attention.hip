@@ -134,27 +134,40 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   const v4i p0 = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]), static_cast<int>(pw[3])};
   const v4i p1 = {static_cast<int>(pw[4]), static_cast<int>(pw[5]), static_cast<int>(pw[6]), static_cast<int>(pw[7])};
 
-  // ---- numerator: O^T += (V^T (u - 128) + 128 colsum) * beta / 255 ----
+  // ---- numerator: O^T += (V^T (u - 128) + 128 colsum) * beta / 255, two D chunks' MFMA chains
+  // in flight at a time (the score and probability registers are dead here) ----
   const v4i* corr4 = reinterpret_cast<const v4i*>(stage + L::kCorrOffset);
 #pragma unroll
-  for (int j = 0; j < kChunksD; ++j) {
-    v16i acc;
+  for (int j0 = 0; j0 < kChunksD; j0 += 2) {
+    v16i acc[2];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const v4i c4 = corr4[8 * j + 2 * g + h];
-      acc[4 * g + 0] = c4[0];
-      acc[4 * g + 1] = c4[1];
-      acc[4 * g + 2] = c4[2];
-      acc[4 * g + 3] = c4[3];
+    for (int u = 0; u < 2; ++u) {
+      const int j = j0 + u;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const v4i c4 = corr4[8 * j + 2 * g + h];
+        acc[u][4 * g + 0] = c4[0];
+        acc[u][4 * g + 1] = c4[1];
+        acc[u][4 * g + 2] = c4[2];
+        acc[u][4 * g + 3] = c4[3];
+      }
     }
-    const char* vrow = stage + L::kKBytes + (32 * j + n) * L::kVStride + 16 * h;
-    const v4i a0 = *reinterpret_cast<const v4i*>(vrow);
-    const v4i a1 = *reinterpret_cast<const v4i*>(vrow + 32);
-    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, p0, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, p1, acc, 0, 0, 0);
+    v4i a0[2], a1[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const char* vrow = stage + L::kKBytes + (32 * (j0 + u) + n) * L::kVStride + 16 * h;
+      a0[u] = *reinterpret_cast<const v4i*>(vrow);
+      a1[u] = *reinterpret_cast<const v4i*>(vrow + 32);
+    }
+    acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[0], p0, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[1], p0, acc[1], 0, 0, 0);
+    acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[0], p1, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[1], p1, acc[1], 0, 0, 0);
     // acc started from the biased correction: its bits are 1.5 * 2^23 + (u @ v) exactly.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) num[j][r] = fmaf(unbias(acc[r]), weight, num[j][r]);
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) num[j0 + u][r] = fmaf(unbias(acc[u][r]), weight, num[j0 + u][r]);
   }
 }
 
