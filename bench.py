@@ -53,6 +53,16 @@ sys.path[:0] = [str(REPO), str(REPO / "piper-kernels_amd")]
 
 INT8_PEAK_TOPS = 5033.2  # MI355X dense INT8 MFMA: 256 CU x 2.4 GHz x 8192 ops/clk/CU
 HBM_PEAK_GBPS = 8000.0
+# benchmarks/README.md:521 of the reference: B1 H8 N8192 D128 BF16 non-causal, centred V
+REFERENCE_R1 = {
+    "hardware": "RTX 5090 (SM120), Torch 2.12.1+cu130, Triton 3.7.1",
+    "hot_ms": 0.674,
+    "hot_tops": 407.8,
+    "complete_ms": 0.775,
+    "complete_tops": 354.7,
+    "sqnr_db_vs_sdpa": 36.08,
+    "source": "benchmarks/README.md:521",
+}
 
 
 def log(msg: str) -> None:
@@ -65,7 +75,12 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--warmup-ms", type=float, default=300.0, help="minimum GPU time of the warm-up steps")
-    parser.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument(
+        "--workload",
+        default="c3",
+        choices=["c1", "c2", "c3", "c4", "c5", "r1"],
+        help="BASELINE.json's configurations c1-c5, or r1: the shape of the reference's published RTX 5090 figures",
+    )
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     parser.add_argument("--quality-rows", type=int, default=256, help="query rows per head in the FP64 SDPA check")
@@ -425,7 +440,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded numpy PCG64 per head, fp16 inputs resident in HBM)",
+        "data": f"synthetic (seeded numpy PCG64 per head, {workload.as_dict()['dtype']} inputs resident in HBM)",
         "config": {
             **workload.as_dict(),
             "operator": args.operator,
@@ -472,6 +487,16 @@ def main() -> int:
     else:
         result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
         result["config"]["qk_granularity"] = args.qk_granularity
+        if workload.name == "r1":
+            # the reference's only published Piper Attention figures are for this shape, on another GPU
+            # (benchmarks/README.md:521: RTX 5090, BF16, centred V, p50): complete call 0.775 ms, hot
+            # prepared kernel 0.674 ms, SQNR vs SDPA 36.08 dB
+            result["vs_baseline"] = round(value / REFERENCE_R1["complete_tops"], 3)
+            result["reference_published"] = {
+                **REFERENCE_R1,
+                "kernel_speedup": round(REFERENCE_R1["hot_ms"] / attn_mean, 3),
+                "complete_speedup": round(REFERENCE_R1["complete_ms"] / ms_per_step, 3),
+            }
     result["environment"] = environment(device)
     if not args.no_probes:
         # the sustained dense MFMA rate of this GPU and the issue probe (after the timed region)

@@ -60,6 +60,11 @@ WORKLOADS: dict[str, Workload] = {
     "c5": Workload("c5", 2, 40, 32768, 32768, 128, torch.float16, False, 5, "student_t",
                    "B2 H40 S32768 D128 fp16 non-causal; QK = 0.5*t(3); heads<20 V constant along S, "
                    "others V~N(0,1)+N(0,8) per feature"),
+    # the shape of the reference's only published Piper Attention figures (RTX 5090,
+    # benchmarks/README.md:511-523), inputs standard normal as its benchmark draws them
+    # (benchmarks/lib/attention.py:99-120)
+    "r1": Workload("r1", 1, 8, 8192, 8192, 128, torch.bfloat16, False, 11, "plain",
+                   "B1 H8 S8192 D128 bf16 non-causal; QKV~N(0,1) (the reference's published benchmark shape)"),
 }
 
 
@@ -78,6 +83,8 @@ def _head(w: Workload, b: int, h: int) -> tuple[np.ndarray, np.ndarray, np.ndarr
     q = rng.standard_normal((sq, d), dtype=np.float32)
     k = rng.standard_normal((sk, d), dtype=np.float32)
     v = rng.standard_normal((sk, d), dtype=np.float32)
+    if w.kind == "plain":
+        return q, k, v
     k_bias_std = 1.0 if w.kind == "kbias1" else np.sqrt(2.0)
     k += np.float32(k_bias_std) * rng.standard_normal((1, d), dtype=np.float32)
     if w.kind == "kbias_vbias4":

@@ -369,6 +369,18 @@ def test_workload_inputs_are_reproducible_per_head() -> None:
     assert torch.equal(q1[:, [3, 5]], q2) and torch.equal(k1[:, [3, 5]], k2) and torch.equal(v1[:, [3, 5]], v2)
 
 
+def test_reference_benchmark_workload_is_plain_standard_normal() -> None:
+    """r1: the shape of the reference's published figures (benchmarks/README.md:521), inputs
+    drawn as its benchmark draws them: standard normal Q, K, V with no per-channel offsets."""
+    w = WORKLOADS["r1"]
+    assert w.shape == (1, 8, 8192, 8192, 128) and w.dtype is torch.bfloat16 and not w.is_causal
+    q, k, v = make_inputs(w, heads=[2])
+    for x in (q, k, v):
+        x = x.float()
+        assert abs(x.mean().item()) < 0.01 and abs(x.std().item() - 1.0) < 0.01
+        assert x.mean(dim=2).abs().max().item() < 0.05  # no per-channel offset
+
+
 def test_student_t_workload_has_constant_value_heads() -> None:
     w = WORKLOADS["c5"]
     small = type(w)(**{**w.__dict__, "query_length": 256, "key_length": 256})
