@@ -20,7 +20,8 @@
 //   is round().clamp(0, 255) of the reference.
 // * K, V^T, per-key log2 scales, inverse multipliers and column sums of a tile form one
 //   record laid out exactly like its LDS stage (padded rows against bank conflicts); it is
-//   copied with direct global -> LDS loads into a 6-stage ring, 4 blocks ahead.
+//   copied with direct global -> LDS loads into an LDS ring: two stages, one block ahead, with
+//   three workgroups per CU (the default); four or six stages in the two-waves-per-SIMD plans.
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"

@@ -23,7 +23,8 @@
 // one query and keys {16h .. 16h+15} and {32+16h .. 32+16h+15} of every block -- which, packed
 // in that order, is directly the B operand of the FP8 MFMA (which contracts over any key order
 // the A operand shares: V^T rows are read at bytes [16h, +16) and [32 + 16h, +16)); the query
-// is quantised in the prologue; tile records are copied straight into a 6-stage LDS ring.
+// is quantised in the prologue; tile records are copied straight into an LDS ring (two stages per
+// workgroup with three workgroups per CU, the default; four or six in the two-waves-per-SIMD plans).
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"
