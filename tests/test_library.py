@@ -313,6 +313,9 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     args.flags = native.ATTENTION_QK_PER_THREAD | native.SAGE_FP16_PARTIALS  # both known
     with pytest.raises(RuntimeError, match="output pointer is NULL"):
         lib.sage_attention_forward(args, 0)
+    args.plan = 16  # three workgroups per CU: SageAttention2++'s default plan
+    with pytest.raises(RuntimeError, match="output pointer is NULL"):
+        lib.sage_attention_forward(args, 0)
     args.is_causal = 1
     args.shape = native.PiperShape(1, 1, 8, 9, 64)
     with pytest.raises(RuntimeError, match="equal query and key lengths"):
