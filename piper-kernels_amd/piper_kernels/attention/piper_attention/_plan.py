@@ -131,8 +131,18 @@ def piper_heuristic_plan(batch: int, heads: int, query_length: int, is_causal: b
     """Piper Attention's plan for an untuned shape: three 4-wave workgroups per CU.  With three
     waves per SIMD from three independent workgroups, one wave's MFMA, LDS and barrier waits are
     filled by the other two: measured 7-24% faster than the two-waves-per-SIMD plans at c2-c5 and
-    within 1% of the best at c1 (tiny grid)."""
-    return MI355XPlan(waves=4, three_per_cu=True)
+    within 1% of the best at c1 (tiny grid).  A non-causal grid whose 128-query tiles cannot fill
+    three slots per CU, but whose 256-query tiles give every CU one, runs two waves per SIMD
+    either way; one 8-wave workgroup per CU is then 1-2% faster (measured at r1, B1 H8 N8192)."""
+    three = MI355XPlan(waves=4, three_per_cu=True)
+    wide = MI355XPlan(waves=8)
+    if (
+        not is_causal
+        and three.workgroups(batch, heads, query_length) < 3 * COMPUTE_UNITS
+        and wide.workgroups(batch, heads, query_length) >= COMPUTE_UNITS
+    ):
+        return wide
+    return three
 
 
 def sage_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:

@@ -235,6 +235,12 @@ def test_plan_selection() -> None:
     # Piper Attention's untuned shapes: three 4-wave workgroups per CU
     for shape in ((1, 24, 16384, False), (1, 24, 16384, True), (2, 32, 8192, False), (1, 1, 32768, False)):
         assert _plan.piper_heuristic_plan(*shape) == MI355XPlan(waves=4, three_per_cu=True)
+    # ... except non-causal grids of 256-1535 query tiles of 256 rows that cannot fill three
+    # 128-row slots per CU: one 8-wave workgroup per CU (r1, B1 H8 N8192, measured)
+    assert _plan.piper_heuristic_plan(1, 8, 8192, False) == MI355XPlan(waves=8)
+    assert _plan.piper_heuristic_plan(1, 8, 8192, True) == MI355XPlan(waves=4, three_per_cu=True)
+    assert _plan.piper_heuristic_plan(1, 24, 4096, False) == MI355XPlan(waves=4, three_per_cu=True)  # 768 tiles
+    assert _plan.piper_heuristic_plan(1, 8, 1024, False) == MI355XPlan(waves=4, three_per_cu=True)  # tiny grid
     assert _plan.sage_plan(1, 24, 16384) == MI355XPlan(waves=4, three_per_cu=True)  # SageAttention2++: three per CU
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
