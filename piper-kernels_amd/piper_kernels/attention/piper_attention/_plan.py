@@ -148,7 +148,8 @@ def piper_heuristic_plan(batch: int, heads: int, query_length: int, is_causal: b
 def sage_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
     """The SageAttention2++ operator's plan: three 4-wave workgroups per CU on every shape
     (same-box A/B against two per CU: c2 14%, c3 8%, c4 7%, c5 8% faster; two per CU had been
-    4-22% faster than one 8-wave workgroup per CU at c2-c5)."""
+    4-22% faster than one 8-wave workgroup per CU at c2-c5; at r1, where the grid cannot fill
+    three slots per CU, three per CU still beat one 8-wave workgroup per CU by 3%)."""
     return MI355XPlan(waves=4, three_per_cu=True)
 
 
