@@ -479,9 +479,9 @@ def main() -> int:
     from piper_kernels.attention.piper_attention._plan import select_plan
 
     if sage:
-        from piper_kernels.attention.piper_attention._plan import sage_plan
+        from piper_kernels.attention.piper_attention._plan import select_sage_plan
 
-        result["config"]["plan"] = sage_plan(b, h, sq).as_dict()
+        result["config"]["plan"] = select_sage_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
         result["roofline"]["traffic"] = None
         result["dtype"] = "int8 QK, fp8 e4m3 PV"
     else:

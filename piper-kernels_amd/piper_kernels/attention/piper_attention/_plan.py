@@ -5,7 +5,9 @@ Plays the role of the reference's ``PiperAttentionExecutionPlan`` /
 for gfx950: an immutable record chosen from the shape, never autotuned at call time.
 ``select_plan`` looks the shape up in the frozen table ``mi355x_plans.json`` (written offline
 by ``piper_kernels.attention.piper_attention.tune``, the counterpart of the reference's
-``benchmarks/tune_piper_attention.py``) and falls back to a heuristic for other shapes.
+``benchmarks/tune_piper_attention.py``) and falls back to a heuristic for other shapes;
+``select_sage_plan`` does the same for SageAttention2++ with ``mi355x_sage_plans.json`` (the
+counterpart of ``sage_attention_2pp/_policy.py`` and ``benchmarks/tune_sage_attention_2pp.py``).
 Every plan computes bit-identical results; only the speed differs.
 """
 
@@ -20,6 +22,7 @@ COMPUTE_UNITS = 256  # MI355X
 KEY_BLOCK = 64  # keys per streamed tile and per P block (reference.py:16)
 QUERIES_PER_WAVE = 32  # one v_mfma_i32_32x32x32_i8 column block
 PLAN_TABLE = Path(__file__).with_name("mi355x_plans.json")
+SAGE_PLAN_TABLE = Path(__file__).with_name("mi355x_sage_plans.json")
 
 # piper_attention_args.plan bits (include/piper_mi355x.h)
 PLAN_FOUR_WAVES = 1
@@ -104,18 +107,29 @@ def shape_key(batch: int, heads: int, query_length: int, key_length: int, head_d
     return (batch * heads, query_length, key_length, head_dim, bool(is_causal))
 
 
-@lru_cache(maxsize=1)
-def frozen_plans() -> dict:
-    """The committed tuner table: shape key -> plan (empty if the file is absent)."""
-    if not PLAN_TABLE.exists():
+def _read_plan_table(path: Path) -> dict:
+    """A tuner table: shape key -> plan (empty if the file is absent)."""
+    if not path.exists():
         return {}
-    table = json.loads(PLAN_TABLE.read_text())
+    table = json.loads(path.read_text())
     plans = {}
     for entry in table.get("entries", []):
         k = entry["key"]
         key = (k["batch_heads"], k["query_length"], k["key_length"], k["head_dim"], bool(k["is_causal"]))
         plans[key] = MI355XPlan(**entry["plan"])
     return plans
+
+
+@lru_cache(maxsize=1)
+def frozen_plans() -> dict:
+    """Piper Attention's committed tuner table: shape key -> plan."""
+    return _read_plan_table(PLAN_TABLE)
+
+
+@lru_cache(maxsize=1)
+def frozen_sage_plans() -> dict:
+    """SageAttention2++'s committed tuner table: shape key -> plan."""
+    return _read_plan_table(SAGE_PLAN_TABLE)
 
 
 def heuristic_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
@@ -157,3 +171,10 @@ def select_plan(batch: int, heads: int, query_length: int, key_length: int, head
     """The frozen table's plan for a tuned shape, else Piper Attention's heuristic."""
     plan = frozen_plans().get(shape_key(batch, heads, query_length, key_length, head_dim, is_causal))
     return plan if plan is not None else piper_heuristic_plan(batch, heads, query_length, is_causal)
+
+
+def select_sage_plan(batch: int, heads: int, query_length: int, key_length: int, head_dim: int,
+                     is_causal: bool) -> MI355XPlan:
+    """SageAttention2++'s frozen-table plan for a tuned shape, else ``sage_plan``."""
+    plan = frozen_sage_plans().get(shape_key(batch, heads, query_length, key_length, head_dim, is_causal))
+    return plan if plan is not None else sage_plan(batch, heads, query_length)

@@ -5,9 +5,13 @@ search over the plan axes the gfx950 kernel exposes (query waves per workgroup a
 workgroups per CU, causal
 query-tile order -- forward, longest first head by head, or longest first across the heads of
 an XCD -- and XCD-aware workgroup order), quality-gated, whose result is frozen into
-``mi355x_plans.json`` for ``select_plan``.
+``mi355x_plans.json`` for ``select_plan``.  With ``--operator sage_attention_2pp`` it tunes the
+SageAttention2++ kernel over the same axes (the counterpart of the reference's
+``benchmarks/tune_sage_attention_2pp.py``) into ``mi355x_sage_plans.json`` for
+``select_sage_plan``; that operator's default plan is three 4-wave workgroups per CU.
 
     python -m piper_kernels.attention.piper_attention.tune --workloads c1 c2 c3 c4 c5 --write
+    python -m piper_kernels.attention.piper_attention.tune --operator sage_attention_2pp --write
 
 For each shape: synthetic inputs are prepared once (K and V; the kernel quantises the query,
 as the operator runs it); every candidate plan is launched on the same prepared operands and
@@ -48,23 +52,45 @@ def candidate_plans(is_causal: bool):
     ]
 
 
-def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launches: int, margin: float) -> dict:
+def _operator_entry_points(operator: str):
+    """(default plan, prepare(q, k, v, scale, causal, plan), launch(prepared, output=None))."""
+    from piper_kernels.attention.piper_attention._plan import MI355XPlan
+
+    if operator == "sage_attention_2pp":
+        from piper_kernels.attention.sage_attention_2pp.hip import (
+            _launch_sage_attention_2pp,
+            _prepare_sage_attention_2pp,
+        )
+
+        def prepare(q, k, v, scale, causal, plan):
+            return _prepare_sage_attention_2pp(q, k, v, scale, causal, plan=plan)
+
+        return MI355XPlan(waves=4, three_per_cu=True), prepare, _launch_sage_attention_2pp
+    from piper_kernels.attention.piper_attention.hip import _launch_piper_attention, _prepare_piper_attention
+
+    def prepare(q, k, v, scale, causal, plan):
+        return _prepare_piper_attention(q, k, v, scale, causal, plan=plan, quantize_query=False)
+
+    return MI355XPlan(), prepare, _launch_piper_attention
+
+
+def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launches: int, margin: float,
+               operator: str = "piper_attention") -> dict:
     import torch
 
-    from piper_kernels.attention.piper_attention._plan import MI355XPlan, shape_key
-    from piper_kernels.attention.piper_attention.hip import _launch_piper_attention, _prepare_piper_attention
+    from piper_kernels.attention.piper_attention._plan import shape_key
 
     b, h, sq, d = q.shape
     sk = k.shape[2]
-    default = MI355XPlan()
-    prepared = _prepare_piper_attention(q, k, v, d**-0.5, is_causal, plan=default, quantize_query=False)
+    default, prepare, launch = _operator_entry_points(operator)
+    prepared = prepare(q, k, v, d**-0.5, is_causal, default)
     plans = candidate_plans(is_causal)
     reference = torch.empty(q.shape, device=q.device, dtype=torch.float32)
-    _launch_piper_attention(prepared, output=reference)
+    launch(prepared, output=reference)
     candidate_out = torch.empty_like(reference)
     passed = {}
     for plan in plans:
-        _launch_piper_attention(replace(prepared, plan=plan), output=candidate_out)
+        launch(replace(prepared, plan=plan), output=candidate_out)
         torch.cuda.synchronize()
         passed[plan] = bool(torch.equal(candidate_out, reference))
     times = {plan: [] for plan in plans}
@@ -74,7 +100,7 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
     warm_start.record(stream)
     while True:
         for plan in plans:
-            _launch_piper_attention(runs[plan])
+            launch(runs[plan])
         warm_end = torch.cuda.Event(enable_timing=True)
         warm_end.record(stream)
         warm_end.synchronize()
@@ -87,7 +113,7 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record(stream)
             for _ in range(launches):
-                _launch_piper_attention(runs[plan])
+                launch(runs[plan])
             end.record(stream)
             events.append((plan, start, end))
         torch.cuda.synchronize()
@@ -113,18 +139,19 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
 
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--operator", choices=("piper_attention", "sage_attention_2pp"), default="piper_attention")
     parser.add_argument("--workloads", nargs="+", default=["c1", "c2", "c3", "c4", "c5"])
     parser.add_argument("--warmup-ms", type=float, default=1000.0, help="GPU time of warm-up launches per shape")
     parser.add_argument("--rounds", type=int, default=8)
     parser.add_argument("--launches", type=int, default=3)
     parser.add_argument("--margin", type=float, default=0.01, help="minimum gain over the default plan")
-    parser.add_argument("--write", action="store_true", help="write the frozen table next to _plan.py")
+    parser.add_argument("--write", action="store_true", help="write the operator's frozen table next to _plan.py")
     parser.add_argument("--out", type=Path, help="also write the table here")
     args = parser.parse_args(argv)
 
     import torch
 
-    from piper_kernels.attention.piper_attention._plan import PLAN_TABLE
+    from piper_kernels.attention.piper_attention._plan import PLAN_TABLE, SAGE_PLAN_TABLE
     from piper_kernels.workloads import WORKLOADS, make_inputs
 
     device = torch.device("cuda", 0)
@@ -134,7 +161,7 @@ def main(argv: list[str] | None = None) -> int:
             w = WORKLOADS[name]
             q, k, v = make_inputs(w, device)
             entry = tune_shape(q, k, v, w.is_causal, warmup_ms=args.warmup_ms, rounds=args.rounds,
-                               launches=args.launches, margin=args.margin)
+                               launches=args.launches, margin=args.margin, operator=args.operator)
             entry["workload"] = name
             entries.append(entry)
             print(f"[tune] {name}: default {entry['default_ms']:.4f} ms, chosen {entry['plan']} {entry['chosen_ms']:.4f} ms",
@@ -142,13 +169,14 @@ def main(argv: list[str] | None = None) -> int:
             del q, k, v
             torch.cuda.empty_cache()
     table = {
+        "operator": args.operator,
         "device": torch.cuda.get_device_properties(device).gcnArchName,
         "tuner": "python -m piper_kernels.attention.piper_attention.tune " + " ".join(argv if argv is not None else sys.argv[1:]),
         "entries": entries,
     }
     text = json.dumps(table, indent=1) + "\n"
     if args.write:
-        PLAN_TABLE.write_text(text)
+        (SAGE_PLAN_TABLE if args.operator == "sage_attention_2pp" else PLAN_TABLE).write_text(text)
     if args.out:
         args.out.write_text(text)
     print(text)

@@ -18,7 +18,7 @@ from dataclasses import dataclass
 import torch
 
 from ..._hip import library as native
-from ..piper_attention._plan import MI355XPlan, sage_plan
+from ..piper_attention._plan import MI355XPlan, select_sage_plan
 
 _DTYPE_CODES = {torch.float16: native.FLOAT16, torch.bfloat16: native.BFLOAT16, torch.float32: native.FLOAT32}
 
@@ -91,7 +91,7 @@ def _prepare_sage_attention_2pp(
     batch, heads, sq, d = query.shape
     sk = key.shape[2]
     if plan is None:
-        plan = sage_plan(batch, heads, sq)
+        plan = select_sage_plan(batch, heads, sq, sk, d, is_causal)
     shape = native.PiperShape(batch, heads, sq, sk, d)
     layout = lib.sage_prepared_layout(shape)
     device = query.device

@@ -304,6 +304,28 @@ def test_committed_plan_table_is_well_formed() -> None:
         assert len(key) == 5 and isinstance(plan, MI355XPlan)
 
 
+def test_committed_sage_plan_table_lookup_and_fallback() -> None:
+    """SageAttention2++'s frozen table: the tuner's entries are what select_sage_plan returns for
+    their shapes (c4 took the interleaved causal order, plan 24), and an untuned shape gets
+    sage_plan's three 4-wave workgroups per CU."""
+    import json
+
+    from piper_kernels.attention.piper_attention import _plan
+
+    _plan.frozen_sage_plans.cache_clear()
+    table = json.loads(_plan.SAGE_PLAN_TABLE.read_text())
+    assert table["operator"] == "sage_attention_2pp" and table["entries"]
+    for entry in table["entries"]:
+        k = entry["key"]
+        assert all(c["bitwise_equal_to_default"] for c in entry["candidates"]), entry["workload"]
+        chosen = _plan.select_sage_plan(1, k["batch_heads"], k["query_length"], k["key_length"], k["head_dim"],
+                                        k["is_causal"])
+        assert chosen == MI355XPlan(**entry["plan"])
+        assert min(c["median_ms"] for c in entry["candidates"]) >= entry["chosen_ms"] * (1 - 0.01) - 1e-9
+    assert _plan.select_sage_plan(4, 32, 8192, 8192, 128, True).plan_id == 24
+    assert _plan.select_sage_plan(1, 3, 777, 777, 64, False) == _plan.sage_plan(1, 3, 777)
+
+
 # ---- custom op -----------------------------------------------------------------------
 def test_custom_op_is_registered_with_reference_schema_and_fake() -> None:
     op = torch.ops.piper_kernels.piper_attention.default
