@@ -296,6 +296,47 @@ def quality_block(workload, output, reference_outputs: dict, rows: int) -> dict:
 # ---------------------------------------------------------------------------------------
 # environment
 # ---------------------------------------------------------------------------------------
+HIP_ATTRIBUTE_CLOCK_RATE = 5  # hipDeviceAttributeClockRate (hip_runtime_api.h): peak clock in kHz
+
+
+def peak_sclk_mhz(device) -> int | None:
+    """The device's peak engine clock from hipDeviceGetAttribute (torch does not expose it on ROCm)."""
+    import ctypes
+
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+    except OSError:
+        return None
+    value = ctypes.c_int(0)
+    if hip.hipDeviceGetAttribute(ctypes.byref(value), HIP_ATTRIBUTE_CLOCK_RATE, int(device.index or 0)) != 0:
+        return None
+    return value.value // 1000 or None
+
+
+def source_digest() -> dict:
+    """SHA-256 of the measured code as it sits in this tree (the GPU box's copy has no git
+    history): the HIP sources and header, the Python package and bench.py, and the built library."""
+    import hashlib
+
+    package = REPO / "piper-kernels_amd"
+    files = [
+        *sorted((package / "csrc").glob("*")),
+        *sorted((REPO / "include").glob("*.h")),
+        *sorted((package / "piper_kernels").rglob("*.py")),
+        *sorted((package / "piper_kernels").rglob("*.json")),
+        REPO / "bench.py",
+    ]
+    digest = hashlib.sha256()
+    for path in files:
+        if path.is_file():
+            digest.update(str(path.relative_to(REPO)).encode() + b"\0" + path.read_bytes())
+    library = package / "piper_kernels" / "_hip" / "libpiper_mi355x.so"
+    return {
+        "sources_sha256": digest.hexdigest(),
+        "library_sha256": hashlib.sha256(library.read_bytes()).hexdigest() if library.is_file() else None,
+    }
+
+
 def environment(device) -> dict:
     import numpy as np
     import torch
@@ -316,7 +357,7 @@ def environment(device) -> dict:
         "gpu": props.name,
         "arch": props.gcnArchName,
         "compute_units": props.multi_processor_count,
-        "max_sclk_mhz": getattr(props, "clock_rate", 0) // 1000 or None,
+        "max_sclk_mhz": peak_sclk_mhz(device),
         "torch": torch.__version__,
         "hip": torch.version.hip,
         "numpy": np.__version__,
@@ -324,6 +365,7 @@ def environment(device) -> dict:
         "host_cpu": cpu,
         "host_cpu_count": os.cpu_count(),
         "source_revision": revision,
+        **source_digest(),
     }
 
 

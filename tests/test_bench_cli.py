@@ -35,3 +35,14 @@ def test_reference_figures_match_the_baseline_document() -> None:
     ops = 4 * 1 * 8 * 8192 * 8192 * 128
     assert abs(ops / (ref["complete_ms"] * 1e-3) / 1e12 - ref["complete_tops"]) < 0.5
     assert abs(ops / (ref["hot_ms"] * 1e-3) / 1e12 - ref["hot_tops"]) < 0.5
+
+
+def test_source_digest_identifies_the_tree() -> None:
+    """The record's code identity without git: stable across calls, hex SHA-256 values."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    first, second = bench.source_digest(), bench.source_digest()
+    assert first == second
+    assert len(first["sources_sha256"]) == 64 and int(first["sources_sha256"], 16) >= 0
+    assert first["library_sha256"] is None or len(first["library_sha256"]) == 64
