@@ -300,11 +300,16 @@ HIP_ATTRIBUTE_CLOCK_RATE = 5  # hipDeviceAttributeClockRate (hip_runtime_api.h):
 
 
 def peak_sclk_mhz(device) -> int | None:
-    """The device's peak engine clock from hipDeviceGetAttribute (torch does not expose it on ROCm)."""
+    """The device's peak engine clock from hipDeviceGetAttribute (torch does not expose it on ROCm),
+    called in the HIP runtime this process already has mapped (never a second copy of it)."""
     import ctypes
 
     try:
-        hip = ctypes.CDLL("libamdhip64.so")
+        with open("/proc/self/maps") as maps:
+            path = next((line.split()[-1] for line in maps if "libamdhip64.so" in line.split()[-1]), None)
+        if path is None:
+            return None
+        hip = ctypes.CDLL(path, mode=os.RTLD_NOLOAD)
     except OSError:
         return None
     value = ctypes.c_int(0)
