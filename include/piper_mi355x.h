@@ -13,8 +13,8 @@
  *                               (K/V means triton.py:638-699, Q/K quantisation
  *                               attention/kernels/qk_quantization/int8/sage/triton.py:238-356,
  *                               per-key V quantisation triton.py:176-246 / :839-860)
- *   piper_prepare_static     <- no reference counterpart: piper_prepare with the mean partials in
- *                               a static per-GPU scratch, for callers that cannot allocate
+ *   piper_prepare_static     <- no reference counterpart: piper_prepare with its workspace in a
+ *                               static per-GPU scratch, for callers that cannot allocate
  *   piper_attention_forward  <- _launch_piper_attention
  *                               src/piper_kernels/attention/piper_attention/triton.py:893-951
  *                               (fused kernel _piper_attention_kernel triton.py:303-635)
@@ -33,6 +33,8 @@
  *   piper_sage_prepared_layout <- the buffer allocations of _prepare_sage_attention_2pp
  *   piper_prepared_layout    <- the buffer allocations of _prepare_piper_attention
  *                               (triton.py:797-874); the sizes the caller must provide
+ *   piper_prepare_status     <- no reference counterpart: how many chunks of the last prep gave
+ *                               up waiting for their tensor's mean and computed it themselves
  *   piper_abi_version,
  *   piper_last_error         <- no reference counterpart: version handshake and the error
  *                               text the Python layer raises as RuntimeError
@@ -50,7 +52,7 @@
 extern "C" {
 #endif
 
-#define PIPER_ABI_VERSION 2
+#define PIPER_ABI_VERSION 3
 
 /* Rows per quantisation group (sage/reference.py:6-7) and keys per P block (reference.py:16). */
 #define PIPER_QUERY_BLOCK 32
@@ -148,11 +150,15 @@ typedef struct piper_layout {
   int64_t mean_bytes; /* each of key_mean, value_mean */
   int64_t kv_tile_bytes; /* one tile record */
   int64_t kv_tiles_bytes; /* all tile records */
-  int64_t workspace_bytes; /* scratch for piper_prepare: FP32 partial sums of the K/V means
-                              (torch's CPU summation order, so the means and every K/V code
-                              equal the reference's torch.mean(dim=2) path bit for bit), then
-                              4 * (4 * B * H + 4) bytes of arrival counters and a status
-                              word; the library clears what it needs on the stream */
+  int64_t workspace_bytes; /* scratch for piper_prepare, 16-byte aligned: FP32 partial sums of
+                              the K/V means (torch's CPU summation order, so the means and every
+                              K/V code equal the reference's torch.mean(dim=2) path bit for
+                              bit), 2 * B * H * (ceil(Sk / L^2) + 1) * D * 4 bytes (L = 16 up to
+                              Sk = 2^19), then 4 * (4 * B * H + 4) bytes of sync words: arrival
+                              counters and the status word; the library clears what it needs on
+                              the stream */
+  int64_t workspace_status_offset; /* byte offset of the status word in the workspace (a
+                              uint32: see piper_prepare_status) */
 } piper_layout;
 
 /* piper_prepare_args.flags */
@@ -160,6 +166,9 @@ typedef struct piper_layout {
                                       for piper_attention_forward_fused, which quantises Q itself */
 #define PIPER_PREPARE_QK_PER_THREAD 2 /* Q and K scales per thread group (the reference's
                                          "per_thread"); default: one per block ("per_warp") */
+#define PIPER_PREPARE_SELF_MEAN 4 /* diagnostic, for tests: every single-pass chunk that would wait
+                                     for its tensor's mean computes it itself at once (the bounded
+                                     wait's fallback; same bits, slower) */
 
 typedef struct piper_prepare_args {
   int32_t abi_version; /* PIPER_ABI_VERSION */
@@ -296,21 +305,39 @@ int piper_abi_version(void);
 int piper_prepared_layout(const piper_shape* shape, piper_layout* layout);
 
 /* Quantise Q, K, V into args->prepared on `stream` (a hipStream_t; NULL = default stream);
- * with PIPER_PREPARE_SKIP_QUERY only K and V.
- * Launches: FP32 mean partials (torch's CPU order), mean finalisation, one quantisation kernel. */
+ * with PIPER_PREPARE_SKIP_QUERY only K and V.  key_mean must be 4-byte aligned, the workspace
+ * and the other prepared buffers 16-byte aligned.
+ *
+ * Launches, at D = 128 with Sk <= 16384 when one XCC of the device holds a tensor's 256-row
+ * chunks at once (4 * CUs / XCCs >= ceil(Sk / 256); every MI355X partition mode): a fill kernel
+ * (sync words cleared, means marked pending) and the single pass, which reads K and V once: each
+ * chunk publishes its partial sums, the last chunk of a batch-head tensor finalises the mean,
+ * the others wait for it (bounded: a chunk whose wait ends computes the mean itself from K/V in
+ * HBM, same bits, and is counted in the status word), then every chunk quantises its rows.
+ * Otherwise: FP32 mean partials (torch's CPU order), mean finalisation, one quantisation kernel.
+ * Work on other streams or in other processes that holds the GPU's workgroup slots can delay a
+ * tensor's last chunk: the results stay exact, the prep gets slower (piper_prepare_status). */
 int piper_prepare(const piper_prepare_args* args, void* stream);
+
+/* The status word of the last prep that used `workspace` (NULL: the static scratch of
+ * piper_prepare_static on the current device) for `shape`: the number of single-pass chunks
+ * whose bounded wait for their tensor's mean ended, so that they computed it themselves (0 for
+ * the three-kernel path).  Diagnostic: copies the word to *count and synchronises `stream`. */
+int piper_prepare_status(const piper_shape* shape, const void* workspace, uint32_t* count, void* stream);
 
 /* piper_prepare without a caller workspace.  No counterpart in the reference: for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc).  args->workspace must be NULL and args->workspace_bytes 0; the FP32
- * mean partials go to a static scratch array inside the library instead, of
- * PIPER_STATIC_SCRATCH_BYTES bytes per GPU (each GPU the library runs on holds its own copy
- * until the process ends).  Shapes whose piper_layout.workspace_bytes exceeds it are rejected
- * with PIPER_ERROR_UNSUPPORTED before anything is launched (2 * B * H * (ceil(Sk / 256) + 1) *
- * D * 4 bytes for Sk <= 2^19: 10.1 MiB for 80 batch-heads at Sk = 32768, D = 128).  Call it with the
- * stream's device current.  It calls no allocator.  Every call on one GPU shares that GPU's
- * scratch: calls on one stream are ordered, calls that overlap on one GPU (other streams or
- * threads) race.  Outputs are identical to piper_prepare's. */
+ * that forbid hipMalloc).  args->workspace must be NULL and args->workspace_bytes 0; the
+ * workspace (FP32 mean partials, then the sync words) goes to a static scratch array inside the
+ * library instead, of PIPER_STATIC_SCRATCH_BYTES bytes per GPU (each GPU the library runs on
+ * holds its own copy until the process ends).  Shapes whose piper_layout.workspace_bytes exceeds
+ * it are rejected with PIPER_ERROR_UNSUPPORTED before anything is launched (2 * B * H *
+ * (ceil(Sk / 256) + 1) * D * 4 + 4 * (4 * B * H + 4) bytes up to Sk = 2^19: 10.1 MiB for 80
+ * batch-heads at Sk = 32768, D = 128).  Call it with the stream's device current.  It calls no
+ * allocator.  Every call on one GPU shares that GPU's scratch, which each call clears and fills
+ * on its stream: calls on one stream are ordered; calls that overlap on one GPU (other streams
+ * or threads) race on the partials and on the single pass's arrival counters, and their means
+ * and codes are then undefined.  Outputs are identical to piper_prepare's. */
 #define PIPER_STATIC_SCRATCH_BYTES (16ll << 20)
 int piper_prepare_static(const piper_prepare_args* args, void* stream);
 

@@ -41,6 +41,11 @@ const char* piper_probe_last_error(void);
  * as the PV MFMA's signed operand.  P_CODES_FP8: SageAttention2++'s FP8 E4M3 codes. */
 #define PIPER_MFMA_PROBE_P_CODES_U8 2
 #define PIPER_MFMA_PROBE_P_CODES_FP8 3
+/* P_CODES_U8_SCALED: Piper Attention's scaled packer (the kernels' subtraction-free exp2 path):
+ * thread t reads E = words 4 (t % 64) .. + 3 and the multiplier c = word 256 + 4 (t % 64) of its
+ * workgroup's part and stores the UINT8 codes of the exact products E_i * c (round half to even;
+ * defined for products in [0, 255.5)), as bytes u - 128 like P_CODES_U8. */
+#define PIPER_MFMA_PROBE_P_CODES_U8_SCALED 4
 #define PIPER_MFMA_PROBE_THREADS 512
 #define PIPER_MFMA_PROBE_OPS(kind) ((kind) == PIPER_MFMA_PROBE_F8 ? 131072 : 65536)
 int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream);

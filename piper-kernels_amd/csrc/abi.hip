@@ -66,12 +66,13 @@ int check_input(const char* name, const piper_tensor& t) {
   return PIPER_OK;
 }
 
-// Static scratch of piper_prepare_static: the prep's FP32 mean partials for callers that cannot
-// allocate.  Each GPU the library runs on holds its own copy until the process ends.  In host
-// code `scratch` only names the symbol: its device address on the current GPU comes from
-// hipGetSymbolAddress, looked up once per device (device_scratch) and used for every launch.
-// The mean pass writes every partial the finalisation reads, so nothing needs clearing between
-// calls; calls that overlap on one GPU share the array and race.
+// Static scratch of piper_prepare_static: the prep's workspace (FP32 mean partials, then the
+// single pass's sync words) for callers that cannot allocate.  Each GPU the library runs on holds
+// its own copy until the process ends.  In host code `scratch` only names the symbol: its device
+// address on the current GPU comes from hipGetSymbolAddress, looked up once per device
+// (device_scratch) and used for every launch.  Each call clears the sync words it uses with its
+// own fill kernel and writes every partial it reads; calls that overlap on one GPU share the
+// array and race (on the arrival counters too, which then give wrong means).
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_address[kMaxDevices] = {};
@@ -92,6 +93,33 @@ int device_scratch(void** address) {
     g_scratch_address[device] = ptr;
   }
   *address = g_scratch_address[device];
+  return PIPER_OK;
+}
+
+// Compute units and XCCs of the current device, looked up once per device: the single-pass
+// prep deals its workgroups over the XCCs and needs a tensor's chunks resident in one XCC.
+std::mutex g_topology_mutex;
+int g_topology[kMaxDevices][2] = {};
+
+int device_topology(int* cus, int* xccs) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(PIPER_ERROR_UNSUPPORTED, "device %d is beyond the %d this build tracks", device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_topology_mutex);
+  if (g_topology[device][0] == 0) {
+    int c = 0, x = 0;
+    err = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "compute-unit count query failed: %s", hipGetErrorString(err));
+    // no XCC count (an older runtime): 0, which keeps the prep on its three-kernel path
+    if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, device) != hipSuccess || x < 0) x = 0;
+    (void)hipGetLastError();
+    g_topology[device][0] = c;
+    g_topology[device][1] = x;
+  }
+  *cus = g_topology[device][0];
+  *xccs = g_topology[device][1];
   return PIPER_OK;
 }
 
@@ -194,6 +222,7 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout) {
   layout->kv_tile_bytes = PIPER_KV_TILE_BYTES(d);
   layout->kv_tiles_bytes = bh * (sk64 / PIPER_KEY_BLOCK) * PIPER_KV_TILE_BYTES(d);
   layout->workspace_bytes = 2 * bh * (chunks + 1) * d * 4 + 4 * piper::prep_sync_words(bh);
+  layout->workspace_status_offset = 2 * bh * (chunks + 1) * d * 4 + 4 * piper::prep_status_word(bh);
   g_last_error[0] = '\0';
   return PIPER_OK;
 }
@@ -210,7 +239,7 @@ static int prepare_call(const piper_prepare_args* a, bool use_scratch, void* str
   if (int st = check_shape(&a->shape)) return st;
   if (a->is_causal && a->shape.query_length != a->shape.key_length)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "causal attention requires equal query and key lengths");
-  if ((a->flags & ~(PIPER_PREPARE_SKIP_QUERY | PIPER_PREPARE_QK_PER_THREAD)) != 0)
+  if ((a->flags & ~(PIPER_PREPARE_SKIP_QUERY | PIPER_PREPARE_QK_PER_THREAD | PIPER_PREPARE_SELF_MEAN)) != 0)
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   const bool with_query = (a->flags & PIPER_PREPARE_SKIP_QUERY) == 0;
   if (with_query)
@@ -223,6 +252,11 @@ static int prepare_call(const piper_prepare_args* a, bool use_scratch, void* str
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "a prepared output pointer is NULL");
   if ((with_query && !aligned16(o.query_code)) || !aligned16(o.kv_tiles) || !aligned16(o.value_mean))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "prepared buffers must be 16-byte aligned");
+  // the prep reads and writes the means and the workspace's sync words with 32-bit atomics
+  if ((reinterpret_cast<uintptr_t>(o.key_mean) & 3u) != 0)
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "key_mean must be 4-byte aligned");
+  if (!use_scratch && !aligned16(a->workspace))
+    return fail(PIPER_ERROR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   piper_layout layout;
   if (int st = piper_prepared_layout(&a->shape, &layout)) return st;
   void* workspace = a->workspace;
@@ -258,6 +292,11 @@ static int prepare_call(const piper_prepare_args* a, bool use_scratch, void* str
   mp.block_rows = piper::cascade_block_rows(static_cast<int>(s.key_length));
   mp.chunks = piper::cascade_chunks(static_cast<int>(s.key_length));
   mp.tensors = a->is_causal ? 1 : 2;
+  mp.status = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + layout.workspace_status_offset);
+
+  piper::PrepDevice dev{};
+  if (int st = device_topology(&dev.cus, &dev.xccs)) return st;
+  dev.spin_limit = (a->flags & PIPER_PREPARE_SELF_MEAN) ? 0 : piper::kPrepSpinLimit;
 
   piper::QuantParams qp{};
   qp.query = to_input(a->query);
@@ -284,7 +323,8 @@ static int prepare_call(const piper_prepare_args* a, bool use_scratch, void* str
   qp.value_scale = o.value_scale;
   qp.kv_tiles = static_cast<uint8_t*>(o.kv_tiles);
 
-  const hipError_t err = piper::launch_prep(a->dtype == PIPER_BFLOAT16, d, mp, qp, static_cast<hipStream_t>(stream));
+  const hipError_t err =
+      piper::launch_prep(a->dtype == PIPER_BFLOAT16, d, mp, qp, dev, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "prep launch failed: %s", hipGetErrorString(err));
   g_last_error[0] = '\0';
   return PIPER_OK;
@@ -293,6 +333,29 @@ static int prepare_call(const piper_prepare_args* a, bool use_scratch, void* str
 int piper_prepare(const piper_prepare_args* a, void* stream) { return prepare_call(a, false, stream); }
 
 int piper_prepare_static(const piper_prepare_args* a, void* stream) { return prepare_call(a, true, stream); }
+
+int piper_prepare_status(const piper_shape* shape, const void* workspace, uint32_t* count, void* stream) {
+  if (count == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "count is NULL");
+  piper_layout layout;
+  if (int st = piper_prepared_layout(shape, &layout)) return st;
+  const void* base = workspace;
+  if (base == nullptr) {
+    void* scratch_address = nullptr;
+    if (layout.workspace_bytes > PIPER_STATIC_SCRATCH_BYTES)
+      return fail(PIPER_ERROR_UNSUPPORTED, "shape does not fit the static scratch of piper_prepare_static");
+    if (int st = device_scratch(&scratch_address)) return st;
+    base = scratch_address;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t word = 0;
+  hipError_t err = hipMemcpyAsync(&word, static_cast<const char*>(base) + layout.workspace_status_offset,
+                                  sizeof(word), hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  if (err != hipSuccess) return fail(PIPER_ERROR_HIP, "status read failed: %s", hipGetErrorString(err));
+  *count = word;
+  g_last_error[0] = '\0';
+  return PIPER_OK;
+}
 
 int piper_attention_forward(const piper_attention_args* a, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");

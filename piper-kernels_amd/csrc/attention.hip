@@ -31,6 +31,7 @@ namespace piper {
 
 constexpr float kLazyRescale = 8.0f;               // log2 headroom before num/den are rescaled
 constexpr float kLog2Of255 = 7.994353436858858f;   // log2(255)
+constexpr float kDirectRange = 96.0f;              // |block max| of the subtraction-free exp2 path
 
 template <int D, int NW>
 struct TileLayout : StagePieces<kv_tile_bytes(D), NW> {  // the tile record is the stage image
@@ -49,8 +50,8 @@ struct TileLayout : StagePieces<kv_tile_bytes(D), NW> {  // the tile record is t
 // 2 (q % 2) + i / 2.
 template <int D, int NW, bool kCausal>
 __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[2], const float (&ct)[4], int t,
-                                             int q0, int n, int h, float (&num)[D / 32][16], float& den,
-                                             float& mref) {
+                                             int q0, int n, int h, uint32_t sel, float (&num)[D / 32][16],
+                                             float& den, float& mref) {
   using L = TileLayout<D, NW>;
   constexpr int kChunksD = D / 32;
 
@@ -102,34 +103,68 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   // ---- e = 255 * vs * p = exp2(x - bm + log2 255), den += sum(p) * beta, UINT8 codes ----
   const bool empty = mx == -__builtin_inff();
   const float beta = empty ? 0.0f : __builtin_amdgcn_exp2f(mx - mref);
-  const float shift = empty ? 0.0f : mx - kLog2Of255;
   const float4* iv4 = reinterpret_cast<const float4*>(stage + L::kInvOffset);
   float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   uint32_t pw[8];
+  float pscale;  // sum(p) = pscale * sum(ps)
+  if (__builtin_amdgcn_ballot_w64(!empty && !(fabsf(mx) <= kDirectRange)) == 0) {
+    // E = exp2(x) and e = E * C with C = 2^(log2 255 - bm): no per-key subtraction; the code
+    // FMA multiplies by C (pack_scaled_codes) and sum(p) = C * sum(E / (255 vs)).  |bm| <= 96
+    // keeps E and C normal and finite for every key that can take a nonzero code.
+    const float c = empty ? 0.0f : __builtin_amdgcn_exp2f(kLog2Of255 - mx);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float4 ia = iv4[4 * h + q];
-    const float4 ib = iv4[8 + 4 * h + q];
-    const float e0 = __builtin_amdgcn_exp2f(x[4 * q + 0] - shift);
-    const float e1 = __builtin_amdgcn_exp2f(x[4 * q + 1] - shift);
-    const float e2 = __builtin_amdgcn_exp2f(x[4 * q + 2] - shift);
-    const float e3 = __builtin_amdgcn_exp2f(x[4 * q + 3] - shift);
-    const float f0 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 0] - shift);
-    const float f1 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 1] - shift);
-    const float f2 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 2] - shift);
-    const float f3 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 3] - shift);
-    ps[0] = fmaf(e0, ia.x, ps[0]);
-    ps[1] = fmaf(e1, ia.y, ps[1]);
-    ps[2] = fmaf(e2, ia.z, ps[2]);
-    ps[3] = fmaf(e3, ia.w, ps[3]);
-    ps[0] = fmaf(f0, ib.x, ps[0]);
-    ps[1] = fmaf(f1, ib.y, ps[1]);
-    ps[2] = fmaf(f2, ib.z, ps[2]);
-    ps[3] = fmaf(f3, ib.w, ps[3]);
-    pw[q] = pack_codes(e0, e1, e2, e3);
-    pw[4 + q] = pack_codes(f0, f1, f2, f3);
+    for (int q = 0; q < 4; ++q) {
+      const float4 ia = iv4[4 * h + q];
+      const float4 ib = iv4[8 + 4 * h + q];
+      const float e0 = __builtin_amdgcn_exp2f(x[4 * q + 0]);
+      const float e1 = __builtin_amdgcn_exp2f(x[4 * q + 1]);
+      const float e2 = __builtin_amdgcn_exp2f(x[4 * q + 2]);
+      const float e3 = __builtin_amdgcn_exp2f(x[4 * q + 3]);
+      const float f0 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 0]);
+      const float f1 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 1]);
+      const float f2 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 2]);
+      const float f3 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 3]);
+      ps[0] = fmaf(e0, ia.x, ps[0]);
+      ps[1] = fmaf(e1, ia.y, ps[1]);
+      ps[2] = fmaf(e2, ia.z, ps[2]);
+      ps[3] = fmaf(e3, ia.w, ps[3]);
+      ps[0] = fmaf(f0, ib.x, ps[0]);
+      ps[1] = fmaf(f1, ib.y, ps[1]);
+      ps[2] = fmaf(f2, ib.z, ps[2]);
+      ps[3] = fmaf(f3, ib.w, ps[3]);
+      pw[q] = pack_scaled_codes(e0, e1, e2, e3, c, sel);
+      pw[4 + q] = pack_scaled_codes(f0, f1, f2, f3, c, sel);
+    }
+    pscale = c;
+  } else {
+    // extreme block maxima: subtract the shift first, as the reference's exp(s - bm)
+    const float shift = empty ? 0.0f : mx - kLog2Of255;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 ia = iv4[4 * h + q];
+      const float4 ib = iv4[8 + 4 * h + q];
+      const float e0 = __builtin_amdgcn_exp2f(x[4 * q + 0] - shift);
+      const float e1 = __builtin_amdgcn_exp2f(x[4 * q + 1] - shift);
+      const float e2 = __builtin_amdgcn_exp2f(x[4 * q + 2] - shift);
+      const float e3 = __builtin_amdgcn_exp2f(x[4 * q + 3] - shift);
+      const float f0 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 0] - shift);
+      const float f1 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 1] - shift);
+      const float f2 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 2] - shift);
+      const float f3 = __builtin_amdgcn_exp2f(x[16 + 4 * q + 3] - shift);
+      ps[0] = fmaf(e0, ia.x, ps[0]);
+      ps[1] = fmaf(e1, ia.y, ps[1]);
+      ps[2] = fmaf(e2, ia.z, ps[2]);
+      ps[3] = fmaf(e3, ia.w, ps[3]);
+      ps[0] = fmaf(f0, ib.x, ps[0]);
+      ps[1] = fmaf(f1, ib.y, ps[1]);
+      ps[2] = fmaf(f2, ib.z, ps[2]);
+      ps[3] = fmaf(f3, ib.w, ps[3]);
+      pw[q] = pack_codes(e0, e1, e2, e3);
+      pw[4 + q] = pack_codes(f0, f1, f2, f3);
+    }
+    pscale = 1.0f;
   }
-  const float psum = cross_half_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
+  const float psum = cross_half_sum((ps[0] + ps[1]) + (ps[2] + ps[3])) * pscale;
   den = fmaf(psum, beta, den);
   const float weight = beta * (1.0f / 255.0f);
   const v4i p0 = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]), static_cast<int>(pw[3])};
@@ -175,7 +210,7 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
 template <int D, int NW, bool kCausal, bool kPerThread, bool kBarrier>
 __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, int t, int tiles, int wave_tiles, int bh,
                                               int wave, int lane, const v4i (&qf)[D / 32], float cq,
-                                              int q0, int n, int h, int krow,
+                                              int q0, int n, int h, int krow, uint32_t sel,
                                               const v16i (&s_cur)[2], v16i (&s_next)[2], float (&num)[D / 32][16],
                                               float& den, float& mref) {
   using L = TileLayout<D, NW>;
@@ -198,7 +233,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
     } else {  // per-block scales: the four slots hold the same value
       ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
     }
-    block_update<D, NW, kCausal>(stage, s_cur, ct, t, q0, n, h, num, den, mref);
+    block_update<D, NW, kCausal>(stage, s_cur, ct, t, q0, n, h, sel, num, den, mref);
   }
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }
@@ -284,6 +319,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
   // MFMA row m of the K operand holds key 16*((m>>2)&1) + 4*(m>>3) + (m&3), so that output
   // register r of lane half h holds key 16h + r.
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+  const uint32_t sel = code_selector();
 
   stage_barrier<0>();  // all prologue copies landed
 
@@ -295,13 +331,13 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
     pipeline_step<D, NW, kCausal, kPerThread, R::kEveryIteration>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq,
-                                                               q0, n, h, krow, s_a, s_b, num, den, mref);
+                                                               q0, n, h, krow, sel, s_a, s_b, num, den, mref);
     pipeline_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
-                                        h, krow, s_b, s_a, num, den, mref);
+                                        h, krow, sel, s_b, s_a, num, den, mref);
   }
   if (t < tiles)
     pipeline_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
-                                         krow, s_a, s_b, num, den, mref);
+                                         krow, sel, s_a, s_b, num, den, mref);
   // no direct copy may still be writing this workgroup's LDS when its waves end
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -400,6 +436,7 @@ attention_w3_kernel(const AttnParams p) {
   float den = 0.0f;
   float mref = -__builtin_inff();
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
+  const uint32_t sel = code_selector();
 
   for (int t = 0; t < tiles; ++t) {
     // this wave's copies of tile t landed; after the barrier every wave's have, and every read
@@ -421,7 +458,7 @@ attention_w3_kernel(const AttnParams p) {
       } else {
         ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
       }
-      block_update<D, NW, kCausal>(stage, sc, ct, t, q0, n, h, num, den, mref);
+      block_update<D, NW, kCausal>(stage, sc, ct, t, q0, n, h, sel, num, den, mref);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

@@ -66,6 +66,15 @@ __device__ __forceinline__ float cross_half_sum(float v) {
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Remap the
 // hardware block id so that consecutive logical ids -- the query blocks of one head, which
 // stream the same K/V tiles -- run on the same XCD.
+// The same for `xccs` XCCs (block b runs on XCC b % xccs); xcc_remap(b, n, 8) == xcd_remap(b, n).
+__device__ __forceinline__ int xcc_remap(int block, int blocks, int xccs) {
+  const int xcc = block % xccs;
+  const int local = block / xccs;
+  const int base = blocks / xccs;
+  const int rem = blocks - base * xccs;
+  return xcc * base + (xcc < rem ? xcc : rem) + local;
+}
+
 __device__ __forceinline__ int xcd_remap(int block, int blocks) {
   const int xcd = block & 7;
   const int local = block >> 3;

@@ -33,6 +33,9 @@ inline long prep_partial_bytes(long batch_heads, int length, int head_dim) {
   return 2 * batch_heads * (cascade_chunks(length) + 1) * head_dim * 4;
 }
 inline long prep_sync_words(long batch_heads) { return 4 * batch_heads + 4; }
+// Index of the status word among the sync words (after the 2 * batch_heads arrival counters):
+// the number of chunks of the last call that gave up waiting and computed their mean themselves.
+inline long prep_status_word(long batch_heads) { return 2 * batch_heads; }
 
 // One 64-key tile record is byte for byte the attention kernel's LDS stage, so it is copied
 // with direct global -> LDS loads in 1 KiB pieces: K codes [64][D] in rows of D + 16 bytes,
@@ -81,6 +84,7 @@ struct MeanParams {
   // value_scale = amax / 2.25 + 1e-7; 0: the V sum, finalised into value_mean
   int value_absmax;
   float* value_scale;  // [batch_heads][D] (value_absmax only)
+  uint32_t* status;    // the prep's give-up count, cleared by the finalisation (NULL: none)
 };
 
 // Scales stored per quantisation block: one per thread group of the reference's per_thread
@@ -183,7 +187,24 @@ struct SageParams {
   int fp16_partials;  // round each block's FP8 product to FP16 (the reference's arithmetic)
 };
 
-hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream);
+constexpr int kPrepSpinLimit = 1 << 20;  // polls of a waiting single-pass chunk (with s_sleep): about a second
+
+// The GPU the prep runs on, and the single-pass prep's wait bound.
+struct PrepDevice {
+  int cus;         // compute units
+  int xccs;        // XCCs (accelerator complex dies) the workgroups are dealt over, round-robin
+  int spin_limit;  // polls of a waiting chunk before it computes the mean itself (0: at once)
+};
+
+// The single-pass prep keeps each chunk of a batch-head tensor resident until the tensor's last
+// chunk has arrived, so all of a tensor's chunks must fit in one XCC at once: at least four
+// workgroups per CU (the kernel's occupancy allows more) on cus / xccs CUs.
+__host__ __device__ inline bool single_pass_resident(int chunks, int cus, int xccs) {
+  return xccs > 0 && cus >= xccs && chunks <= 4 * (cus / xccs);
+}
+
+hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, const PrepDevice& dev,
+                       hipStream_t stream);
 hipError_t launch_sage_prep(bool bf16, int head_dim, const MeanParams& mp, const SageQuantParams& qp,
                             hipStream_t stream);
 hipError_t launch_sage_attention(int head_dim, bool causal, int out_dtype, int waves, const SageParams& sp,

@@ -164,6 +164,7 @@ __device__ __forceinline__ void finalize_column(const MeanParams& p, int tensor,
 
 __global__ void __launch_bounds__(64) mean_finalize_kernel(const MeanParams p, int head_dim) {
   const int gid = blockIdx.x * 64 + threadIdx.x;
+  if (gid == 0 && p.status != nullptr) *p.status = 0u;  // this path never waits
   const int per_tensor = p.batch_heads * head_dim;
   if (gid >= 2 * per_tensor) return;
   const int tensor = gid / per_tensor;
@@ -508,11 +509,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) q
 // Causal V needs no mean and does not wait.
 //
 // Progress: a chunk waits only for chunks of its own batch-head tensor, whose workgroup ids are
-// consecutive; ids are remapped so that each XCD runs a consecutive range, and an XCD dispatches
-// its workgroups in order, so once the first chunk of a tensor runs, the rest are dispatched as
-// soon as slots free up -- and a tensor's kSinglePassChunks chunks fit in one XCD's slots (32 CUs
-// x 4 workgroups).  Every wait is bounded: past kSpinLimit polls it gives up, records a status
-// and quantises with a NaN mean, so the kernel always ends.
+// consecutive; ids are remapped with the device's XCC count so that each XCC runs a consecutive
+// range (workgroups are dealt round-robin over the XCCs, and an XCC dispatches its share in
+// order), so once the first chunk of a tensor runs, the rest are dispatched as soon as slots free
+// up -- and the host takes this path only when a tensor's chunks fit in one XCC's slots (at least
+// four workgroups per CU).  Other work holding an XCC's slots (a kernel on another stream, another
+// process) can still keep a tensor's last chunk from being dispatched, so every wait is bounded:
+// past the spin limit the chunk computes the mean itself from the rows in HBM in the same
+// cascade order (column_mean_from_rows: exact, slow), and counts itself in the status word.
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ float load_coherent(const float* p) {  // agent-scope relaxed: bypasses L2
   return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
@@ -583,12 +587,65 @@ struct SinglePassParams {
   QuantParams q;
   MeanParams m;
   uint32_t* arrivals;  // [batch_heads][2] chunks arrived (zero before the launch)
-  uint32_t* status;    // nonzero: a wait gave up (zero before the launch)
+  uint32_t* status;    // chunks whose wait gave up and computed the mean themselves (zero before the launch)
   int kv_workgroups;   // batch_heads * 2 * chunks; Q-block workgroups (4 blocks each) follow
+  int xccs;            // XCCs the workgroups are dealt over (the remap's stride)
+  int spin_limit;      // polls before a wait gives up (0: no wait, every waiter computes the mean)
 };
 
 constexpr int kSinglePassChunks = 64;
-constexpr int kSpinLimit = 1 << 20;  // polls (with s_sleep): about a second
+
+// The mean of column `col` of one batch-head's K or V straight from its rows in HBM, in the
+// cascade order of the published partials and single_pass_mean (L = 16): rows summed in
+// blocks of 16 from +0.0 (level 0), 16 blocks per chunk (level 1), 16 chunks per group (level
+// 2), the groups in order (level 3), then ((trailing rows + the short chunk's complete blocks)
+// + the unfinished group) + the complete groups, divided by the length in FP32.  Bit-identical
+// to the published mean; the fallback of a wait that gives up (one thread per column).
+template <bool kBf16>
+__device__ float block_rows_sum(const uint16_t* rows, long stride, int n) {
+  float v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t bits = r < n ? static_cast<uint32_t>(rows[static_cast<long>(r) * stride]) : 0u;
+    v[r] = kBf16 ? __uint_as_float(bits << 16) : half_bits_to_float(bits);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (r < n) acc += v[r];
+  return acc;
+}
+
+template <bool kBf16>
+__device__ float column_mean_from_rows(const InputTensor& in, int b, int h, int col, int length) {
+  constexpr int L = 16;
+  const uint16_t* base = static_cast<const uint16_t*>(in.data) + b * in.stride_batch + h * in.stride_head + col;
+  const long stride = in.stride_seq;
+  const int full = length / (L * L);  // complete chunks
+  float level3 = 0.0f, group = 0.0f;
+  for (int c = 0; c < full; ++c) {
+    float chunk_sum = 0.0f;
+    for (int blk = 0; blk < L; ++blk)
+      chunk_sum += block_rows_sum<kBf16>(base + static_cast<long>(c * L * L + blk * L) * stride, stride, L);
+    group += chunk_sum;
+    if ((c + 1) % L == 0) {
+      level3 += group;
+      group = 0.0f;
+    }
+  }
+  const float level2 = full % L != 0 ? group : 0.0f;
+  const int rows = length - full * L * L;  // the short chunk, if any
+  const int blocks = rows / L;
+  const int tail = rows - blocks * L;
+  float level1 = 0.0f;
+  for (int blk = 0; blk < blocks; ++blk)
+    level1 += block_rows_sum<kBf16>(base + static_cast<long>(full * L * L + blk * L) * stride, stride, L);
+  const float level0 =
+      tail > 0 ? block_rows_sum<kBf16>(base + static_cast<long>(full * L * L + blocks * L) * stride, stride, tail)
+               : 0.0f;
+  const float total = ((level0 + level1) + level2) + level3;
+  return total / static_cast<float>(length);
+}
 constexpr uint32_t kMeanPending = 0x7fa5a5a5u;  // a signalling NaN: the mean slot before it is published
 
 // The mean of one column from the published partials, torch's cascade order (finalize_column),
@@ -728,21 +785,26 @@ __device__ __forceinline__ void single_pass_chunk(const SinglePassParams& p, Sin
         sh.mean[col] = m;
         store_coherent(mean_out + col, m);  // replaces the pending mark: the other chunks go on
       }
-    } else if (threadIdx.x < D) {
+    } else {
       // wait for this column's mean to replace the pending mark (kMeanPending, a signalling NaN
-      // that no arithmetic produces)
-      uint32_t bits;
-      int polls = 0;
-      while ((bits = __hip_atomic_load(reinterpret_cast<const uint32_t*>(mean_out) + threadIdx.x, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT)) == kMeanPending) {
-        if (++polls > kSpinLimit) {
-          __hip_atomic_store(p.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          bits = 0x7fc00000u;  // gave up: a NaN mean
-          break;
+      // that no arithmetic produces), at most spin_limit polls
+      bool waiting = false;
+      if (threadIdx.x < D) {
+        uint32_t bits = kMeanPending;
+        for (int polls = 0; polls < p.spin_limit; ++polls) {
+          bits = __hip_atomic_load(reinterpret_cast<const uint32_t*>(mean_out) + threadIdx.x, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+          if (bits != kMeanPending) break;
+          __builtin_amdgcn_s_sleep(2);
         }
-        __builtin_amdgcn_s_sleep(2);
+        waiting = bits == kMeanPending;
+        sh.mean[threadIdx.x] = __builtin_bit_cast(float, bits);
       }
-      sh.mean[threadIdx.x] = __builtin_bit_cast(float, bits);
+      // a column still pending: the chunk computes every column's mean from the rows itself
+      if (__syncthreads_or(waiting)) {
+        if (threadIdx.x < D) sh.mean[threadIdx.x] = column_mean_from_rows<kBf16>(in, b, h, threadIdx.x, length);
+        if (threadIdx.x == 0) __hip_atomic_fetch_add(p.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __syncthreads();
   } else if (chunk == 0 && threadIdx.x < D) {
@@ -781,7 +843,7 @@ prep_single_pass_kernel(const SinglePassParams p) {
   __shared__ __attribute__((aligned(16))) SinglePassShared sh;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: index math stays scalar
   const int lane = threadIdx.x & 63;
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int logical = xcc_remap(blockIdx.x, gridDim.x, p.xccs);
   if (logical >= p.kv_workgroups) {  // the two-step path's Q blocks: no mean, no wait
     const int unit = (logical - p.kv_workgroups) * 4 + wave;
     if (unit < p.q.batch_heads * p.q.nqb) quantize_query_unit<kBf16, 128>(p.q, unit);
@@ -907,8 +969,10 @@ static hipError_t launch_mean_partials(const MeanParams& mp, hipStream_t stream)
 }
 
 template <bool kBf16, int D>
-static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {
-  if (D == 128 && mp.block_rows == 16 && mp.chunks <= kSinglePassChunks && !mp.value_absmax) {
+static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp, const PrepDevice& dev,
+                                    hipStream_t stream) {
+  if (D == 128 && mp.block_rows == 16 && mp.chunks <= kSinglePassChunks && !mp.value_absmax &&
+      single_pass_resident(mp.chunks, dev.cus, dev.xccs)) {
     SinglePassParams sp{};
     sp.q = qp;
     sp.m = mp;
@@ -916,8 +980,10 @@ static hipError_t launch_prep_typed(const MeanParams& mp, const QuantParams& qp,
     uint32_t* sync = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(mp.partials) +
                                                  prep_partial_bytes(mp.batch_heads, mp.length, D));
     sp.arrivals = sync;
-    sp.status = sync + 2 * mp.batch_heads;
+    sp.status = sync + prep_status_word(mp.batch_heads);
     sp.kv_workgroups = 2 * mp.batch_heads * mp.chunks;
+    sp.xccs = dev.xccs;
+    sp.spin_limit = dev.spin_limit;
     // a fill kernel, not hipMemsetAsync: safe to record in a captured graph
     const int means = mp.batch_heads * D;
     const int threads = words > means ? words : means;
@@ -964,11 +1030,14 @@ hipError_t launch_sage_prep(bool bf16, int head_dim, const MeanParams& mp, const
                          : launch_sage_prep_typed<false, 64>(mp, qp, stream);
 }
 
-hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, hipStream_t stream) {
+hipError_t launch_prep(bool bf16, int head_dim, const MeanParams& mp, const QuantParams& qp, const PrepDevice& dev,
+                       hipStream_t stream) {
   if (bf16) {
-    return head_dim == 128 ? launch_prep_typed<true, 128>(mp, qp, stream) : launch_prep_typed<true, 64>(mp, qp, stream);
+    return head_dim == 128 ? launch_prep_typed<true, 128>(mp, qp, dev, stream)
+                           : launch_prep_typed<true, 64>(mp, qp, dev, stream);
   }
-  return head_dim == 128 ? launch_prep_typed<false, 128>(mp, qp, stream) : launch_prep_typed<false, 64>(mp, qp, stream);
+  return head_dim == 128 ? launch_prep_typed<false, 128>(mp, qp, dev, stream)
+                         : launch_prep_typed<false, 64>(mp, qp, dev, stream);
 }
 
 }  // namespace piper

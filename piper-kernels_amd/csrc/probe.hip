@@ -25,11 +25,19 @@ constexpr int kProbeThreads = PIPER_MFMA_PROBE_THREADS;  // 8 waves: two per SIM
 // Kinds I8 and F8: four accumulator chains per wave, `iterations` rounds of four MFMAs on
 // all-ones operands; each lane stores the 32-bit sum of its 64 accumulator registers.
 // Kinds P_CODES_U8 / P_CODES_FP8: thread t packs four of its workgroup's values with the
-// kernels' packer and stores the word over word t.
+// kernels' packer and stores the word over word t.  P_CODES_U8_SCALED: thread t packs values
+// 4 (t % 64) .. + 3 times the multiplier in word 256 + 4 (t % 64).
 template <int kKind>
 __global__ void __launch_bounds__(kProbeThreads, 1) mfma_probe_kernel(uint32_t* sink, int iterations) {
   uint32_t total = 0;
-  if constexpr (kKind == PIPER_MFMA_PROBE_P_CODES_U8 || kKind == PIPER_MFMA_PROBE_P_CODES_FP8) {
+  if constexpr (kKind == PIPER_MFMA_PROBE_P_CODES_U8_SCALED) {
+    const float* values = reinterpret_cast<const float*>(sink) + static_cast<long>(blockIdx.x) * kProbeThreads;
+    const int g = threadIdx.x % 64;
+    const float a = values[4 * g], b = values[4 * g + 1], c = values[4 * g + 2], d = values[4 * g + 3];
+    const float m = values[256 + 4 * g];
+    __syncthreads();  // every read of this workgroup's words precedes every store over them
+    total = pack_scaled_codes(a, b, c, d, m, code_selector());
+  } else if constexpr (kKind == PIPER_MFMA_PROBE_P_CODES_U8 || kKind == PIPER_MFMA_PROBE_P_CODES_FP8) {
     const float* values = reinterpret_cast<const float*>(sink) + static_cast<long>(blockIdx.x) * kProbeThreads;
     const int i = 4 * (threadIdx.x % (kProbeThreads / 4));
     const float a = values[i], b = values[i + 1], c = values[i + 2], d = values[i + 3];
@@ -373,7 +381,7 @@ const char* piper_probe_last_error(void) { return piper::g_last_error; }
 
 int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint32_t* sink, void* stream) {
   using namespace piper;
-  if (kind < PIPER_MFMA_PROBE_I8 || kind > PIPER_MFMA_PROBE_P_CODES_FP8)
+  if (kind < PIPER_MFMA_PROBE_I8 || kind > PIPER_MFMA_PROBE_P_CODES_U8_SCALED)
     return fail(2, "unknown MFMA probe kind %d", kind);
   if (workgroups < 1 || workgroups > 65536 || iterations < 1 || iterations > (1 << 24))
     return fail(1, "probe needs 1..65536 workgroups and 1..2^24 iterations, got %d and %d", workgroups, iterations);
@@ -388,8 +396,11 @@ int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint3
     case PIPER_MFMA_PROBE_P_CODES_U8:
       hipLaunchKernelGGL(mfma_probe_kernel<PIPER_MFMA_PROBE_P_CODES_U8>, grid, block, 0, s, sink, iterations);
       break;
-    default:
+    case PIPER_MFMA_PROBE_P_CODES_FP8:
       hipLaunchKernelGGL(mfma_probe_kernel<PIPER_MFMA_PROBE_P_CODES_FP8>, grid, block, 0, s, sink, iterations);
+      break;
+    default:
+      hipLaunchKernelGGL(mfma_probe_kernel<PIPER_MFMA_PROBE_P_CODES_U8_SCALED>, grid, block, 0, s, sink, iterations);
       break;
   }
   const hipError_t err = hipGetLastError();

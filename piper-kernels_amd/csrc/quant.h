@@ -93,6 +93,31 @@ __device__ __forceinline__ uint32_t pack_codes(float e0, float e1, float e2, flo
   return w ^ 0x80808080u;  // u - 128 as signed INT8
 }
 
+// The byte selector of pack_scaled_codes (v_perm_b32: byte 0 of the second operand, byte 0 of
+// the first, two zero bytes), held in a VGPR: a VOP3 instruction takes no literal operand, and
+// one that reads an SGPR issues at half rate.
+__device__ __forceinline__ uint32_t code_selector() {
+  uint32_t sel = 0x0c0c0400u;
+  asm volatile("" : "+v"(sel));
+  return sel;
+}
+
+// Piper Attention's UINT8 probability codes of e_i = E_i * c (the same rule as pack_codes, for
+// products in [0, 255.5)), e0 in byte 0, as u - 128 in signed INT8.  fma(E, c, 1.5 * 2^23 - 128)
+// rounds the exact product once, into the binade [2^23, 2^24) whose spacing is 1: to the nearest
+// integer, half to even (1.5 * 2^23 - 128 is even), and the low byte of its bits is u - 128 in
+// two's complement.  The multiplier c rides in the FMA, so the caller needs no per-code scaling.
+__device__ __forceinline__ uint32_t pack_scaled_codes(float e0, float e1, float e2, float e3, float c, uint32_t sel) {
+  constexpr float kMagic = 12582784.0f;  // 1.5 * 2^23 - 128
+  const uint32_t a = __builtin_bit_cast(uint32_t, fmaf(e0, c, kMagic));
+  const uint32_t b = __builtin_bit_cast(uint32_t, fmaf(e1, c, kMagic));
+  const uint32_t d2 = __builtin_bit_cast(uint32_t, fmaf(e2, c, kMagic));
+  const uint32_t d3 = __builtin_bit_cast(uint32_t, fmaf(e3, c, kMagic));
+  const uint32_t lo = __builtin_amdgcn_perm(b, a, sel);    // [u0, u1, 0, 0] - 128
+  const uint32_t hi = __builtin_amdgcn_perm(d3, d2, sel);  // [u2, u3, 0, 0] - 128
+  return (hi << 16) | lo;
+}
+
 // SageAttention2++'s FP8 E4M3 probability codes, a in byte 0 (round to nearest even, like
 // torch's float8_e4m3fn cast).  Both 16-bit halves are written, so the word starts from an
 // undefined register (no clearing move).

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first; see module docstrin
 
 from .build import LIBRARY_PATH, PROBE_LIBRARY_PATH
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 QUERY_BLOCK = 32
 KEY_BLOCK = 64
 QUERY_SCALE_SLOTS = 8  # per 32-row Q block: one per thread group (per-block prep repeats its scale)
@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "piper_prepared_layout",
     "piper_prepare",
     "piper_prepare_static",
+    "piper_prepare_status",
     "piper_attention_forward",
     "piper_attention_forward_fused",
     "piper_sage_prepared_layout",
@@ -44,6 +45,7 @@ EXPORTED_SYMBOLS = (
 STATIC_SCRATCH_BYTES = 16 << 20  # PIPER_STATIC_SCRATCH_BYTES: piper_prepare_static's per-GPU scratch
 PREPARE_SKIP_QUERY = 1  # piper_prepare_args.flags
 PREPARE_QK_PER_THREAD = 2
+PREPARE_SELF_MEAN = 4  # diagnostic: waiting single-pass chunks compute the mean themselves (the wait's fallback)
 ATTENTION_QK_PER_THREAD = 1  # piper_attention_args.flags / piper_attention_fused_args.flags
 SAGE_FP16_PARTIALS = 2  # piper_sage_attention_args.flags: FP16-rounded 64-key partial products
 
@@ -88,6 +90,7 @@ class PiperLayout(ctypes.Structure):
         ("kv_tile_bytes", _i64),
         ("kv_tiles_bytes", _i64),
         ("workspace_bytes", _i64),
+        ("workspace_status_offset", _i64),
     ]
 
 
@@ -230,6 +233,8 @@ class NativeLibrary:
         lib.piper_prepare.restype = ctypes.c_int
         lib.piper_prepare_static.argtypes = [ctypes.POINTER(PiperPrepareArgs), _ptr]
         lib.piper_prepare_static.restype = ctypes.c_int
+        lib.piper_prepare_status.argtypes = [ctypes.POINTER(PiperShape), _ptr, ctypes.POINTER(ctypes.c_uint32), _ptr]
+        lib.piper_prepare_status.restype = ctypes.c_int
         lib.piper_attention_forward.argtypes = [ctypes.POINTER(PiperAttentionArgs), _ptr]
         lib.piper_attention_forward.restype = ctypes.c_int
         lib.piper_attention_forward_fused.argtypes = [ctypes.POINTER(PiperAttentionFusedArgs), _ptr]
@@ -270,6 +275,17 @@ class NativeLibrary:
     def prepare_static(self, args: PiperPrepareArgs, stream: int) -> None:
         """piper_prepare with the library's static per-GPU scratch (no workspace in ``args``)."""
         self._check(self._lib.piper_prepare_static(ctypes.byref(args), _ptr(stream)), "piper_prepare_static")
+
+    def prepare_status(self, shape: PiperShape, workspace: int | None, stream: int) -> int:
+        """The give-up count of the last prep on ``workspace`` (None: the static scratch of the
+        current device): chunks of the single-pass prep whose bounded wait for their tensor's
+        mean ended and that computed it themselves.  Synchronises ``stream``."""
+        count = ctypes.c_uint32(0)
+        self._check(
+            self._lib.piper_prepare_status(ctypes.byref(shape), _ptr(workspace), ctypes.byref(count), _ptr(stream)),
+            "piper_prepare_status",
+        )
+        return int(count.value)
 
     def attention_forward(self, args: PiperAttentionArgs, stream: int) -> None:
         self._check(self._lib.piper_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_attention_forward")
@@ -339,6 +355,7 @@ MFMA_PROBE_I8 = 0
 MFMA_PROBE_F8 = 1
 MFMA_PROBE_P_CODES_U8 = 2  # Piper Attention's UINT8 probability-code packer on FP32 values from the sink
 MFMA_PROBE_P_CODES_FP8 = 3  # SageAttention2++'s FP8 E4M3 probability-code packer, the same way
+MFMA_PROBE_P_CODES_U8_SCALED = 4  # Piper Attention's scaled packer: codes of E * c, 64 groups of 4 per workgroup
 MFMA_PROBE_THREADS = 512
 MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 

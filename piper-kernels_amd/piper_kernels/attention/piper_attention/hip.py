@@ -118,6 +118,7 @@ def _prepare_piper_attention(
     quantize_query: bool = True,
     qk_granularity: str = "per_thread",
     static_workspace: bool = False,
+    prep_flags: int = 0,
 ) -> PreparedPiperAttention:
     """Quantise Q/K/V on the GPU (one HIP prep pipeline) and allocate the output.
 
@@ -130,7 +131,9 @@ def _prepare_piper_attention(
     per K block, over interleaved rows) or ``"per_warp"`` (one scale per 32-row Q / 64-row K
     block, its grouped SM12x Triton path).  ``static_workspace=True`` runs ``piper_prepare_static``
     instead: no workspace is allocated, the library's static per-GPU scratch holds the mean
-    partials (same outputs; calls overlapping on one GPU race).
+    partials (same outputs; calls overlapping on one GPU race).  ``prep_flags`` adds diagnostic
+    ``PIPER_PREPARE_*`` bits (``native.PREPARE_SELF_MEAN``: every waiting single-pass chunk
+    computes its tensor's mean itself, the bounded wait's fallback; same outputs).
     """
     if qk_granularity not in ("per_warp", "per_thread"):
         raise ValueError(f"unknown Q/K quantization granularity: {qk_granularity}")
@@ -182,7 +185,9 @@ def _prepare_piper_attention(
         abi_version=native.ABI_VERSION,
         dtype=_DTYPE_CODES[query.dtype],
         is_causal=int(bool(is_causal)),
-        flags=(0 if quantize_query else native.PREPARE_SKIP_QUERY) | (native.PREPARE_QK_PER_THREAD if per_thread else 0),
+        flags=(0 if quantize_query else native.PREPARE_SKIP_QUERY)
+        | (native.PREPARE_QK_PER_THREAD if per_thread else 0)
+        | (prep_flags & native.PREPARE_SELF_MEAN),
         shape=shape,
         query=q_arg,
         key=k_arg,

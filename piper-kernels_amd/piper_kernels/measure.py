@@ -200,6 +200,41 @@ def probability_codes(values, codes: str, device: torch.device):
     return packed[: flat.size]
 
 
+def scaled_probability_codes(values, multipliers, device: torch.device):
+    """Piper Attention's UINT8 codes of the products ``values[4i + j] * multipliers[i]``,
+    computed on the GPU by the kernels' scaled packer (the subtraction-free exp2 path: one FMA
+    per code with the block's multiplier).  ``values`` holds 4N FP32 values, ``multipliers`` N;
+    returns the 4N codes u (the packer's bytes u - 128, shifted back) as uint8."""
+    import numpy as np
+
+    from ._hip import library as native
+
+    flat = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    mult = np.ascontiguousarray(multipliers, dtype=np.float32).reshape(-1)
+    if flat.size != 4 * mult.size:
+        raise ValueError(f"need four values per multiplier, got {flat.size} values and {mult.size} multipliers")
+    groups = 64  # groups of four values per workgroup
+    workgroups = max(1, -(-mult.size // groups))
+    host = np.zeros((workgroups, native.MFMA_PROBE_THREADS), dtype=np.float32)
+    padded = np.zeros(workgroups * groups * 4, dtype=np.float32)
+    padded[: flat.size] = flat
+    host[:, :256] = padded.reshape(workgroups, 256)
+    pm = np.zeros(workgroups * groups, dtype=np.float32)
+    pm[: mult.size] = mult
+    host[:, 256::4] = pm.reshape(workgroups, groups)
+    sink = torch.from_numpy(host.reshape(-1).view(np.int32)).to(device)
+    stream = torch.cuda.current_stream(device)
+    with torch.cuda.device(device):
+        native.load_probe_library().mfma_probe(native.MFMA_PROBE_P_CODES_U8_SCALED, workgroups, 1, sink.data_ptr(),
+                                               stream.cuda_stream)
+        stream.synchronize()
+    words = sink.cpu().numpy().view(np.uint32).reshape(workgroups, native.MFMA_PROBE_THREADS // groups, groups)
+    if not (words == words[:, :1]).all():  # thread t and t + 64k pack the same four values
+        raise RuntimeError("scaled probability-code probe: threads packing the same values disagree")
+    packed = np.ascontiguousarray(words[:, 0]).view(np.uint8).reshape(-1) ^ np.uint8(0x80)
+    return packed[: flat.size]
+
+
 def _time_probe(lib, kind: int, workgroups: int, iterations: int, launches: int, device: torch.device) -> float:
     """Median milliseconds of ``launches`` probe launches (after two warm-ups); the result
     words are checked against their exact value."""

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from _parity import log
-from piper_kernels.measure import probability_codes
+from piper_kernels.measure import probability_codes, scaled_probability_codes
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +52,41 @@ def test_u8_codes_round_half_to_even_and_saturate(gfx950_device) -> None:
     bad = np.flatnonzero(got != expected)
     assert bad.size == 0, f"{bad.size} codes differ, e.g. {values[bad[:8]].tolist()} -> {got[bad[:8]].tolist()}"
     assert got[:256].tolist() == [k + (k & 1) for k in range(256)][:255] + [255]  # k + 0.5 -> even neighbour
+
+
+def test_scaled_u8_codes_round_the_exact_product_half_to_even(gfx950_device) -> None:
+    """The kernel's subtraction-free path codes e = E * C with one FMA per code (E = exp2 of the
+    shifted score, C = 2^(log2 255 - block max)): the code must be the exact product rounded half
+    to even, for products in [0, 255.5)."""
+    rng = np.random.default_rng(13)
+    # the kernel's range: E = 2^x with x <= bm, C = 2^(log2 255 - bm), |bm| <= 96
+    bm = rng.uniform(-96.0, 96.0, 4000).astype(np.float32)
+    x = (bm[:, None] - rng.exponential(3.0, (4000, 4))).astype(np.float32)
+    e_kernel = np.exp2(x.astype(np.float64)).astype(np.float32)
+    c_kernel = np.exp2(np.float64(7.994353436858858) - bm.astype(np.float64)).astype(np.float32)
+    # exact ties k + 1/2 and their float neighbours, split as (k + 1/2) 2^-j times 2^j
+    k = np.arange(255, dtype=np.float64) + 0.5
+    j = rng.integers(-60, 60, k.size).astype(np.float64)
+    tie_e = (k * np.exp2(-j)).astype(np.float32)
+    tie_c = np.exp2(j).astype(np.float32)
+    tie_e = np.stack([tie_e, np.nextafter(tie_e, np.float32(0)), np.nextafter(tie_e, np.float32(np.inf)),
+                      tie_e], axis=1)
+    # empty rows: E = 0 (masked keys) with C = 0 or finite; the block maximum itself (E C ~ 255)
+    special_e = np.array([[0.0, 0.0, 2.0**90, 2.0**-90]], dtype=np.float32)
+    special_c = np.array([0.0], dtype=np.float32)
+    top_e = np.exp2(bm[:8, None].astype(np.float64) * np.ones((8, 4))).astype(np.float32)
+    values = np.concatenate([e_kernel, tie_e, np.zeros((1, 4), np.float32), special_e, top_e]).reshape(-1)
+    mults = np.concatenate([c_kernel, tie_c, np.array([1.0], np.float32), special_c, c_kernel[:8]])
+    product = values.astype(np.float64).reshape(-1, 4) * mults.astype(np.float64)[:, None]  # exact: 24 + 24 bits
+    assert product.max() < 255.5
+    log(f"[case] scaled u8 codes of {values.size} products (kernel range, ties, neighbours, empty rows)")
+    got = scaled_probability_codes(values, mults, gfx950_device)
+    expected = np.rint(product).reshape(-1).astype(np.uint8)
+    bad = np.flatnonzero(got != expected)
+    assert bad.size == 0, f"{bad.size} codes differ, e.g. {product.reshape(-1)[bad[:8]].tolist()} -> {got[bad[:8]].tolist()}"
+    ties = got[4 * 4000: 4 * (4000 + 255)].reshape(255, 4)
+    assert ties[:, 0].tolist() == [m + (m & 1) for m in range(255)]  # m + 1/2 -> the even neighbour
+    assert got[4 * (4000 + 255 + 2): 4 * (4000 + 255 + 2) + 32].tolist() == [255] * 32  # the block maxima
 
 
 def _e4m3_values() -> np.ndarray:

@@ -190,3 +190,26 @@ def test_public_operator_runs_custom_op_and_keeps_dtype(gfx950_device) -> None:
         log(f"[parity] public op {dtype}: mean={error.mean():.3e} max={error.max():.3e}")
         # the reference's own envelope for its optimised backend (test_triton.py:139-145)
         assert error.mean() < 0.003 and error.max() < 0.12
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_extreme_block_maxima_take_the_subtracting_path(causal, gfx950_device) -> None:
+    """The kernel forms P codes from E = exp2(x) and C = 2^(log2 255 - block max) while every
+    block maximum of the wave lies within +-96 (log2 units), and subtracts the maximum before
+    exp2 otherwise.  Query rows scaled 40x give block maxima of several hundred; rows left at
+    N(0, 1) stay in range, so waves of both kinds, and mixed blocks, meet the oracle's gate."""
+    torch.manual_seed(31)
+    b, h, s, d = 1, 2, 512, 128
+    q = torch.randn(b, h, s, d)
+    q[:, :, 64:192] *= 40.0  # two and a half waves of large logits
+    q[:, :, 300:301] *= 40.0  # one large row inside an otherwise ordinary wave
+    q = q.to(torch.float16)
+    k = (torch.randn(b, h, s, d) + torch.randn(b, h, 1, d)).to(torch.float16)
+    v = (torch.randn(b, h, s, d) + 2 * torch.randn(b, h, 1, d)).to(torch.float16)
+    scale = d**-0.5
+    log(f"[case] extreme block maxima causal={causal}")
+    prep = oracle.prepare(q, k, v, causal, "per_thread")
+    prepared = gpu_prepare(q, k, v, scale, causal, gfx950_device, quantize_query=False, qk_granularity="per_thread")
+    out32 = gpu_attention(prepared, torch.float32).cpu().numpy()
+    expected, bound = oracle_attention(prep, scale, causal)
+    assert_attention_close(out32, expected, f"extreme maxima causal={causal}", flip_bound=bound)

@@ -79,8 +79,8 @@ def mean_workspace_bytes(batch_heads: int, key_length: int, head_dim: int) -> in
 
 
 def prep_workspace_bytes(batch_heads: int, key_length: int, head_dim: int) -> int:
-    """piper_prepare's workspace: the mean partials, then the single-pass prep's arrival counter
-    and ready flag per batch-head tensor, a status word and padding (4 * B * H + 4 words)."""
+    """piper_prepare's workspace: the mean partials, then the single-pass prep's sync words: an
+    arrival counter per batch-head tensor, the status word and spare words (4 * B * H + 4)."""
     return mean_workspace_bytes(batch_heads, key_length, head_dim) + 4 * (4 * batch_heads + 4)
 
 
@@ -105,6 +105,19 @@ def test_prepared_layout_sizes(lib, shape) -> None:
     assert layout.kv_tile_bytes % 1024 == 0 and layout.kv_tile_bytes - raw < 1024
     assert layout.kv_tiles_bytes == b * h * (sk64 // 64) * layout.kv_tile_bytes
     assert layout.workspace_bytes == prep_workspace_bytes(b * h, sk, d)
+    # the status word follows the mean partials and the 2 * B * H arrival counters
+    assert layout.workspace_status_offset == mean_workspace_bytes(b * h, sk, d) + 4 * 2 * b * h
+    assert layout.workspace_status_offset + 4 <= layout.workspace_bytes
+
+
+def test_prepare_status_validates_before_touching_the_gpu(lib) -> None:
+    with pytest.raises(RuntimeError, match="count is NULL"):
+        lib._check(lib._lib.piper_prepare_status(ctypes.byref(native.PiperShape(1, 1, 8, 8, 64)), None, None, None),
+                   "piper_prepare_status")
+    with pytest.raises(RuntimeError, match="head_dim"):
+        lib.prepare_status(native.PiperShape(1, 1, 8, 8, 32), 0x1000, 0)
+    with pytest.raises(RuntimeError, match="static scratch"):
+        lib.prepare_status(native.PiperShape(2, 64, 32768, 32768, 128), None, 0)
 
 
 @pytest.mark.parametrize("bad", [(1, 1, 8, 8, 32), (0, 1, 8, 8, 64), (1, 1, 0, 8, 64)])
@@ -165,7 +178,7 @@ def test_attention_validates_before_launching(lib) -> None:
 
 def test_prepare_flags(lib) -> None:
     args = native.PiperPrepareArgs(abi_version=native.ABI_VERSION, dtype=native.FLOAT16, shape=native.PiperShape(1, 1, 8, 8, 64))
-    for flags in (4, 8, native.PREPARE_SKIP_QUERY | 4):
+    for flags in (8, 16, native.PREPARE_SKIP_QUERY | 8):
         args.flags = flags
         with pytest.raises(RuntimeError, match="unknown flags"):
             lib.prepare(args, 0)
@@ -187,6 +200,30 @@ def test_prepare_flags(lib) -> None:
     args.flags = 0
     args.query = native.PiperTensor(fake, 512, 512, 64)
     with pytest.raises(RuntimeError, match="prepared output pointer is NULL"):
+        lib.prepare(args, 0)
+    # the self-mean diagnostic is a known flag, alone or with the others
+    args.flags = native.PREPARE_SELF_MEAN | native.PREPARE_SKIP_QUERY | native.PREPARE_QK_PER_THREAD
+    with pytest.raises(RuntimeError, match="workspace"):
+        lib.prepare(args, 0)
+
+
+def test_prepare_rejects_misaligned_means_and_workspace(lib) -> None:
+    """The prep polls the means and counts arrivals in the workspace with 32-bit atomics: a
+    key_mean that is not 4-byte aligned and a workspace that is not 16-byte aligned are refused
+    on the host (a caller sub-allocating from a byte arena must keep them aligned)."""
+    fake = 0x1000
+    tensor = native.PiperTensor(fake, 512, 512, 64)
+    args = native.PiperPrepareArgs(
+        abi_version=native.ABI_VERSION, dtype=native.FLOAT16, flags=native.PREPARE_SKIP_QUERY,
+        shape=native.PiperShape(1, 1, 8, 8, 64), key=tensor, value=tensor,
+        prepared=native.PiperPrepared(None, None, fake, fake, fake + 2, fake, fake),
+        workspace=fake, workspace_bytes=1 << 20,
+    )
+    with pytest.raises(RuntimeError, match="key_mean must be 4-byte aligned"):
+        lib.prepare(args, 0)
+    args.prepared = native.PiperPrepared(None, None, fake, fake, fake + 4, fake, fake)
+    args.workspace = fake + 8
+    with pytest.raises(RuntimeError, match="workspace must be 16-byte aligned"):
         lib.prepare(args, 0)
 
 
@@ -354,8 +391,9 @@ def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
     roles = ["IDLE", "MFMA", "FMA", "EXP", "CVT", "MIX", "VALU_MIX", "LDS", "MFMA_FMA", "MIX_VGPR", "CLUSTER", "ADD_LIT",
              "ADD_SGPR"]
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "piper_probe.h"', "int main(void) {",
-             '  printf("%d %d %d %d %d %d %d %d\\n", PIPER_PROBE_ABI_VERSION, PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8,'
-             ' PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8, PIPER_MFMA_PROBE_THREADS,'
+             '  printf("%d %d %d %d %d %d %d %d %d\\n", PIPER_PROBE_ABI_VERSION, PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8,'
+             ' PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8, PIPER_MFMA_PROBE_P_CODES_U8_SCALED,'
+             ' PIPER_MFMA_PROBE_THREADS,'
              ' PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8));']
     lines.append('  printf("' + " ".join(["%d"] * (len(roles) + 3)) + '\\n", '
                  + ", ".join(f"PIPER_ISSUE_{r}" for r in roles)
@@ -369,15 +407,16 @@ def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
     exe = tmp_path / "probe"
     subprocess.run(["gcc", f"-I{REPO / 'include'}", str(source), "-o", str(exe)], check=True)
     values = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()))
-    assert values[:8] == [native.PROBE_ABI_VERSION, native.MFMA_PROBE_I8, native.MFMA_PROBE_F8,
-                          native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8, native.MFMA_PROBE_THREADS,
+    assert values[:9] == [native.PROBE_ABI_VERSION, native.MFMA_PROBE_I8, native.MFMA_PROBE_F8,
+                          native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8,
+                          native.MFMA_PROBE_P_CODES_U8_SCALED, native.MFMA_PROBE_THREADS,
                           native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8]]
     n = len(roles)
-    assert values[8:8 + n] == list(range(len(native.ISSUE_ROLES)))
+    assert values[9:9 + n] == list(range(len(native.ISSUE_ROLES)))
     assert [r.upper() for r in native.ISSUE_ROLES] == roles
-    assert values[8 + n:11 + n] == [len(native.ISSUE_ROLES), native.ISSUE_MAX_WAVES_PER_SIMD,
+    assert values[9 + n:12 + n] == [len(native.ISSUE_ROLES), native.ISSUE_MAX_WAVES_PER_SIMD,
                                     native.ISSUE_RECORDS_PER_WORKGROUP]
-    offsets = values[11 + n:]
+    offsets = values[12 + n:]
     expected = []
     for cls in (native.PiperIssueRecord, native.PiperIssueProbeArgs):
         expected.append(ctypes.sizeof(cls))
@@ -389,7 +428,7 @@ def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
 
 def test_mfma_probe_validates_before_launching(probe) -> None:
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
-        probe.mfma_probe(4, 1, 1, 0x1000, 0)
+        probe.mfma_probe(5, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="unknown MFMA probe kind"):
         probe.mfma_probe(-1, 1, 1, 0x1000, 0)
     with pytest.raises(RuntimeError, match="workgroups and"):

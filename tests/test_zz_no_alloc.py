@@ -1,6 +1,8 @@
-"""piper_prepare_static (no caller workspace: the mean partials live in the library's static
+"""piper_prepare_static (no caller workspace: the prep's workspace lives in the library's static
 per-GPU scratch) against piper_prepare, through the C ABI on MI355X: every prepared byte the
-header specifies and the attention output equal, on two calls in a row, the second smaller."""
+header specifies and the attention output equal, on calls in a row, each smaller than the one
+before (non-causal single pass, the three-kernel path at D = 64, causal single pass); and a call
+on preallocated buffers makes no allocation at all."""
 
 from __future__ import annotations
 
@@ -16,6 +18,7 @@ CASES = [
     # (B, H, Sq, Sk, D, dtype, causal): the second is smaller and reuses the scratch the first filled
     (1, 4, 4096, 4096, 128, torch.float16, False),
     (1, 2, 300, 193, 64, torch.bfloat16, False),
+    (1, 2, 192, 192, 128, torch.bfloat16, True),
 ]
 
 
@@ -58,3 +61,38 @@ def test_static_scratch_prep_equals_workspace_prep(gfx950_device) -> None:
         out_static = gpu_attention(static, torch.float32)
         out_reference = gpu_attention(reference, torch.float32)
         assert torch.equal(out_static, out_reference), f"attention output differs (call {i + 1})"
+
+
+def test_static_prep_allocates_nothing(gfx950_device) -> None:
+    """A second piper_prepare_static on buffers a first call left: torch's allocator records no
+    allocation and no reserved byte more across it, and the outputs repeat bit for bit."""
+    from piper_kernels._hip import library as native
+    from piper_kernels.attention.piper_attention.hip import _native_input
+
+    case = (1, 2, 1024, 1024, 128, torch.float16, False)
+    log(f"[case] piper_prepare_static on preallocated buffers: {case}")
+    b, h, sq, sk, d, dtype, causal = case
+    q, k, v = (t.to(gfx950_device) for t in _inputs(case, 900))
+    first = _prepare(q, k, v, d, causal, gfx950_device, static=True)
+    # every buffer the prep writes (the output is the attention kernel's, left uninitialised here)
+    saved = {name: value.clone() for name, value in vars(first).items()
+             if isinstance(value, torch.Tensor) and name != "output"}
+    q, q_arg = _native_input(q)
+    k, k_arg = _native_input(k)
+    v, v_arg = _native_input(v)
+    args = native.PiperPrepareArgs(
+        abi_version=native.ABI_VERSION, dtype=native.FLOAT16, is_causal=0, flags=native.PREPARE_QK_PER_THREAD,
+        shape=native.PiperShape(b, h, sq, sk, d), query=q_arg, key=k_arg, value=v_arg,
+        prepared=first.native_prepared(), workspace=None, workspace_bytes=0,
+    )
+    lib = native.load_library()
+    stream = torch.cuda.current_stream(gfx950_device)
+    torch.cuda.synchronize(gfx950_device)
+    before = torch.cuda.memory_stats(gfx950_device)
+    lib.prepare_static(args, stream.cuda_stream)
+    torch.cuda.synchronize(gfx950_device)
+    after = torch.cuda.memory_stats(gfx950_device)
+    for key in ("allocation.all.allocated", "reserved_bytes.all.allocated", "segment.all.allocated"):
+        assert after.get(key, 0) == before.get(key, 0), f"{key}: {before.get(key)} -> {after.get(key)}"
+    for name, value in saved.items():
+        assert torch.equal(getattr(first, name).view(torch.uint8), value.view(torch.uint8)), f"{name} changed"
