@@ -53,7 +53,9 @@ sys.path[:0] = [str(REPO), str(REPO / "piper-kernels_amd")]
 
 INT8_PEAK_TOPS = 5033.2  # MI355X dense INT8 MFMA: 256 CU x 2.4 GHz x 8192 ops/clk/CU
 HBM_PEAK_GBPS = 8000.0
-# benchmarks/README.md:521 of the reference: B1 H8 N8192 D128 BF16 non-causal, centred V
+# The reference's published Piper Attention figures (RTX 5090, BF16 non-causal, p50), by the
+# workload of the same shape: benchmarks/README.md:521 (B1 H8 N8192 D128, centred V) and :526
+# (B1 H1 N131072 D128, uncentred V, the reference's development control of the same cost)
 REFERENCE_R1 = {
     "hardware": "RTX 5090 (SM120), Torch 2.12.1+cu130, Triton 3.7.1",
     "hot_ms": 0.674,
@@ -63,6 +65,16 @@ REFERENCE_R1 = {
     "sqnr_db_vs_sdpa": 36.08,
     "source": "benchmarks/README.md:521",
 }
+REFERENCE_R2 = {
+    "hardware": "RTX 5090 (SM120), Torch 2.12.1+cu130, Triton 3.7.1",
+    "hot_ms": 19.579,
+    "hot_tops": 449.3,
+    "complete_ms": 19.824,
+    "complete_tops": 443.7,
+    "sqnr_db_vs_sdpa": 35.48,
+    "source": "benchmarks/README.md:526 (uncentred V)",
+}
+REFERENCE_PUBLISHED = {"r1": REFERENCE_R1, "r2": REFERENCE_R2}
 
 
 def log(msg: str) -> None:
@@ -78,8 +90,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument(
         "--workload",
         default="c3",
-        choices=["c1", "c2", "c3", "c4", "c5", "r1"],
-        help="BASELINE.json's configurations c1-c5, or r1: the shape of the reference's published RTX 5090 figures",
+        choices=["c1", "c2", "c3", "c4", "c5", "r1", "r2"],
+        help="BASELINE.json's configurations c1-c5, or r1 / r2: the shapes of the reference's published RTX 5090 "
+        "figures (B1 H8 N8192, B1 H1 N131072)",
     )
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
@@ -534,15 +547,15 @@ def main() -> int:
     else:
         result["config"]["plan"] = select_plan(b, h, sq, sk, d, workload.is_causal).as_dict()
         result["config"]["qk_granularity"] = args.qk_granularity
-        if workload.name == "r1":
-            # the reference's only published Piper Attention figures are for this shape, on another GPU
-            # (benchmarks/README.md:521: RTX 5090, BF16, centred V, p50): complete call 0.775 ms, hot
-            # prepared kernel 0.674 ms, SQNR vs SDPA 36.08 dB
-            result["vs_baseline"] = round(value / REFERENCE_R1["complete_tops"], 3)
+        if workload.name in REFERENCE_PUBLISHED:
+            # the reference's only published Piper Attention figures are for these shapes, on another
+            # GPU (RTX 5090, BF16, p50): the complete call and the hot prepared kernel
+            published = REFERENCE_PUBLISHED[workload.name]
+            result["vs_baseline"] = round(value / published["complete_tops"], 3)
             result["reference_published"] = {
-                **REFERENCE_R1,
-                "kernel_speedup": round(REFERENCE_R1["hot_ms"] / attn_mean, 3),
-                "complete_speedup": round(REFERENCE_R1["complete_ms"] / ms_per_step, 3),
+                **published,
+                "kernel_speedup": round(published["hot_ms"] / attn_mean, 3),
+                "complete_speedup": round(published["complete_ms"] / ms_per_step, 3),
             }
     result["environment"] = environment(device)
     if not args.no_probes:

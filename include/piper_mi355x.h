@@ -35,6 +35,9 @@
  *                               (triton.py:797-874); the sizes the caller must provide
  *   piper_prepare_status     <- no reference counterpart: how many chunks of the last prep gave
  *                               up waiting for their tensor's mean and computed it themselves
+ *   piper_attention_workspace_bytes
+ *                            <- no reference counterpart: the partial-sum workspace of the
+ *                               key-range split plans (small grids)
  *   piper_abi_version,
  *   piper_last_error         <- no reference counterpart: version handshake and the error
  *                               text the Python layer raises as RuntimeError
@@ -52,7 +55,7 @@
 extern "C" {
 #endif
 
-#define PIPER_ABI_VERSION 3
+#define PIPER_ABI_VERSION 4
 
 /* Rows per quantisation group (sage/reference.py:6-7) and keys per P block (reference.py:16). */
 #define PIPER_QUERY_BLOCK 32
@@ -196,7 +199,15 @@ typedef struct piper_prepare_args {
                                           PIPER_PLAN_NO_XCD_REMAP) instead of head by head */
 #define PIPER_PLAN_THREE_WORKGROUPS 16 /* three 4-wave workgroups per CU (three waves per SIMD, 2-stage LDS
                                           rings); overrides PIPER_PLAN_FOUR_WAVES.  Both operators */
-#define PIPER_PLAN_MASK 31
+/* Key-range split (Piper Attention, non-causal, with PIPER_PLAN_THREE_WORKGROUPS): the key tiles
+ * of each query tile are cut into `parts` ranges (2..8), one workgroup each, which write their
+ * FP32 partial numerator, denominator and reference maximum to the call's workspace; a merge
+ * kernel combines them (piper_attention_workspace_bytes gives the size).  For grids too small to
+ * give every SIMD three waves.  The merge adds the parts in another order than one sequential
+ * pass, so split plans agree with the others to rounding, not bit for bit. */
+#define PIPER_PLAN_KEY_PARTS(parts) (((parts) - 1) << 5)
+#define PIPER_PLAN_KEY_PARTS_OF(plan) ((((plan) >> 5) & 7) + 1)
+#define PIPER_PLAN_MASK 255
 
 /* piper_attention_args.flags / piper_attention_fused_args.flags */
 #define PIPER_ATTENTION_QK_PER_THREAD 1 /* Q/K scales per thread group: read slot (row % 8) of the
@@ -213,6 +224,9 @@ typedef struct piper_attention_args {
   int32_t flags;        /* PIPER_ATTENTION_QK_PER_THREAD if the prep ran with PIPER_PREPARE_QK_PER_THREAD */
   piper_prepared prepared; /* inputs, as written by piper_prepare */
   void* output;            /* [B, H, Sq, D] dense row-major, output_dtype */
+  void* workspace;         /* key-range split plans: piper_attention_workspace_bytes bytes, 16-byte
+                              aligned; otherwise unused (NULL) */
+  int64_t workspace_bytes;
 } piper_attention_args;
 
 /* The fused entry point: like piper_attention_forward, but each query wave quantises its own
@@ -232,6 +246,8 @@ typedef struct piper_attention_fused_args {
   piper_tensor query;      /* [B, H, Sq, D], the layout rules of piper_prepare_args.query */
   piper_prepared prepared; /* from piper_prepare; query_code and query_scale are not read */
   void* output;            /* [B, H, Sq, D] dense row-major, output_dtype */
+  void* workspace;         /* as piper_attention_args.workspace */
+  int64_t workspace_bytes;
 } piper_attention_fused_args;
 
 /* ---------------------------------------------------------------------------------------
@@ -343,6 +359,10 @@ int piper_prepare_static(const piper_prepare_args* args, void* stream);
 
 /* Fused INT8-QK / UINT8-P x INT8-V online-softmax attention on `stream`. */
 int piper_attention_forward(const piper_attention_args* args, void* stream);
+
+/* Workspace bytes the attention entry points need for `plan` (0 unless the plan splits the key
+ * range: parts * B * H * Sq * (D + 2) * 4). */
+int piper_attention_workspace_bytes(const piper_shape* shape, int32_t plan, int64_t* bytes);
 
 /* The same with the query quantised inside the kernel (see piper_attention_fused_args). */
 int piper_attention_forward_fused(const piper_attention_fused_args* args, void* stream);

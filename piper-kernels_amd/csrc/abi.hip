@@ -132,7 +132,8 @@ piper::InputTensor to_input(const piper_tensor& t) {
 // piper_attention_forward_fused (query != NULL: the kernel quantises the query itself).
 int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_causal, int32_t plan, int32_t flags,
                           const piper_shape& s, float scale, const piper_prepared& o, void* output,
-                          const piper_tensor* query, int32_t query_dtype, void* stream) {
+                          const piper_tensor* query, int32_t query_dtype, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
   if (abi_version != PIPER_ABI_VERSION)
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "ABI version mismatch: caller %d, library %d", abi_version,
                 PIPER_ABI_VERSION);
@@ -145,6 +146,18 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
   if (plan < 0 || plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", plan);
   if ((flags & ~PIPER_ATTENTION_QK_PER_THREAD) != 0) return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", flags);
+  const int key_parts = PIPER_PLAN_KEY_PARTS_OF(plan);
+  if (key_parts > 1) {
+    if (is_causal) return fail(PIPER_ERROR_UNSUPPORTED, "the key-range split plans are non-causal");
+    if (!(plan & PIPER_PLAN_THREE_WORKGROUPS))
+      return fail(PIPER_ERROR_UNSUPPORTED, "the key-range split needs PIPER_PLAN_THREE_WORKGROUPS");
+    int64_t need = 0;
+    if (int st = piper_attention_workspace_bytes(&s, plan, &need)) return st;
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(PIPER_ERROR_INVALID_ARGUMENT, "the key-range split needs a workspace of %lld bytes, got %lld",
+                  (long long)need, (long long)workspace_bytes);
+    if (!aligned16(workspace)) return fail(PIPER_ERROR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  }
   if (query != nullptr) {
     if (query_dtype != PIPER_FLOAT16 && query_dtype != PIPER_BFLOAT16)
       return fail(PIPER_ERROR_UNSUPPORTED, "query dtype must be float16 or bfloat16");
@@ -188,7 +201,14 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
     ap.query_bf16 = query_dtype == PIPER_BFLOAT16 ? 1 : 0;
     ap.query = to_input(*query);
   }
-  if (static_cast<int64_t>(ap.query_tiles) * ap.batch_heads > 0x7fffffff)
+  // key-range split: part_tiles tiles per part, and no empty part
+  ap.key_parts = 1;
+  if (key_parts > 1) {
+    ap.part_tiles = static_cast<int>(ceil_div(ap.nkb, key_parts));
+    ap.key_parts = static_cast<int>(ceil_div(ap.nkb, ap.part_tiles));
+    ap.partials = static_cast<float*>(workspace);
+  }
+  if (static_cast<int64_t>(ap.query_tiles) * ap.batch_heads * ap.key_parts > 0x7fffffff)
     return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
 
   const hipError_t err = piper::launch_attention(static_cast<int>(s.head_dim), is_causal != 0, output_dtype, waves,
@@ -360,13 +380,24 @@ int piper_prepare_status(const piper_shape* shape, const void* workspace, uint32
 int piper_attention_forward(const piper_attention_args* a, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
   return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->flags, a->shape,
-                               a->scale, a->prepared, a->output, nullptr, 0, stream);
+                               a->scale, a->prepared, a->output, nullptr, 0, a->workspace, a->workspace_bytes, stream);
+}
+
+int piper_attention_workspace_bytes(const piper_shape* shape, int32_t plan, int64_t* bytes) {
+  if (int st = check_shape(shape)) return st;
+  if (bytes == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "bytes is NULL");
+  if (plan < 0 || plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", plan);
+  *bytes = piper::attention_partial_bytes(shape->batch * shape->heads, shape->query_length,
+                                          static_cast<int>(shape->head_dim), PIPER_PLAN_KEY_PARTS_OF(plan));
+  g_last_error[0] = '\0';
+  return PIPER_OK;
 }
 
 int piper_attention_forward_fused(const piper_attention_fused_args* a, void* stream) {
   if (a == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "args is NULL");
   return launch_attention_call(a->abi_version, a->output_dtype, a->is_causal, a->plan, a->flags, a->shape,
-                               a->scale, a->prepared, a->output, &a->query, a->dtype, stream);
+                               a->scale, a->prepared, a->output, &a->query, a->dtype, a->workspace,
+                               a->workspace_bytes, stream);
 }
 
 int piper_sage_prepared_layout(const piper_shape* shape, piper_sage_layout* layout) {
@@ -465,6 +496,8 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   if (!(std::isfinite(a->scale) && a->scale > 0.0f))
     return fail(PIPER_ERROR_INVALID_ARGUMENT, "scale must be finite and positive");
   if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
+  if (PIPER_PLAN_KEY_PARTS_OF(a->plan) > 1)
+    return fail(PIPER_ERROR_UNSUPPORTED, "SageAttention2++ has no key-range split plans");
   if ((a->flags & ~(PIPER_ATTENTION_QK_PER_THREAD | PIPER_SAGE_FP16_PARTIALS)) != 0)
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   if (int st = check_input("query", a->query)) return st;

@@ -51,7 +51,7 @@ struct TileLayout : StagePieces<kv_tile_bytes(D), NW> {  // the tile record is t
 template <int D, int NW, bool kCausal>
 __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[2], const float (&ct)[4], int t,
                                              int q0, int n, int h, uint32_t sel, float (&num)[D / 32][16],
-                                             float& den, float& mref) {
+                                             float& den, float& mref, float& mlim) {
   using L = TileLayout<D, NW>;
   constexpr int kChunksD = D / 32;
 
@@ -89,10 +89,14 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   const float mx = cross_half_max(max32(x));
 
   // ---- lazy rescale of num/den when the block maximum outgrows the reference by 2^8 ----
-  const bool grow = mx > mref + kLazyRescale;
+  // (mlim = mref + 2^8 is kept beside mref)
+  const bool grow = mx > mlim;
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
     const float alpha = grow ? __builtin_amdgcn_exp2f(mref - mx) : 1.0f;
-    if (grow) mref = mx;
+    if (grow) {
+      mref = mx;
+      mlim = mx + kLazyRescale;
+    }
 #pragma unroll
     for (int j = 0; j < kChunksD; ++j)
 #pragma unroll
@@ -166,11 +170,11 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   }
   const float psum = cross_half_sum((ps[0] + ps[1]) + (ps[2] + ps[3])) * pscale;
   den = fmaf(psum, beta, den);
-  const float weight = beta * (1.0f / 255.0f);
+  const float weight = beta;  // the reference's 1/255 is applied once, in the epilogue
   const v4i p0 = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]), static_cast<int>(pw[3])};
   const v4i p1 = {static_cast<int>(pw[4]), static_cast<int>(pw[5]), static_cast<int>(pw[6]), static_cast<int>(pw[7])};
 
-  // ---- numerator: O^T += (V^T (u - 128) + 128 colsum) * beta / 255, two D chunks' MFMA chains
+  // ---- numerator: O^T += (V^T (u - 128) + 128 colsum) * beta (x 1/255 at the end), two D chunks' MFMA chains
   // in flight at a time (the score and probability registers are dead here) ----
   const v4i* corr4 = reinterpret_cast<const v4i*>(stage + L::kCorrOffset);
 #pragma unroll
@@ -212,7 +216,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
                                               int wave, int lane, const v4i (&qf)[D / 32], float cq,
                                               int q0, int n, int h, int krow, uint32_t sel,
                                               const v16i (&s_cur)[2], v16i (&s_next)[2], float (&num)[D / 32][16],
-                                              float& den, float& mref) {
+                                              float& den, float& mref, float& mlim) {
   using L = TileLayout<D, NW>;
   using R = Ring<NW>;
   // unconditional (clamped) so every iteration issues the same number of copies; a clamped
@@ -233,7 +237,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
     } else {  // per-block scales: the four slots hold the same value
       ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
     }
-    block_update<D, NW, kCausal>(stage, s_cur, ct, t, q0, n, h, sel, num, den, mref);
+    block_update<D, NW, kCausal>(stage, s_cur, ct, t, q0, n, h, sel, num, den, mref, mlim);
   }
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }
@@ -315,6 +319,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
     for (int r = 0; r < 16; ++r) num[j][r] = 0.0f;
   float den = 0.0f;
   float mref = -__builtin_inff();
+  float mlim = -__builtin_inff();
 
   // MFMA row m of the K operand holds key 16*((m>>2)&1) + 4*(m>>3) + (m&3), so that output
   // register r of lane half h holds key 16h + r.
@@ -331,20 +336,20 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
     pipeline_step<D, NW, kCausal, kPerThread, R::kEveryIteration>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq,
-                                                               q0, n, h, krow, sel, s_a, s_b, num, den, mref);
+                                                               q0, n, h, krow, sel, s_a, s_b, num, den, mref, mlim);
     pipeline_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
-                                        h, krow, sel, s_b, s_a, num, den, mref);
+                                        h, krow, sel, s_b, s_a, num, den, mref, mlim);
   }
   if (t < tiles)
     pipeline_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
-                                         krow, sel, s_a, s_b, num, den, mref);
+                                         krow, sel, s_a, s_b, num, den, mref, mlim);
   // no direct copy may still be writing this workgroup's LDS when its waves end
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue: num / max(den, 1e-30) + mean(V), one query per lane ----
   const int query = q0 + n;
   if (!wave_live || query >= p.query_length) return;
-  const float rden = 1.0f / fmaxf(den, 1e-30f);
+  const float rden = (1.0f / 255.0f) / fmaxf(den, 1e-30f);  // the numerator holds 255 x the reference's
   const float* vmean = p.value_mean + static_cast<long>(bh) * D;
   const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
 #pragma unroll
@@ -370,6 +375,11 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
 // of tile t - 1 done), start the copy of tile t + 1 into the stage tile t - 1 used, then the
 // scores, softmax and PV of tile t.  The arithmetic is block_update's, so the output is
 // bit-identical to the other plans.
+// kOut: 0, 1, 2 = fp16, bf16, fp32 output; kPartials = the key-range split's partial sums
+// (non-causal only): the workgroup covers key tiles [part * part_tiles, +part_tiles) of its query
+// tile and writes its numerator, denominator and reference maximum for attention_merge_kernel.
+constexpr int kPartials = 3;
+
 template <int D, bool kCausal, int kOut, bool kPerThread>
 __global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3, 3)))
 attention_w3_kernel(const AttnParams p) {
@@ -377,20 +387,41 @@ attention_w3_kernel(const AttnParams p) {
   using L = TileLayout<D, NW>;
   constexpr int kChunksD = D / 32;
   constexpr int kStages = 2;
+  static_assert(kOut != kPartials || !kCausal, "the key-range split is non-causal");
   __shared__ __attribute__((aligned(16))) char smem[kStages * L::kStageBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5;
   const int n = lane & 31;
-  const TileCoord tc = workgroup_tile<kCausal>(p);
+  int part = 0;
+  TileCoord tc;
+  if constexpr (kOut == kPartials) {
+    // logical id -> (batch-head, key part, query tile): the workgroups of one key range of a
+    // head are neighbours, so an XCD's workgroups stream the same tiles through its L2
+    const int logical = p.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
+    const int per_head = p.key_parts * p.query_tiles;
+    tc.bh = logical / per_head;
+    const int rem = logical - tc.bh * per_head;
+    part = rem / p.query_tiles;
+    tc.qtile = rem - part * p.query_tiles;
+  } else {
+    tc = workgroup_tile<kCausal>(p);
+  }
   const int bh = __builtin_amdgcn_readfirstlane(tc.bh);
   const int qtile = __builtin_amdgcn_readfirstlane(tc.qtile);
+  part = __builtin_amdgcn_readfirstlane(part);
   const int q0 = qtile * (NW * 32) + wave * 32;
   const bool wave_live = q0 < p.query_length;
 
+  // key tiles [t0, t0 + tiles) of this workgroup, local index i = t - t0
+  int t0 = 0;
   int tiles = p.nkb;
-  int wave_tiles = wave_live ? p.nkb : 0;
+  if constexpr (kOut == kPartials) {
+    t0 = part * p.part_tiles;
+    tiles = max(0, min(p.part_tiles, p.nkb - t0));
+  }
+  int wave_tiles = wave_live ? tiles : 0;
   if constexpr (kCausal) {
     const int last_query = min(p.query_length, (qtile + 1) * NW * 32) - 1;
     tiles = last_query / kKeyBlock + 1;
@@ -416,10 +447,12 @@ attention_w3_kernel(const AttnParams p) {
     for (int c = 0; c < kChunksD; ++c) qf[c] = v4i{0, 0, 0, 0};
   }
 
-  copy_block<L>(p, smem, bh, 0, wave, lane);  // tile 0 into stage 0
+  if (tiles > 0) copy_block<L>(p, smem, bh, t0, wave, lane);  // tile t0 into stage 0
   if (fused_live) {
-    // wait for the query loads only (issued before this wave's copies of tile 0)
-    if (wave < L::kFullWaves)
+    // wait for the query loads only (issued before this wave's copies of tile t0)
+    if (tiles == 0)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (wave < L::kFullWaves)
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds - 1) : "memory");
@@ -435,17 +468,19 @@ attention_w3_kernel(const AttnParams p) {
     for (int r = 0; r < 16; ++r) num[j][r] = 0.0f;
   float den = 0.0f;
   float mref = -__builtin_inff();
+  float mlim = -__builtin_inff();
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
   const uint32_t sel = code_selector();
 
-  for (int t = 0; t < tiles; ++t) {
-    // this wave's copies of tile t landed; after the barrier every wave's have, and every read
-    // of tile t - 1 (stage (t + 1) % 2) is done
-    if constexpr (!kCausal) progress_priority(t, 1, tiles);  // causal: workgroups differ in length
+  for (int i = 0; i < tiles; ++i) {
+    // this wave's copies of tile i landed; after the barrier every wave's have, and every read
+    // of tile i - 1 (stage (i + 1) % 2) is done
+    if constexpr (!kCausal) progress_priority(i, 1, tiles);  // causal: workgroups differ in length
     stage_barrier<0>();
-    if (t + 1 < tiles) copy_block<L>(p, smem + ((t + 1) & 1) * L::kStageBytes, bh, t + 1, wave, lane);
-    if (t < wave_tiles) {
-      const char* stage = smem + (t & 1) * L::kStageBytes;
+    if (i + 1 < tiles) copy_block<L>(p, smem + ((i + 1) & 1) * L::kStageBytes, bh, t0 + i + 1, wave, lane);
+    const int t = t0 + i;
+    if (i < wave_tiles) {
+      const char* stage = smem + (i & 1) * L::kStageBytes;
       v16i sc[2];
       block_scores<D, L>(stage, qf, h, krow, sc);
       float ct[4];
@@ -458,33 +493,98 @@ attention_w3_kernel(const AttnParams p) {
       } else {
         ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
       }
-      block_update<D, NW, kCausal>(stage, sc, ct, t, q0, n, h, sel, num, den, mref);
+      block_update<D, NW, kCausal>(stage, sc, ct, t, q0, n, h, sel, num, den, mref, mlim);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const int query = q0 + n;
   if (!wave_live || query >= p.query_length) return;
-  const float rden = 1.0f / fmaxf(den, 1e-30f);
-  const float* vmean = p.value_mean + static_cast<long>(bh) * D;
-  const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
+  if constexpr (kOut == kPartials) {
+    const long rows = static_cast<long>(p.batch_heads) * p.query_length;
+    const long row = static_cast<long>(part) * rows + static_cast<long>(bh) * p.query_length + query;
+    float* dst = p.partials + row * D;
 #pragma unroll
-  for (int j = 0; j < kChunksD; ++j) {
+    for (int j = 0; j < kChunksD; ++j)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = 32 * j + 8 * g + 4 * h;
-      float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
-      if constexpr (!kCausal) m = *reinterpret_cast<const float4*>(vmean + d0);
-      store4<kOut>(p.output, out_row + d0, fmaf(num[j][4 * g + 0], rden, m.x), fmaf(num[j][4 * g + 1], rden, m.y),
-                   fmaf(num[j][4 * g + 2], rden, m.z), fmaf(num[j][4 * g + 3], rden, m.w));
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(dst + 32 * j + 8 * g + 4 * h) =
+            make_float4(num[j][4 * g + 0], num[j][4 * g + 1], num[j][4 * g + 2], num[j][4 * g + 3]);
+    // both lane halves hold the row's den and mref
+    if (h == 0) reinterpret_cast<float2*>(p.partials + p.key_parts * rows * D)[row] = make_float2(den, mref);
+    return;
+  } else {
+    const float rden = (1.0f / 255.0f) / fmaxf(den, 1e-30f);  // the numerator holds 255 x the reference's
+    const float* vmean = p.value_mean + static_cast<long>(bh) * D;
+    const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
+#pragma unroll
+    for (int j = 0; j < kChunksD; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * j + 8 * g + 4 * h;
+        float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (!kCausal) m = *reinterpret_cast<const float4*>(vmean + d0);
+        store4<kOut>(p.output, out_row + d0, fmaf(num[j][4 * g + 0], rden, m.x), fmaf(num[j][4 * g + 1], rden, m.y),
+                     fmaf(num[j][4 * g + 2], rden, m.z), fmaf(num[j][4 * g + 3], rden, m.w));
+      }
     }
   }
 }
 
+// The key-range split's merge, one thread per four features of a query row: the parts' reference
+// maxima m_p are aligned on their maximum M with weights 2^(m_p - M) (0 for a part that saw no
+// key), then num = sum w_p num_p, den = sum w_p den_p, and the epilogue of the unsplit kernel:
+// num / (255 max(den, 1e-30)) + mean(V).  The parts' sums enter in another order than one
+// sequential pass, so split plans agree with the others to rounding, not bit for bit.
+template <int D, int kOut>
+__global__ void __launch_bounds__(256) attention_merge_kernel(const AttnParams p) {
+  const long rows = static_cast<long>(p.batch_heads) * p.query_length;
+  const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * (D / 4)) return;
+  const long row = i / (D / 4);
+  const int d0 = static_cast<int>(i - row * (D / 4)) * 4;
+  const int bh = static_cast<int>(row / p.query_length);
+  const float2* stats = reinterpret_cast<const float2*>(p.partials + p.key_parts * rows * D);
+  float top = -__builtin_inff();
+  for (int q = 0; q < p.key_parts; ++q) top = fmaxf(top, stats[q * rows + row].y);
+  float den = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int q = 0; q < p.key_parts; ++q) {
+    const float2 st = stats[q * rows + row];
+    const float w = st.y == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(st.y - top);
+    den = fmaf(st.x, w, den);
+    const float4 v = *reinterpret_cast<const float4*>(p.partials + (q * rows + row) * D + d0);
+    acc.x = fmaf(v.x, w, acc.x);
+    acc.y = fmaf(v.y, w, acc.y);
+    acc.z = fmaf(v.z, w, acc.z);
+    acc.w = fmaf(v.w, w, acc.w);
+  }
+  const float rden = (1.0f / 255.0f) / fmaxf(den, 1e-30f);
+  const float4 m = *reinterpret_cast<const float4*>(p.value_mean + static_cast<long>(bh) * D + d0);
+  store4<kOut>(p.output, row * D + d0, fmaf(acc.x, rden, m.x), fmaf(acc.y, rden, m.y), fmaf(acc.z, rden, m.z),
+               fmaf(acc.w, rden, m.w));
+}
+
 template <int D, bool kCausal, bool kPerThread>
 static hipError_t launch_w3(int out_dtype, const AttnParams& ap, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(ap.query_tiles * ap.batch_heads));
   const dim3 block(256);
+  if constexpr (!kCausal) {
+    if (ap.key_parts > 1) {
+      const dim3 grid(static_cast<unsigned>(ap.query_tiles * ap.batch_heads * ap.key_parts));
+      hipLaunchKernelGGL((attention_w3_kernel<D, false, kPartials, kPerThread>), grid, block, 0, stream, ap);
+      hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return err;
+      const long threads = static_cast<long>(ap.batch_heads) * ap.query_length * (D / 4);
+      const dim3 merge_grid(static_cast<unsigned>((threads + 255) / 256));
+      switch (out_dtype) {
+        case 0: hipLaunchKernelGGL((attention_merge_kernel<D, 0>), merge_grid, block, 0, stream, ap); break;
+        case 1: hipLaunchKernelGGL((attention_merge_kernel<D, 1>), merge_grid, block, 0, stream, ap); break;
+        default: hipLaunchKernelGGL((attention_merge_kernel<D, 2>), merge_grid, block, 0, stream, ap); break;
+      }
+      return hipGetLastError();
+    }
+  }
+  const dim3 grid(static_cast<unsigned>(ap.query_tiles * ap.batch_heads));
   switch (out_dtype) {
     case 0: hipLaunchKernelGGL((attention_w3_kernel<D, kCausal, 0, kPerThread>), grid, block, 0, stream, ap); break;
     case 1: hipLaunchKernelGGL((attention_w3_kernel<D, kCausal, 1, kPerThread>), grid, block, 0, stream, ap); break;

@@ -51,10 +51,14 @@ __device__ __forceinline__ uint32_t float_to_bf16_bits(float x) {
 }
 
 // Max / sum of a value over the two 32-lane halves of a wave (lane l and l ^ 32).
+// (The final max is one v_max_f32 written as assembly: fmaxf would first quiet each swapped
+// operand with a v_max_f32 of itself, since the compiler cannot tell they hold no signalling NaN.)
 __device__ __forceinline__ float cross_half_max(float v) {
   const uint32_t u = __float_as_uint(v);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(r[0])), "v"(__uint_as_float(r[1])));
+  return m;
 }
 
 __device__ __forceinline__ float cross_half_sum(float v) {

@@ -147,7 +147,20 @@ struct AttnParams {
   int query_bf16;
   int heads;
   InputTensor query;
+  // Key-range split (non-causal, three workgroups per CU): each query tile's key tiles are cut
+  // into key_parts ranges of part_tiles tiles, one workgroup per range, which writes its
+  // unnormalised numerator (x 255), denominator and reference maximum to `partials`
+  // ([key_parts][batch_heads][query_length][D] floats, then [key_parts][batch_heads][query_length]
+  // float2 (den, mref)); attention_merge_kernel combines them.  key_parts = 1: no split.
+  int key_parts;
+  int part_tiles;
+  float* partials;
 };
+
+// The workspace bytes of a key-range split (0 without one).
+inline long attention_partial_bytes(long batch_heads, long query_length, int head_dim, int key_parts) {
+  return key_parts > 1 ? static_cast<long>(key_parts) * batch_heads * query_length * (head_dim + 2) * 4 : 0;
+}
 
 // SageAttention2++: the prep quantises K (per 64-row block, after K smoothing) and V (FP8
 // per channel) into tile records; the attention kernel quantises each query block itself.

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first; see module docstrin
 
 from .build import LIBRARY_PATH, PROBE_LIBRARY_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 QUERY_BLOCK = 32
 KEY_BLOCK = 64
 QUERY_SCALE_SLOTS = 8  # per 32-row Q block: one per thread group (per-block prep repeats its scale)
@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "piper_prepare_status",
     "piper_attention_forward",
     "piper_attention_forward_fused",
+    "piper_attention_workspace_bytes",
     "piper_sage_prepared_layout",
     "piper_sage_prepare",
     "piper_sage_attention_forward",
@@ -141,6 +142,8 @@ class PiperAttentionArgs(ctypes.Structure):
         ("flags", _i32),
         ("prepared", PiperPrepared),
         ("output", _ptr),
+        ("workspace", _ptr),
+        ("workspace_bytes", _i64),
     ]
 
 
@@ -158,6 +161,8 @@ class PiperAttentionFusedArgs(ctypes.Structure):
         ("query", PiperTensor),
         ("prepared", PiperPrepared),
         ("output", _ptr),
+        ("workspace", _ptr),
+        ("workspace_bytes", _i64),
     ]
 
 
@@ -239,6 +244,8 @@ class NativeLibrary:
         lib.piper_attention_forward.restype = ctypes.c_int
         lib.piper_attention_forward_fused.argtypes = [ctypes.POINTER(PiperAttentionFusedArgs), _ptr]
         lib.piper_attention_forward_fused.restype = ctypes.c_int
+        lib.piper_attention_workspace_bytes.argtypes = [ctypes.POINTER(PiperShape), _i32, ctypes.POINTER(_i64)]
+        lib.piper_attention_workspace_bytes.restype = ctypes.c_int
         lib.piper_sage_prepared_layout.argtypes = [ctypes.POINTER(PiperShape), ctypes.POINTER(PiperSageLayout)]
         lib.piper_sage_prepared_layout.restype = ctypes.c_int
         lib.piper_sage_prepare.argtypes = [ctypes.POINTER(PiperSagePrepareArgs), _ptr]
@@ -286,6 +293,13 @@ class NativeLibrary:
             "piper_prepare_status",
         )
         return int(count.value)
+
+    def attention_workspace_bytes(self, shape: PiperShape, plan: int) -> int:
+        """Workspace bytes of the attention entry points for ``plan`` (key-range split plans only)."""
+        value = _i64(0)
+        self._check(self._lib.piper_attention_workspace_bytes(ctypes.byref(shape), plan, ctypes.byref(value)),
+                    "piper_attention_workspace_bytes")
+        return int(value.value)
 
     def attention_forward(self, args: PiperAttentionArgs, stream: int) -> None:
         self._check(self._lib.piper_attention_forward(ctypes.byref(args), _ptr(stream)), "piper_attention_forward")

@@ -8,7 +8,9 @@ by ``piper_kernels.attention.piper_attention.tune``, the counterpart of the refe
 ``benchmarks/tune_piper_attention.py``) and falls back to a heuristic for other shapes;
 ``select_sage_plan`` does the same for SageAttention2++ with ``mi355x_sage_plans.json`` (the
 counterpart of ``sage_attention_2pp/_policy.py`` and ``benchmarks/tune_sage_attention_2pp.py``).
-Every plan computes bit-identical results; only the speed differs.
+Every plan without a key-range split computes bit-identical results; only the speed differs.
+The key-range split plans (``key_parts`` > 1, for grids too small to give every SIMD three waves)
+merge partial sums in another order and agree with the others to rounding.
 """
 
 from __future__ import annotations
@@ -30,7 +32,10 @@ PLAN_CAUSAL_FORWARD = 2
 PLAN_NO_XCD_REMAP = 4
 PLAN_CAUSAL_INTERLEAVE = 8
 PLAN_THREE_WORKGROUPS = 16
-PLAN_MASK = 31
+PLAN_KEY_PARTS_SHIFT = 5  # bits 5-7: key parts - 1 (PIPER_PLAN_KEY_PARTS)
+PLAN_MASK = 255
+MAX_KEY_PARTS = 8
+WAVE_SLOTS = 3 * 4 * COMPUTE_UNITS  # three waves on each of the 1024 SIMDs
 
 
 @dataclass(frozen=True)
@@ -46,7 +51,9 @@ class MI355XPlan:
     by head (a shorter tail for short and medium sequences; less L2 reuse for long ones).
     ``three_per_cu`` (4-wave workgroups only): three workgroups per CU, so three waves share each
     SIMD (a 2-stage LDS ring per workgroup and no score look-ahead, to fit 168 VGPRs) instead of
-    two.
+    two.  ``key_parts`` (three per CU, non-causal): the key tiles of each query tile are cut into
+    that many ranges, one workgroup each, whose FP32 partial sums a merge kernel combines; for
+    grids with too few query waves to give every SIMD three (results equal to rounding).
     """
 
     waves: int = 8
@@ -54,12 +61,17 @@ class MI355XPlan:
     xcd_remap: bool = True
     causal_interleave: bool = False
     three_per_cu: bool = False
+    key_parts: int = 1
 
     def __post_init__(self) -> None:
         if self.waves not in (4, 8):
             raise ValueError(f"waves must be 4 or 8, got {self.waves}")
         if self.three_per_cu and self.waves != 4:
             raise ValueError("three workgroups per CU need 4-wave workgroups")
+        if not 1 <= self.key_parts <= MAX_KEY_PARTS:
+            raise ValueError(f"key_parts must be 1..{MAX_KEY_PARTS}, got {self.key_parts}")
+        if self.key_parts > 1 and not self.three_per_cu:
+            raise ValueError("the key-range split runs three workgroups per CU")
 
     @property
     def block_m(self) -> int:
@@ -74,6 +86,7 @@ class MI355XPlan:
             | (0 if self.xcd_remap else PLAN_NO_XCD_REMAP)
             | (PLAN_CAUSAL_INTERLEAVE if self.causal_interleave else 0)
             | (PLAN_THREE_WORKGROUPS if self.three_per_cu else 0)
+            | ((self.key_parts - 1) << PLAN_KEY_PARTS_SHIFT)
         )
 
     @classmethod
@@ -87,16 +100,25 @@ class MI355XPlan:
             xcd_remap=not plan_id & PLAN_NO_XCD_REMAP,
             causal_interleave=bool(plan_id & PLAN_CAUSAL_INTERLEAVE),
             three_per_cu=three,
+            key_parts=(plan_id >> PLAN_KEY_PARTS_SHIFT) + 1,
         )
 
     @classmethod
     def all_plans(cls) -> list["MI355XPlan"]:
-        """Every distinct plan, by plan id (PIPER_PLAN_THREE_WORKGROUPS implies 4-wave workgroups, so
-        ids that also carry PIPER_PLAN_FOUR_WAVES name the same plans and are left out)."""
-        return [cls.from_id(i) for i in range(PLAN_MASK + 1) if not (i & PLAN_THREE_WORKGROUPS and i & PLAN_FOUR_WAVES)]
+        """Every distinct plan without a key-range split, by plan id: the plans that compute
+        bit-identical results (PIPER_PLAN_THREE_WORKGROUPS implies 4-wave workgroups, so ids that
+        also carry PIPER_PLAN_FOUR_WAVES name the same plans and are left out)."""
+        return [cls.from_id(i) for i in range(PLAN_THREE_WORKGROUPS * 2)
+                if not (i & PLAN_THREE_WORKGROUPS and i & PLAN_FOUR_WAVES)]
+
+    @classmethod
+    def split_plans(cls) -> list["MI355XPlan"]:
+        """The key-range split plans: three workgroups per CU, 2..8 key parts, either workgroup order."""
+        return [cls(waves=4, three_per_cu=True, key_parts=k, xcd_remap=x)
+                for k in range(2, MAX_KEY_PARTS + 1) for x in (True, False)]
 
     def workgroups(self, batch: int, heads: int, query_length: int) -> int:
-        return batch * heads * (-(-query_length // self.block_m))
+        return batch * heads * (-(-query_length // self.block_m)) * self.key_parts
 
     def as_dict(self) -> dict:
         return {**asdict(self), "block_m": self.block_m, "block_n": KEY_BLOCK}
@@ -141,21 +163,50 @@ def heuristic_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
     return MI355XPlan(waves=4)
 
 
-def piper_heuristic_plan(batch: int, heads: int, query_length: int, is_causal: bool) -> MI355XPlan:
+def split_parts(batch: int, heads: int, query_length: int, key_length: int) -> int:
+    """Key parts for an untuned non-causal shape (1: no split).  A grid whose 128-query tiles
+    fall short of one round of three workgroups per CU (768) and whose 256-query tiles leave CUs
+    idle splits into 2-4 parts, each of at least two key tiles (c1, 64 tiles: 4 parts, 0.017 vs
+    0.029 ms).  A long key range (>= 32768 keys,
+    where the partial sums' HBM round trip is small against the work) splits in the 2-4 parts
+    that fill the last round best, when that beats the unsplit grid's last round by 10% of a
+    round (B1 H1 N131072: 1024 tiles = 1.33 rounds; 3 parts = 4 full rounds, 7.14 vs 7.97 ms).
+    At 8192 keys the round trip costs more than the fuller round gains (r1: 3 parts 0.262 vs
+    0.254 ms), so mid-length grids stay whole."""
+    tiles = batch * heads * (-(-query_length // MI355XPlan(waves=4, three_per_cu=True).block_m))
+    key_tiles = -(-key_length // KEY_BLOCK)
+    round_slots = 3 * COMPUTE_UNITS
+    if tiles < round_slots and MI355XPlan(waves=8).workgroups(batch, heads, query_length) < COMPUTE_UNITS:
+        parts = min(4, max(2, round_slots // tiles), key_tiles // 2)
+        return parts if parts >= 2 else 1
+    if key_length >= 32768:
+        def fill(p: int) -> float:
+            rounds = tiles * p / round_slots
+            return rounds / -(-rounds // 1)
+        best = max((2, 3, 4), key=lambda p: (round(fill(p), 6), -p))
+        if fill(best) >= fill(1) + 0.1 and key_tiles >= 2 * best:
+            return best
+    return 1
+
+
+def piper_heuristic_plan(batch: int, heads: int, query_length: int, is_causal: bool,
+                         key_length: int | None = None) -> MI355XPlan:
     """Piper Attention's plan for an untuned shape: three 4-wave workgroups per CU.  With three
     waves per SIMD from three independent workgroups, one wave's MFMA, LDS and barrier waits are
-    filled by the other two: measured 7-24% faster than the two-waves-per-SIMD plans at c2-c5 and
-    within 1% of the best at c1 (tiny grid).  A non-causal grid whose 128-query tiles cannot fill
-    three slots per CU, but whose 256-query tiles give every CU one, runs two waves per SIMD
+    filled by the other two: measured 7-24% faster than the two-waves-per-SIMD plans at c2-c5.
+    Non-causal grids too small or too ragged for whole rounds of three workgroups per CU split
+    their key range (``split_parts``).  Otherwise a non-causal grid whose 128-query tiles cannot
+    fill three slots per CU, but whose 256-query tiles give every CU one, runs two waves per SIMD
     either way; one 8-wave workgroup per CU is then 1-2% faster (measured at r1, B1 H8 N8192)."""
     three = MI355XPlan(waves=4, three_per_cu=True)
     wide = MI355XPlan(waves=8)
-    if (
-        not is_causal
-        and three.workgroups(batch, heads, query_length) < 3 * COMPUTE_UNITS
-        and wide.workgroups(batch, heads, query_length) >= COMPUTE_UNITS
-    ):
-        return wide
+    if not is_causal:
+        parts = split_parts(batch, heads, query_length, query_length if key_length is None else key_length)
+        if parts > 1:
+            return MI355XPlan(waves=4, three_per_cu=True, key_parts=parts)
+        if (three.workgroups(batch, heads, query_length) < 3 * COMPUTE_UNITS
+                and wide.workgroups(batch, heads, query_length) >= COMPUTE_UNITS):
+            return wide
     return three
 
 
@@ -170,7 +221,7 @@ def sage_plan(batch: int, heads: int, query_length: int) -> MI355XPlan:
 def select_plan(batch: int, heads: int, query_length: int, key_length: int, head_dim: int, is_causal: bool) -> MI355XPlan:
     """The frozen table's plan for a tuned shape, else Piper Attention's heuristic."""
     plan = frozen_plans().get(shape_key(batch, heads, query_length, key_length, head_dim, is_causal))
-    return plan if plan is not None else piper_heuristic_plan(batch, heads, query_length, is_causal)
+    return plan if plan is not None else piper_heuristic_plan(batch, heads, query_length, is_causal, key_length)
 
 
 def select_sage_plan(batch: int, heads: int, query_length: int, key_length: int, head_dim: int,

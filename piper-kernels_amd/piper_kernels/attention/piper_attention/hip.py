@@ -224,6 +224,12 @@ def _launch_piper_attention(
         raise ValueError("output must be a contiguous [B, H, Sq, D] float16/bfloat16/float32 tensor")
     device = out.device
     flags = native.ATTENTION_QK_PER_THREAD if prepared.qk_granularity == "per_thread" else 0
+    # key-range split plans: FP32 partial sums of each key part, merged by the library's kernel
+    workspace = None
+    if prepared.plan.key_parts > 1:
+        size = lib.attention_workspace_bytes(_native_shape(batch, heads, sq, sk, d), prepared.plan.plan_id)
+        workspace = torch.empty(size, dtype=torch.uint8, device=device)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel())
     if prepared.fused_query:
         query = prepared.query
         fused = native.PiperAttentionFusedArgs(
@@ -239,11 +245,15 @@ def _launch_piper_attention(
             query=native.PiperTensor(query.data_ptr(), *query.stride()[:3]),
             prepared=prepared.native_prepared(),
             output=out.data_ptr(),
+            workspace=ws_ptr,
+            workspace_bytes=ws_bytes,
         )
         with torch.cuda.device(device):
             stream = torch.cuda.current_stream(device)
             lib.attention_forward_fused(fused, stream.cuda_stream)
         query.record_stream(stream)
+        if workspace is not None:
+            workspace.record_stream(stream)
         return out
     args = native.PiperAttentionArgs(
         abi_version=native.ABI_VERSION,
@@ -255,9 +265,14 @@ def _launch_piper_attention(
         flags=flags,
         prepared=prepared.native_prepared(),
         output=out.data_ptr(),
+        workspace=ws_ptr,
+        workspace_bytes=ws_bytes,
     )
     with torch.cuda.device(device):
-        lib.attention_forward(args, torch.cuda.current_stream(device).cuda_stream)
+        stream = torch.cuda.current_stream(device)
+        lib.attention_forward(args, stream.cuda_stream)
+    if workspace is not None:
+        workspace.record_stream(stream)
     return out
 
 

@@ -16,7 +16,9 @@ SageAttention2++ kernel over the same axes (the counterpart of the reference's
 For each shape: synthetic inputs are prepared once (K and V; the kernel quantises the query,
 as the operator runs it); every candidate plan is launched on the same prepared operands and
 gated: its FP32 output must equal the default plan's bit for bit (every plan performs the
-same arithmetic per query; only the order of workgroups differs).  Timing: the GPU first runs
+same arithmetic per query; only the order of workgroups differs), except Piper Attention's
+non-causal key-range split plans (2, 3, 4, 6 or 8 key parts), which merge partial sums in
+another order and must stay within 1e-5 (relative to the output's magnitude) of it.  Timing: the GPU first runs
 the candidates for ``--warmup-ms`` so the clock has ramped, then ``--rounds`` rounds each
 launch every candidate ``--launches`` times back to back, bracketed by HIP events on the
 launch stream with no host synchronisation inside a round (the GPU never idles between
@@ -39,17 +41,25 @@ if __package__ in (None, ""):
     sys.path.insert(0, str(Path(__file__).resolve().parents[3]))
 
 
-def candidate_plans(is_causal: bool):
+SPLIT_PARTS = (2, 3, 4, 6, 8)  # key parts of the split candidates
+SPLIT_TOLERANCE = 1e-5  # split plans: max |difference| to the default plan, relative to max(1, max |output|)
+
+
+def candidate_plans(is_causal: bool, operator: str = "piper_attention"):
     from piper_kernels.attention.piper_attention._plan import MI355XPlan
 
     # causal orders: (longest first, interleaved across heads); both flags only matter when causal
     orders = ((True, False), (True, True), (False, False)) if is_causal else ((True, False),)
     # occupancy: one 8-wave workgroup, two 4-wave workgroups or three 4-wave workgroups per CU
     occupancy = ((8, False), (4, False), (4, True))
-    return [
+    plans = [
         MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x, causal_interleave=i, three_per_cu=t)
         for (w, t), (o, i), x in product(occupancy, orders, (True, False))
     ]
+    if operator == "piper_attention" and not is_causal:
+        plans += [MI355XPlan(waves=4, three_per_cu=True, key_parts=k, xcd_remap=x)
+                  for k, x in product(SPLIT_PARTS, (True, False))]
+    return plans
 
 
 def _operator_entry_points(operator: str):
@@ -84,15 +94,19 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
     sk = k.shape[2]
     default, prepare, launch = _operator_entry_points(operator)
     prepared = prepare(q, k, v, d**-0.5, is_causal, default)
-    plans = candidate_plans(is_causal)
+    plans = candidate_plans(is_causal, operator)
     reference = torch.empty(q.shape, device=q.device, dtype=torch.float32)
     launch(prepared, output=reference)
     candidate_out = torch.empty_like(reference)
+    bound = SPLIT_TOLERANCE * max(1.0, float(reference.abs().max()))
     passed = {}
     for plan in plans:
         launch(replace(prepared, plan=plan), output=candidate_out)
         torch.cuda.synchronize()
-        passed[plan] = bool(torch.equal(candidate_out, reference))
+        if plan.key_parts > 1:
+            passed[plan] = bool((candidate_out - reference).abs().max() <= bound)
+        else:
+            passed[plan] = bool(torch.equal(candidate_out, reference))
     times = {plan: [] for plan in plans}
     runs = {plan: replace(prepared, plan=plan) for plan in plans}
     stream = torch.cuda.current_stream()
@@ -127,9 +141,11 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
     return {
         "key": {"batch_heads": batch_heads, "query_length": ql, "key_length": kl, "head_dim": hd, "is_causal": causal},
         "plan": {"waves": best.waves, "causal_longest_first": best.causal_longest_first, "xcd_remap": best.xcd_remap,
-                 "causal_interleave": best.causal_interleave, "three_per_cu": best.three_per_cu},
+                 "causal_interleave": best.causal_interleave, "three_per_cu": best.three_per_cu,
+                 **({"key_parts": best.key_parts} if best.key_parts > 1 else {})},
         "candidates": [
-            {"plan_id": p.plan_id, **p.as_dict(), "median_ms": round(medians[p], 5), "bitwise_equal_to_default": passed[p]}
+            {"plan_id": p.plan_id, **p.as_dict(), "median_ms": round(medians[p], 5),
+             ("within_split_tolerance" if p.key_parts > 1 else "bitwise_equal_to_default"): passed[p]}
             for p in plans
         ],
         "default_ms": round(medians[default], 5),

@@ -65,6 +65,9 @@ WORKLOADS: dict[str, Workload] = {
     # (benchmarks/lib/attention.py:99-120)
     "r1": Workload("r1", 1, 8, 8192, 8192, 128, torch.bfloat16, False, 11, "plain",
                    "B1 H8 S8192 D128 bf16 non-causal; QKV~N(0,1) (the reference's published benchmark shape)"),
+    # the reference's published long-sequence point (benchmarks/README.md:526): one head of 131072
+    "r2": Workload("r2", 1, 1, 131072, 131072, 128, torch.bfloat16, False, 12, "plain",
+                   "B1 H1 S131072 D128 bf16 non-causal; QKV~N(0,1) (the reference's published long-sequence shape)"),
 }
 
 

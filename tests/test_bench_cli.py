@@ -22,7 +22,7 @@ def test_more_than_one_gpu_is_refused_with_a_message() -> None:
 def test_workloads_are_the_baseline_configs_and_the_reference_shape() -> None:
     result = _run("--help")
     assert result.returncode == 0
-    for name in ("c1", "c2", "c3", "c4", "c5", "r1"):
+    for name in ("c1", "c2", "c3", "c4", "c5", "r1", "r2"):
         assert name in result.stdout
 
 
@@ -31,10 +31,14 @@ def test_reference_figures_match_the_baseline_document() -> None:
     sys.path.insert(0, str(ROOT))
     import bench
 
-    ref = bench.REFERENCE_R1
-    ops = 4 * 1 * 8 * 8192 * 8192 * 128
-    assert abs(ops / (ref["complete_ms"] * 1e-3) / 1e12 - ref["complete_tops"]) < 0.5
-    assert abs(ops / (ref["hot_ms"] * 1e-3) / 1e12 - ref["hot_tops"]) < 0.5
+    from piper_kernels.workloads import WORKLOADS
+
+    for name, ref in bench.REFERENCE_PUBLISHED.items():
+        b, h, sq, sk, d = WORKLOADS[name].shape
+        ops = 4 * b * h * sq * sk * d
+        assert abs(ops / (ref["complete_ms"] * 1e-3) / 1e12 - ref["complete_tops"]) < 0.5, name
+        assert abs(ops / (ref["hot_ms"] * 1e-3) / 1e12 - ref["hot_tops"]) < 0.5, name
+    assert WORKLOADS["r2"].shape == (1, 1, 131072, 131072, 128) and not WORKLOADS["r2"].is_causal
 
 
 def test_source_digest_identifies_the_tree() -> None:

@@ -233,25 +233,44 @@ def test_plan_selection() -> None:
     assert _plan.heuristic_plan(1, 24, 16384) == MI355XPlan(waves=8)
     assert _plan.heuristic_plan(1, 2, 193) == MI355XPlan(waves=4)
     # Piper Attention's untuned shapes: three 4-wave workgroups per CU
-    for shape in ((1, 24, 16384, False), (1, 24, 16384, True), (2, 32, 8192, False), (1, 1, 32768, False)):
+    for shape in ((1, 24, 16384, False), (1, 24, 16384, True), (2, 32, 8192, False), (2, 40, 32768, False)):
         assert _plan.piper_heuristic_plan(*shape) == MI355XPlan(waves=4, three_per_cu=True)
+    # ... with the key range split when the grid is below one round and 256-query tiles leave CUs
+    # idle (c1: 64 tiles, 4 parts), or the keys are long and the last round would be ragged
+    # (B1 H1 N131072: 1024 tiles = 1.33 rounds, 3 parts = 4 rounds)
+    split = lambda parts: MI355XPlan(waves=4, three_per_cu=True, key_parts=parts)  # noqa: E731
+    assert _plan.piper_heuristic_plan(1, 8, 1024, False) == split(4)
+    assert _plan.piper_heuristic_plan(1, 1, 131072, False, 131072) == split(3)
+    assert _plan.piper_heuristic_plan(1, 1, 32768, False) == split(3)
+    assert _plan.piper_heuristic_plan(1, 2, 193, False) == split(2)  # 4 key tiles: at most 2 parts
+    assert _plan.piper_heuristic_plan(1, 1, 64, False) == MI355XPlan(waves=4, three_per_cu=True)  # one key tile
+    assert _plan.piper_heuristic_plan(1, 8, 1024, True) == MI355XPlan(waves=4, three_per_cu=True)  # causal: whole
+    assert _plan.split_parts(1, 24, 4096, 4096) == 1 and _plan.split_parts(1, 24, 16384, 16384) == 1
     # ... except non-causal grids of 256-1535 query tiles of 256 rows that cannot fill three
     # 128-row slots per CU: one 8-wave workgroup per CU (r1, B1 H8 N8192, measured)
     assert _plan.piper_heuristic_plan(1, 8, 8192, False) == MI355XPlan(waves=8)
     assert _plan.piper_heuristic_plan(1, 8, 8192, True) == MI355XPlan(waves=4, three_per_cu=True)
     assert _plan.piper_heuristic_plan(1, 24, 4096, False) == MI355XPlan(waves=4, three_per_cu=True)  # 768 tiles
-    assert _plan.piper_heuristic_plan(1, 8, 1024, False) == MI355XPlan(waves=4, three_per_cu=True)  # tiny grid
     assert _plan.sage_plan(1, 24, 16384) == MI355XPlan(waves=4, three_per_cu=True)  # SageAttention2++: three per CU
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
-                                        "causal_interleave": False, "three_per_cu": False, "block_m": 256,
-                                        "block_n": 64}
+                                        "causal_interleave": False, "three_per_cu": False, "key_parts": 1,
+                                        "block_m": 256, "block_n": 64}
     assert MI355XPlan(4, three_per_cu=True).plan_id == 16 and MI355XPlan(4, three_per_cu=True).block_m == 128
     with pytest.raises(ValueError):
         MI355XPlan(waves=2)
     with pytest.raises(ValueError):
         MI355XPlan(waves=8, three_per_cu=True)
-    for bad in (17, 32, -1):
+    # the key-range split: three per CU only, 1..8 parts, parts - 1 in bits 5-7
+    split = MI355XPlan(4, three_per_cu=True, key_parts=3)
+    assert split.plan_id == 16 | (2 << 5) and MI355XPlan.from_id(split.plan_id) == split
+    assert split.workgroups(1, 1, 131072) == 3 * 1024
+    for bad_parts in (0, 9):
+        with pytest.raises(ValueError):
+            MI355XPlan(4, three_per_cu=True, key_parts=bad_parts)
+    with pytest.raises(ValueError):
+        MI355XPlan(8, key_parts=2)
+    for bad in (17, 32, -1, 256, 1 << 5):
         with pytest.raises(ValueError):
             MI355XPlan.from_id(bad)
 
@@ -261,13 +280,18 @@ def test_plan_ids_round_trip_and_match_the_header() -> None:
 
     header = (REPO / "include" / "piper_mi355x.h").read_text()
     for name, value in (("FOUR_WAVES", 1), ("CAUSAL_FORWARD", 2), ("NO_XCD_REMAP", 4), ("CAUSAL_INTERLEAVE", 8),
-                        ("THREE_WORKGROUPS", 16), ("MASK", 31)):
+                        ("THREE_WORKGROUPS", 16), ("MASK", 255)):
         assert f"#define PIPER_PLAN_{name} {value}" in header
+    assert "#define PIPER_PLAN_KEY_PARTS(parts) (((parts) - 1) << 5)" in header
+    assert "#define PIPER_PLAN_KEY_PARTS_OF(plan) ((((plan) >> 5) & 7) + 1)" in header
     assert (_plan.PLAN_FOUR_WAVES, _plan.PLAN_CAUSAL_FORWARD, _plan.PLAN_NO_XCD_REMAP) == (1, 2, 4)
-    assert (_plan.PLAN_CAUSAL_INTERLEAVE, _plan.PLAN_THREE_WORKGROUPS, _plan.PLAN_MASK) == (8, 16, 31)
-    plans = MI355XPlan.all_plans()
-    assert len(set(plans)) == len(plans) == 24
-    for plan in plans:
+    assert (_plan.PLAN_CAUSAL_INTERLEAVE, _plan.PLAN_THREE_WORKGROUPS, _plan.PLAN_MASK) == (8, 16, 255)
+    assert _plan.PLAN_KEY_PARTS_SHIFT == 5
+    plans = MI355XPlan.all_plans()  # the bit-identical plans
+    assert len(set(plans)) == len(plans) == 24 and all(p.key_parts == 1 for p in plans)
+    split = MI355XPlan.split_plans()
+    assert len(set(split)) == len(split) == 14 and all(p.three_per_cu and p.key_parts > 1 for p in split)
+    for plan in plans + split:
         assert MI355XPlan.from_id(plan.plan_id) == plan
 
 

@@ -160,9 +160,23 @@ def test_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 32
+    args.plan = 256
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward(args, 0)
+    # the key-range split: three workgroups per CU, non-causal, with a workspace
+    args.plan = 32
+    with pytest.raises(RuntimeError, match="needs PIPER_PLAN_THREE_WORKGROUPS"):
+        lib.attention_forward(args, 0)
+    args.plan = 16 | 32
+    with pytest.raises(RuntimeError, match="workspace of 4224 bytes, got 0"):  # 2 parts x 8 rows x (64 + 2) floats
+        lib.attention_forward(args, 0)
+    args.workspace, args.workspace_bytes = 0x1008, 1 << 20
+    with pytest.raises(RuntimeError, match="workspace must be 16-byte aligned"):
+        lib.attention_forward(args, 0)
+    args.is_causal = 1
+    with pytest.raises(RuntimeError, match="non-causal"):
+        lib.attention_forward(args, 0)
+    args.is_causal, args.workspace, args.workspace_bytes = 0, None, 0
     args.plan = 0
     args.flags = 2
     with pytest.raises(RuntimeError, match="unknown flags"):
@@ -279,7 +293,7 @@ def test_fused_attention_validates_before_launching(lib) -> None:
     args.query = native.PiperTensor(fake, 512, 512, 64)
     with pytest.raises(RuntimeError, match="output pointer is NULL"):
         lib.attention_forward_fused(args, 0)
-    args.plan = 32
+    args.plan = 256
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward_fused(args, 0)
     args.plan, args.flags = 0, 4
@@ -341,8 +355,11 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.sage_attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 32
+    args.plan = 256
     with pytest.raises(RuntimeError, match="unknown plan"):
+        lib.sage_attention_forward(args, 0)
+    args.plan = 16 | 32
+    with pytest.raises(RuntimeError, match="no key-range split"):
         lib.sage_attention_forward(args, 0)
     args.plan, args.flags = 0, 4
     with pytest.raises(RuntimeError, match="unknown flags"):
@@ -484,3 +501,17 @@ def test_probability_codes_rejects_unknown_codes() -> None:
 
     with pytest.raises(ValueError, match="'u8' or 'fp8'"):
         probability_codes([0.5], "int4", torch.device("cpu"))
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 131072, 131072, 128), (1, 8, 8192, 8192, 128), (2, 3, 35, 67, 64)])
+def test_attention_workspace_bytes(lib, shape) -> None:
+    """Only the key-range split plans need a workspace: parts x B x H x Sq rows of D numerator
+    floats plus (den, mref)."""
+    b, h, sq, _, d = shape
+    for plan in (0, 1, 16, 31):
+        assert lib.attention_workspace_bytes(native.PiperShape(*shape), plan) == 0
+    for parts in range(2, 9):
+        plan = 16 | ((parts - 1) << 5)
+        assert lib.attention_workspace_bytes(native.PiperShape(*shape), plan) == parts * b * h * sq * (d + 2) * 4
+    with pytest.raises(RuntimeError, match="unknown plan"):
+        lib.attention_workspace_bytes(native.PiperShape(*shape), 256)
