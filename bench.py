@@ -469,6 +469,27 @@ def main() -> int:
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
+        # the engine clock under this load, read from the driver's metrics over ~300 ms more steps
+        # after the timed region (reads only; the published peak stays the roofline's)
+        from piper_kernels.measure import ClockSampler
+
+        sampler = ClockSampler(device)
+        clock = None
+        if sampler.available:
+            sampler.start()
+            window_begin = torch.cuda.Event(enable_timing=True)
+            window_begin.record()
+            while True:
+                for _ in range(5):
+                    step()
+                window_end = torch.cuda.Event(enable_timing=True)
+                window_end.record()
+                window_end.synchronize()
+                if window_begin.elapsed_time(window_end) >= 300.0:
+                    break
+            sampler.stop()
+            clock = sampler.summary()
+
     ms_per_step = elapsed * 1e3 / args.steps
     prep_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
     attn_ms = sorted(e[1].elapsed_time(e[2]) for e in events)
@@ -558,6 +579,18 @@ def main() -> int:
                 "complete_speedup": round(published["complete_ms"] / ms_per_step, 3),
             }
     result["environment"] = environment(device)
+    if clock is not None:
+        # the kernel's rate against the dense INT8 peak at the clock it ran at (8192 ops/clk/CU)
+        mhz = clock["current_gfxclk_mhz_median"]
+        peak_at_clock = INT8_PEAK_TOPS * mhz / 2400.0
+        result["clock"] = {
+            **clock,
+            "max_sclk_mhz": result["environment"].get("max_sclk_mhz"),
+            "window": "about 300 ms of further steps after the timed region, sampled every 2 ms",
+            "attention_kernel_cycles_at_median_clock": round(attn_mean * 1e-3 * mhz * 1e6),
+            "int8_peak_tops_at_median_clock": round(peak_at_clock, 1),
+            "attention_percent_of_int8_peak_at_median_clock": round(100 * attn_tops / peak_at_clock, 2),
+        }
     if not args.no_probes:
         # the sustained dense MFMA rate of this GPU and the issue probe (after the timed region)
         from piper_kernels._hip import library as native

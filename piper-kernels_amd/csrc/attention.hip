@@ -51,7 +51,7 @@ struct TileLayout : StagePieces<kv_tile_bytes(D), NW> {  // the tile record is t
 template <int D, int NW, bool kCausal>
 __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[2], const float (&ct)[4], int t,
                                              int q0, int n, int h, uint32_t sel, float (&num)[D / 32][16],
-                                             float& den, float& mref, float& mlim) {
+                                             float (&den)[4], float& mref, float& mlim, float& kref) {
   using L = TileLayout<D, NW>;
   constexpr int kChunksD = D / 32;
 
@@ -89,33 +89,38 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
   const float mx = cross_half_max(max32(x));
 
   // ---- lazy rescale of num/den when the block maximum outgrows the reference by 2^8 ----
-  // (mlim = mref + 2^8 is kept beside mref)
+  // (kept beside mref: mlim = mref + 2^8 and kref = 255 * 2^-mref)
   const bool grow = mx > mlim;
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
     const float alpha = grow ? __builtin_amdgcn_exp2f(mref - mx) : 1.0f;
     if (grow) {
       mref = mx;
       mlim = mx + kLazyRescale;
+      kref = __builtin_amdgcn_exp2f(kLog2Of255 - mx);
     }
 #pragma unroll
     for (int j = 0; j < kChunksD; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) num[j][r] *= alpha;
-    den *= alpha;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) den[q] *= alpha;
   }
 
   // ---- e = 255 * vs * p = exp2(x - bm + log2 255), den += sum(p) * beta, UINT8 codes ----
-  const bool empty = mx == -__builtin_inff();
-  const float beta = empty ? 0.0f : __builtin_amdgcn_exp2f(mx - mref);
+  // den holds four partial sums per lane (the lane's keys k with k % 4 = q), added across the
+  // slots and the two lane halves once, in the epilogue
   const float4* iv4 = reinterpret_cast<const float4*>(stage + L::kInvOffset);
   float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   uint32_t pw[8];
-  float pscale;  // sum(p) = pscale * sum(ps)
-  if (__builtin_amdgcn_ballot_w64(!empty && !(fabsf(mx) <= kDirectRange)) == 0) {
-    // E = exp2(x) and e = E * C with C = 2^(log2 255 - bm): no per-key subtraction; the code
-    // FMA multiplies by C (pack_scaled_codes) and sum(p) = C * sum(E / (255 vs)).  |bm| <= 96
-    // keeps E and C normal and finite for every key that can take a nonzero code.
-    const float c = empty ? 0.0f : __builtin_amdgcn_exp2f(kLog2Of255 - mx);
+  float beta;  // the block's weight beside the reference maximum, 2^(bm - mref)
+  float dw;    // the denominator weight of sum(ps)
+  if (__builtin_amdgcn_ballot_w64(!(fabsf(mx) <= kDirectRange)) == 0) {
+    // every block maximum of the wave finite and within +-96: E = exp2(x) and e = E * C with
+    // C = 2^(log2 255 - bm), no per-key subtraction; the code FMA multiplies by C
+    // (pack_scaled_codes), and sum(p) * beta = sum(E / (255 vs)) * C * beta, where
+    // C * beta = 255 * 2^-mref = kref (mref >= bm - 2^8 >= -104: finite)
+    const float c = __builtin_amdgcn_exp2f(kLog2Of255 - mx);
+    beta = __builtin_amdgcn_exp2f(mx - mref);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float4 ia = iv4[4 * h + q];
@@ -139,9 +144,12 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
       pw[q] = pack_scaled_codes(e0, e1, e2, e3, c, sel);
       pw[4 + q] = pack_scaled_codes(f0, f1, f2, f3, c, sel);
     }
-    pscale = c;
+    dw = kref;
   } else {
-    // extreme block maxima: subtract the shift first, as the reference's exp(s - bm)
+    // extreme, empty (causal) or non-finite block maxima: subtract the shift first, as the
+    // reference's exp(s - bm)
+    const bool empty = mx == -__builtin_inff();
+    beta = empty ? 0.0f : __builtin_amdgcn_exp2f(mx - mref);
     const float shift = empty ? 0.0f : mx - kLog2Of255;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -166,10 +174,10 @@ __device__ __forceinline__ void block_update(const char* stage, const v16i (&s)[
       pw[q] = pack_codes(e0, e1, e2, e3);
       pw[4 + q] = pack_codes(f0, f1, f2, f3);
     }
-    pscale = 1.0f;
+    dw = beta;
   }
-  const float psum = cross_half_sum((ps[0] + ps[1]) + (ps[2] + ps[3])) * pscale;
-  den = fmaf(psum, beta, den);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) den[q] = fmaf(ps[q], dw, den[q]);
   const float weight = beta;  // the reference's 1/255 is applied once, in the epilogue
   const v4i p0 = {static_cast<int>(pw[0]), static_cast<int>(pw[1]), static_cast<int>(pw[2]), static_cast<int>(pw[3])};
   const v4i p1 = {static_cast<int>(pw[4]), static_cast<int>(pw[5]), static_cast<int>(pw[6]), static_cast<int>(pw[7])};
@@ -216,7 +224,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
                                               int wave, int lane, const v4i (&qf)[D / 32], float cq,
                                               int q0, int n, int h, int krow, uint32_t sel,
                                               const v16i (&s_cur)[2], v16i (&s_next)[2], float (&num)[D / 32][16],
-                                              float& den, float& mref, float& mlim) {
+                                              float (&den)[4], float& mref, float& mlim, float& kref) {
   using L = TileLayout<D, NW>;
   using R = Ring<NW>;
   // unconditional (clamped) so every iteration issues the same number of copies; a clamped
@@ -237,7 +245,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams& p, char* smem, i
     } else {  // per-block scales: the four slots hold the same value
       ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
     }
-    block_update<D, NW, kCausal>(stage, s_cur, ct, t, q0, n, h, sel, num, den, mref, mlim);
+    block_update<D, NW, kCausal>(stage, s_cur, ct, t, q0, n, h, sel, num, den, mref, mlim, kref);
   }
   if constexpr (kBarrier) stage_barrier_keep_last<L>(wave);
 }
@@ -317,9 +325,10 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
   for (int j = 0; j < kChunksD; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) num[j][r] = 0.0f;
-  float den = 0.0f;
+  float den[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float mref = -__builtin_inff();
   float mlim = -__builtin_inff();
+  float kref = 0.0f;
 
   // MFMA row m of the K operand holds key 16*((m>>2)&1) + 4*(m>>3) + (m&3), so that output
   // register r of lane half h holds key 16h + r.
@@ -336,20 +345,22 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
   int t = 0;
   for (; t + 1 < tiles; t += 2) {
     pipeline_step<D, NW, kCausal, kPerThread, R::kEveryIteration>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq,
-                                                               q0, n, h, krow, sel, s_a, s_b, num, den, mref, mlim);
+                                                               q0, n, h, krow, sel, s_a, s_b, num, den, mref, mlim, kref);
     pipeline_step<D, NW, kCausal, kPerThread, true>(p, smem, t + 1, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n,
-                                        h, krow, sel, s_b, s_a, num, den, mref, mlim);
+                                        h, krow, sel, s_b, s_a, num, den, mref, mlim, kref);
   }
   if (t < tiles)
     pipeline_step<D, NW, kCausal, kPerThread, false>(p, smem, t, tiles, wave_tiles, bh, wave, lane, qf, cq, q0, n, h,
-                                         krow, sel, s_a, s_b, num, den, mref, mlim);
+                                         krow, sel, s_a, s_b, num, den, mref, mlim, kref);
   // no direct copy may still be writing this workgroup's LDS when its waves end
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue: num / max(den, 1e-30) + mean(V), one query per lane ----
+  // the row's denominator: the four partial sums of both lane halves
+  const float den_total = cross_half_sum((den[0] + den[1]) + (den[2] + den[3]));
   const int query = q0 + n;
   if (!wave_live || query >= p.query_length) return;
-  const float rden = (1.0f / 255.0f) / fmaxf(den, 1e-30f);  // the numerator holds 255 x the reference's
+  const float rden = (1.0f / 255.0f) / fmaxf(den_total, 1e-30f);  // the numerator holds 255 x the reference's
   const float* vmean = p.value_mean + static_cast<long>(bh) * D;
   const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
 #pragma unroll
@@ -466,9 +477,10 @@ attention_w3_kernel(const AttnParams p) {
   for (int j = 0; j < kChunksD; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) num[j][r] = 0.0f;
-  float den = 0.0f;
+  float den[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float mref = -__builtin_inff();
   float mlim = -__builtin_inff();
+  float kref = 0.0f;
   const int krow = 16 * ((n >> 2) & 1) + 4 * (n >> 3) + (n & 3);
   const uint32_t sel = code_selector();
 
@@ -493,11 +505,13 @@ attention_w3_kernel(const AttnParams p) {
       } else {
         ct[0] = ct[1] = ct[2] = ct[3] = cq * *reinterpret_cast<const float*>(stage + D);
       }
-      block_update<D, NW, kCausal>(stage, sc, ct, t, q0, n, h, sel, num, den, mref, mlim);
+      block_update<D, NW, kCausal>(stage, sc, ct, t, q0, n, h, sel, num, den, mref, mlim, kref);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  // the row's denominator: the four partial sums of both lane halves
+  const float den_total = cross_half_sum((den[0] + den[1]) + (den[2] + den[3]));
   const int query = q0 + n;
   if (!wave_live || query >= p.query_length) return;
   if constexpr (kOut == kPartials) {
@@ -510,11 +524,11 @@ attention_w3_kernel(const AttnParams p) {
       for (int g = 0; g < 4; ++g)
         *reinterpret_cast<float4*>(dst + 32 * j + 8 * g + 4 * h) =
             make_float4(num[j][4 * g + 0], num[j][4 * g + 1], num[j][4 * g + 2], num[j][4 * g + 3]);
-    // both lane halves hold the row's den and mref
-    if (h == 0) reinterpret_cast<float2*>(p.partials + p.key_parts * rows * D)[row] = make_float2(den, mref);
+    // both lane halves hold the row's den_total and mref
+    if (h == 0) reinterpret_cast<float2*>(p.partials + p.key_parts * rows * D)[row] = make_float2(den_total, mref);
     return;
   } else {
-    const float rden = (1.0f / 255.0f) / fmaxf(den, 1e-30f);  // the numerator holds 255 x the reference's
+    const float rden = (1.0f / 255.0f) / fmaxf(den_total, 1e-30f);  // the numerator holds 255 x the reference's
     const float* vmean = p.value_mean + static_cast<long>(bh) * D;
     const long out_row = (static_cast<long>(bh) * p.query_length + query) * D;
 #pragma unroll

@@ -450,3 +450,92 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
             "add_sgpr_ticks": per_instr(sgpr3, "add_sgpr", "valu"),
         },
     }
+
+
+class ClockSampler:
+    """The GPU's engine clock, read from the driver's metrics (amdsmi) by a background thread
+    while a workload runs: what the kernels actually ran at, beside the published peak the
+    roofline uses.  Reads only; the clock is never set.  ``available`` is False when amdsmi or
+    the device's handle cannot be opened (the samples are then empty)."""
+
+    def __init__(self, device: torch.device, period_s: float = 0.002) -> None:
+        import threading
+
+        self.period_s = period_s
+        self.samples: list[dict] = []
+        self._stop = threading.Event()
+        self._thread = None
+        self._handle = None
+        self.available = False
+        try:
+            import amdsmi
+
+            amdsmi.amdsmi_init()
+            handles = amdsmi.amdsmi_get_processor_handles()
+            props = torch.cuda.get_device_properties(device)
+            bus = getattr(props, "pci_bus_id", None)
+            if len(handles) == 1:
+                self._handle = handles[0]
+            elif bus is not None:
+                for handle in handles:
+                    bdf = amdsmi.amdsmi_get_gpu_device_bdf(handle)  # "dddd:bb:dd.f"
+                    if int(bdf.split(":")[1], 16) == int(bus):
+                        self._handle = handle
+                        break
+            self._amdsmi = amdsmi
+            self.available = self._handle is not None
+        except Exception:  # noqa: BLE001  (no amdsmi, no permission: no samples)
+            self.available = False
+
+    def _read(self) -> dict:
+        metrics = self._amdsmi.amdsmi_get_gpu_metrics_info(self._handle)
+        per_xcc = metrics.get("current_gfxclks")
+        return {
+            "current_gfxclk": metrics.get("current_gfxclk"),
+            "average_gfxclk_frequency": metrics.get("average_gfxclk_frequency"),
+            "current_gfxclks": [c for c in per_xcc if isinstance(c, int) and c > 0] if isinstance(per_xcc, list) else None,
+        }
+
+    def _run(self) -> None:
+        import time
+
+        while not self._stop.is_set():
+            try:
+                self.samples.append(self._read())
+            except Exception:  # noqa: BLE001
+                return
+            time.sleep(self.period_s)
+
+    def start(self) -> None:
+        import threading
+
+        if not self.available:
+            return
+        self.samples.clear()
+        self._stop.clear()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self._thread.start()
+
+    def stop(self) -> None:
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join(timeout=2.0)
+            self._thread = None
+
+    def summary(self) -> dict | None:
+        """Median and range of the sampled clocks in MHz (None without samples)."""
+        import statistics
+
+        current = [s["current_gfxclk"] for s in self.samples if isinstance(s.get("current_gfxclk"), int)]
+        if not current:
+            return None
+        average = [s["average_gfxclk_frequency"] for s in self.samples
+                   if isinstance(s.get("average_gfxclk_frequency"), int)]
+        per_xcc = [c for s in self.samples if s.get("current_gfxclks") for c in s["current_gfxclks"]]
+        return {
+            "samples": len(current),
+            "current_gfxclk_mhz_median": statistics.median(current),
+            "current_gfxclk_mhz_min_max": [min(current), max(current)],
+            "average_gfxclk_mhz_median": statistics.median(average) if average else None,
+            "per_xcc_gfxclk_mhz_median": statistics.median(per_xcc) if per_xcc else None,
+        }

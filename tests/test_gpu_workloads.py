@@ -95,14 +95,21 @@ def test_c5_student_t_heads(gfx950_device, granularity) -> None:
 
 
 def test_c3_full_shape_runs_and_matches_its_head_subset(gfx950_device) -> None:
-    """The full headline shape through the public operator; heads match a separate subset run."""
+    """The full headline shape through the public operator; heads match a separate subset run
+    under the same launch plan bit for bit (a one-head grid on its own would take a key-range
+    split plan, equal to rounding only)."""
     from piper_kernels import piper_attention
+    from piper_kernels.attention.piper_attention._plan import select_plan
+    from piper_kernels.attention.piper_attention.hip import _run_piper_attention
 
     w = WORKLOADS["c3"]
     q, k, v = make_inputs(w, gfx950_device)
+    plan = select_plan(*w.shape, w.is_causal)
+    assert plan.key_parts == 1
     with torch.no_grad():
         full = piper_attention(q, k, v)
-        part = piper_attention(q[:, [5]].contiguous(), k[:, [5]].contiguous(), v[:, [5]].contiguous())
+        part = _run_piper_attention(q[:, [5]].contiguous(), k[:, [5]].contiguous(), v[:, [5]].contiguous(),
+                                    w.head_dim**-0.5, False, plan=plan)
     torch.cuda.synchronize()
     assert full.shape == q.shape and full.dtype is torch.float16
     assert torch.isfinite(full).all()
