@@ -324,7 +324,7 @@ int piper_prepared_layout(const piper_shape* shape, piper_layout* layout);
  * with PIPER_PREPARE_SKIP_QUERY only K and V.  key_mean must be 4-byte aligned, the workspace
  * and the other prepared buffers 16-byte aligned.
  *
- * Launches, at D = 128 with Sk <= 16384 when one XCC of the device holds a tensor's 256-row
+ * Launches, at D = 128 with Sk <= 32768 when one XCC of the device holds a tensor's 256-row
  * chunks at once (4 * CUs / XCCs >= ceil(Sk / 256); every MI355X partition mode): a fill kernel
  * (sync words cleared, means marked pending) and the single pass, which reads K and V once: each
  * chunk publishes its partial sums, the last chunk of a batch-head tensor finalises the mean,

@@ -593,7 +593,7 @@ struct SinglePassParams {
   int spin_limit;      // polls before a wait gives up (0: no wait, every waiter computes the mean)
 };
 
-constexpr int kSinglePassChunks = 64;
+constexpr int kSinglePassChunks = 128;  // 2^15 keys: at most 8 level-2 groups of 16 chunks
 
 // The mean of column `col` of one batch-head's K or V straight from its rows in HBM, in the
 // cascade order of the published partials and single_pass_mean (L = 16): rows summed in
@@ -649,29 +649,27 @@ __device__ float column_mean_from_rows(const InputTensor& in, int b, int h, int 
 constexpr uint32_t kMeanPending = 0x7fa5a5a5u;  // a signalling NaN: the mean slot before it is published
 
 // The mean of one column from the published partials, torch's cascade order (finalize_column),
-// with two threads per column: thread `half` sums the level-2 groups [2 half, 2 half + 2) of L
-// chunks each (loads in flight together), the groups meet in LDS and thread 0 of the pair
-// combines them in order.
+// with two threads per column: thread `half` sums the level-2 groups half, half + 2, ... of L
+// chunks each (one group's loads in flight together, the groups one after another to keep the
+// chunk's rows in registers), the groups meet in LDS and thread 0 of the pair combines them in
+// order.
 __device__ __forceinline__ float single_pass_mean(const MeanParams& p, const float* src, int col, int half,
                                                   float (*group_sums)[128]) {
   constexpr int L = 16;
   const int full = p.length / (L * L);  // complete chunks
   const int groups = (full + L - 1) / L;  // level-2 groups (the last may be unfinished)
+#pragma unroll 1
+  for (int g = half; g < groups; g += 2) {
+    const int c0 = g * L;
+    const int n = min(L, full - c0);
+    float part[L];
 #pragma unroll
-  for (int gg = 0; gg < 2; ++gg) {
-    const int g = 2 * half + gg;
-    if (g < groups) {
-      const int c0 = g * L;
-      const int n = min(L, full - c0);
-      float part[L];
+    for (int i = 0; i < L; ++i) part[i] = i < n ? load_coherent(src + static_cast<long>(c0 + i) * 128) : 0.0f;
+    float s = 0.0f;
 #pragma unroll
-      for (int i = 0; i < L; ++i) part[i] = i < n ? load_coherent(src + static_cast<long>(c0 + i) * 128) : 0.0f;
-      float s = 0.0f;
-#pragma unroll
-      for (int i = 0; i < L; ++i)
-        if (i < n) s += part[i];
-      group_sums[g][col] = s;
-    }
+    for (int i = 0; i < L; ++i)
+      if (i < n) s += part[i];
+    group_sums[g][col] = s;
   }
   __syncthreads();
   if (half != 0) return 0.0f;
@@ -689,7 +687,7 @@ __device__ __forceinline__ float single_pass_mean(const MeanParams& p, const flo
 // LDS of a single-pass workgroup.
 struct SinglePassShared {
   float block_sums[16][128];  // the chunk's level-0 sums
-  float group_sums[4][128];
+  float group_sums[kSinglePassChunks / 16][128];
   float mean[128];
   int last;
 };

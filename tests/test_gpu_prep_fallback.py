@@ -25,7 +25,8 @@ CASES = [
     # (B, H, Sq, Sk, dtype, causal); D = 128, the single pass's head size
     (1, 3, 4096, 4096, torch.float16, False),  # 16 chunks
     (2, 2, 1000, 1000, torch.bfloat16, False),  # 4 chunks, the last short (ragged)
-    (1, 2, 16384, 16384, torch.float16, False),  # 64 chunks: the single pass's longest sequence
+    (1, 2, 16384, 16384, torch.float16, False),  # 64 chunks
+    (1, 1, 32768, 32768, torch.float16, False),  # 128 chunks: the single pass's longest sequence
     (1, 2, 4096, 4096, torch.bfloat16, True),  # causal: only K is centred and waits
     (1, 1, 100, 100, torch.float16, False),  # one chunk: it is its tensor's last, nothing waits
 ]

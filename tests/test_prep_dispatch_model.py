@@ -90,7 +90,8 @@ def test_remap_is_a_permutation_with_one_range_per_xcc() -> None:
 
 
 @pytest.mark.parametrize("xccs", [8, 4, 2, 1])
-@pytest.mark.parametrize("batch_heads,chunks", [(24, 64), (128, 32), (80, 64), (7, 64), (3, 17), (1, 1), (33, 63)])
+@pytest.mark.parametrize("batch_heads,chunks", [(24, 64), (128, 32), (80, 64), (7, 64), (3, 17), (1, 1), (33, 63),
+                                                (80, 128), (5, 128), (24, 100)])
 def test_every_tensor_completes_in_every_partition_mode(xccs, batch_heads, chunks) -> None:
     cus = 32 * xccs  # MI355X: 32 CUs per XCC in every partition mode
     assert single_pass_resident(chunks, cus, xccs)
