@@ -21,7 +21,9 @@ Beside the timing (all after the timed region):
   the quantised reference's own distance on the same rows, and against the quantised reference
   (the CPU oracle's output for every head the CPU baseline computed): max and mean absolute
   error, SQNR and cosine (the reference harness's quality columns,
-  benchmarks/benchmark_attention.py:249,380);
+  benchmarks/benchmark_attention.py:249,380), and ``saturation``: how many INT8 Q, K and V
+  codes of the call sit at -127 or 127 (the reference harness's saturation fields,
+  benchmarks/lib/quality.py:16-41);
 * ``cpu_baseline``: the CPU oracle (a numpy restatement of the reference's portable path) on
   whole heads of the same workload, one head per host thread on all the host threads the run
   may use, per thread-group Q/K scales (the reference's default) and, on one round of heads,
@@ -32,7 +34,11 @@ Beside the timing (all after the timed region):
 * ``issue_sharing``: the measurement library's issue probe (VALU issue per waves per SIMD,
   MFMA/VALU overlap across and within waves, the attention loop's mix with and without its
   MFMAs, LDS bandwidth);
+* ``clock``: the engine clock while the workload runs (the driver's GPU metrics, sampled over
+  ~300 ms of further steps) and the kernel's rate against the INT8 peak at that clock;
 * ``environment``: GPU, clocks, software versions, host CPU and the source revision.
+
+``schema_version`` numbers this record's layout beyond the driver's fixed keys.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline] [--two-step]
 """
@@ -75,6 +81,7 @@ REFERENCE_R2 = {
     "source": "benchmarks/README.md:526 (uncentred V)",
 }
 REFERENCE_PUBLISHED = {"r1": REFERENCE_R1, "r2": REFERENCE_R2}
+SCHEMA_VERSION = 2  # 2: clock block, quality.saturation, r2
 
 
 def log(msg: str) -> None:
@@ -306,6 +313,37 @@ def quality_block(workload, output, reference_outputs: dict, rows: int) -> dict:
     return result
 
 
+def saturation_block(q, k, v, scale: float, workload, granularity: str) -> dict:
+    """How many INT8 codes of the call's Q, K and V sit at the quantiser's endpoints (-127, 127),
+    with the field names of the reference harness's ``QuantizerSaturation``
+    (``benchmarks/lib/quality.py:16-41``).  Counted on the GPU from a two-step prep of the timed
+    inputs (the fused path never writes query codes), over the valid rows only.  The UINT8
+    probability codes exist only inside the attention kernel and are not counted."""
+    import torch
+
+    from piper_kernels.attention.piper_attention.hip import _prepare_piper_attention
+
+    b, h, sq, sk, d = workload.shape
+    with torch.no_grad():
+        prepared = _prepare_piper_attention(q, k, v, scale, workload.is_causal, quantize_query=True,
+                                            qk_granularity=granularity)
+        keys = torch.arange(prepared.value_code_transposed().shape[2] * 64, device=q.device)
+        codes = {
+            "query": prepared.query_code[:, :, :sq],
+            "key": prepared.key_code()[:, :, :sk],
+            # V^T codes [B, H, tiles, D, 64] -> [B, H, D, Sk64], valid keys only
+            "value": prepared.value_code_transposed().permute(0, 1, 3, 2, 4).reshape(b, h, d, -1)[..., keys < sk],
+        }
+        result = {}
+        for name, c in codes.items():
+            low = int(torch.count_nonzero(c == -127))
+            high = int(torch.count_nonzero(c == 127))
+            total = c.numel()
+            result[name] = {"minimum": -127, "maximum": 127, "minimum_count": low, "maximum_count": high,
+                            "count": low + high, "total_count": total, "fraction": (low + high) / total}
+    return result
+
+
 # ---------------------------------------------------------------------------------------
 # environment
 # ---------------------------------------------------------------------------------------
@@ -522,6 +560,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": f"synthetic (seeded numpy PCG64 per head, {workload.as_dict()['dtype']} inputs resident in HBM)",
+        # version of this record's layout beyond the driver's fixed keys (as the reference harness's
+        # records carry one, benchmarks/lib/reporting.py:18): bump when a field changes meaning
+        "schema_version": SCHEMA_VERSION,
         "config": {
             **workload.as_dict(),
             "operator": args.operator,
@@ -615,6 +656,7 @@ def main() -> int:
     if not sage:
         log("[bench] quality")
         result["quality"] = quality_block(workload, out, reference_outputs, args.quality_rows)
+        result["quality"]["saturation"] = saturation_block(q, k, v, scale, workload, args.qk_granularity)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -9,10 +9,13 @@ It restates the portable PyTorch reference of ``jumbledpoophj/piper-kernels`` 0.
 ``src/piper_kernels/attention/sage_attention_2pp/reference.py:15-104``:
 
 * K smoothing and INT8 Q/K codes, shared with Piper Attention
-  (:func:`oracle.piper_oracle.quantize_query_key`), at the ``per_warp`` granularity --
-  one scale per 32 query rows and per 64 key rows, the grouped scales the reference's GPU
-  path uses where it groups Q/K scales (``sage_attention_2pp/_policy.py:63``) and that its
-  GPU test compares against (``tests/attention/sage_attention_2pp/test_triton.py:33-34``);
+  (:func:`oracle.piper_oracle.quantize_query_key`), at either of the reference's
+  granularities (the ``granularity`` argument): ``per_thread`` -- per thread group, the
+  default of the reference's portable path (``reference.py:35``) and of the MI355X operator
+  and smoke test -- or ``per_warp`` -- one scale per 32 query rows and per 64 key rows, the
+  grouped scales of the reference's SM12x Triton path (``sage_attention_2pp/_policy.py:63``)
+  that its GPU test compares against (``tests/attention/sage_attention_2pp/test_triton.py:33-34``);
+  the functions here default to ``per_warp``, the granularity the golden fixtures were made at;
 * per-channel FP8 E4M3 V codes, ``scale = amax_S|v| / 2.25 + 1e-7`` (``reference.py:22-25``);
 * the 64-key online-softmax loop whose frame is shifted by ln(448) so probabilities land
   in FP8's range, FP8 probabilities, and 64-key partial products rounded to FP16

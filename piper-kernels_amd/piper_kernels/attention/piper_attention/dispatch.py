@@ -44,8 +44,10 @@ def piper_attention(
     BF16 elements and contiguous head dimensions (64 or 128). Query and key sequence
     lengths may differ for non-causal attention. ``scale`` defaults to ``head_dim**-0.5``.
 
-    K is smoothed by its sequence mean and Q/K are quantised to INT8 per 32-row / 64-row
-    block; each V row gets its own signed-INT8 scale, folded into UINT8 probability codes.
+    K is smoothed by its sequence mean and Q/K are quantised to INT8 with one scale per
+    thread group of each 32-row (Q) or 64-row (K) block, the granularity of the reference's
+    portable path; each V row gets its own signed-INT8 scale, folded into UINT8 probability
+    codes.
     Non-causal calls centre V by its sequence-wide per-feature mean and restore it in the
     epilogue; causal calls stay uncentred. Inference only.
     """
