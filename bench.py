@@ -34,8 +34,9 @@ Beside the timing (all after the timed region):
 * ``issue_sharing``: the measurement library's issue probe (VALU issue per waves per SIMD,
   MFMA/VALU overlap across and within waves, the attention loop's mix with and without its
   MFMAs, LDS bandwidth);
-* ``clock``: the engine clock while the workload runs (the driver's GPU metrics, sampled over
-  ~300 ms of further steps) and the kernel's rate against the INT8 peak at that clock;
+* ``clock``: the engine clock while the workload runs (the measurement library's clock probe on
+  a second stream beside ~300 ms of further steps) and the kernel's rate against the INT8 peak
+  at that clock;
 * ``environment``: GPU, clocks, software versions, host CPU and the source revision.
 
 ``schema_version`` numbers this record's layout beyond the driver's fixed keys.
@@ -507,26 +508,21 @@ def main() -> int:
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
-        # the engine clock under this load, read from the driver's metrics over ~300 ms more steps
-        # after the timed region (reads only; the published peak stays the roofline's)
-        from piper_kernels.measure import ClockSampler
+        # the engine clock under this load, read on the GPU beside ~300 ms of further steps after the
+        # timed region (the clock probe's sleeping waves on a second stream; reads only, the published
+        # peak stays the roofline's)
+        from piper_kernels.measure import ClockProbe
 
-        sampler = ClockSampler(device)
-        clock = None
-        if sampler.available:
-            sampler.start()
-            window_begin = torch.cuda.Event(enable_timing=True)
-            window_begin.record()
-            while True:
-                for _ in range(5):
-                    step()
-                window_end = torch.cuda.Event(enable_timing=True)
-                window_end.record()
-                window_end.synchronize()
-                if window_begin.elapsed_time(window_end) >= 300.0:
-                    break
-            sampler.stop()
-            clock = sampler.summary()
+        probe = ClockProbe(device, duration_ms=300.0)
+        for _ in range(5):
+            step()  # queue work first, so the probe's waves start beside it
+        probe.start()
+        guard = time.perf_counter()
+        while not probe.done() and time.perf_counter() - guard < 5.0:
+            for _ in range(5):
+                step()
+            torch.cuda.current_stream(device).synchronize()
+        clock = probe.summary()
 
     ms_per_step = elapsed * 1e3 / args.steps
     prep_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
@@ -620,14 +616,15 @@ def main() -> int:
                 "complete_speedup": round(published["complete_ms"] / ms_per_step, 3),
             }
     result["environment"] = environment(device)
-    if clock is not None:
+    if clock.get("engine_clock_mhz_median"):
         # the kernel's rate against the dense INT8 peak at the clock it ran at (8192 ops/clk/CU)
-        mhz = clock["current_gfxclk_mhz_median"]
+        mhz = clock["engine_clock_mhz_median"]
         peak_at_clock = INT8_PEAK_TOPS * mhz / 2400.0
         result["clock"] = {
             **clock,
             "max_sclk_mhz": result["environment"].get("max_sclk_mhz"),
-            "window": "about 300 ms of further steps after the timed region, sampled every 2 ms",
+            "window": ("about 300 ms of further steps after the timed region; one sleeping probe wave per XCC "
+                       "on a second stream reads the shader clock counter against the wall clock counter"),
             "attention_kernel_cycles_at_median_clock": round(attn_mean * 1e-3 * mhz * 1e6),
             "int8_peak_tops_at_median_clock": round(peak_at_clock, 1),
             "attention_percent_of_int8_peak_at_median_clock": round(100 * attn_tops / peak_at_clock, 2),

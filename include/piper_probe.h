@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PIPER_PROBE_ABI_VERSION 1
+#define PIPER_PROBE_ABI_VERSION 2
 
 int piper_probe_abi_version(void);
 const char* piper_probe_last_error(void);
@@ -117,6 +117,21 @@ typedef struct piper_issue_probe_args {
 } piper_issue_probe_args;
 
 int piper_issue_probe(const piper_issue_probe_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Engine clock.  `workgroups` one-wave workgroups (1 .. 256; workgroup g runs on XCC g % XCCs)
+ * each read the variable-frequency shader clock counter (s_memtime, HIP's clock64) and the
+ * constant-rate wall clock counter (s_memrealtime, HIP's wall_clock64) when they start, sleep
+ * until the wall clock has advanced by `duration_us` microseconds (1 .. 2 * 10^6; each wave also
+ * stops after 2^20 sleeps), and read both again.  Record g = {wall0, clock0, wall1, clock1} at
+ * records[4 g .. 4 g + 3]; *wall_clock_khz receives the wall counter's rate
+ * (hipDeviceAttributeWallClockRate of the current device).  The engine clock over the wave's life
+ * is (clock1 - clock0) / (wall1 - wall0) * wall_clock_khz kHz: launched on a second stream beside
+ * a workload, it reads the clock the workload runs at (the waves use a few VGPRs and no LDS).
+ * ------------------------------------------------------------------------------------- */
+#define PIPER_CLOCK_PROBE_MAX_WORKGROUPS 256
+int piper_clock_probe(int32_t workgroups, int64_t duration_us, uint64_t* records, int32_t* wall_clock_khz,
+                      void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -370,6 +370,30 @@ int fail(int status, const char* fmt, ...) {
   return status;
 }
 
+// Engine clock: each one-wave workgroup reads the shader clock counter (s_memtime, variable
+// frequency) and the wall clock counter (s_memrealtime, constant rate) at its start, sleeps until
+// the wall clock has advanced by `ticks` (at most kClockProbeMaxSleeps sleeps, so the wave ends
+// even if the counter stalled), and reads both again.
+constexpr uint32_t kClockProbeMaxSleeps = 1u << 20;
+
+__global__ void __launch_bounds__(64) clock_probe_kernel(uint64_t* records, uint64_t ticks) {
+  const uint64_t wall0 = __builtin_amdgcn_s_memrealtime();
+  const uint64_t clock0 = __builtin_amdgcn_s_memtime();
+  uint64_t wall1 = wall0;
+  for (uint32_t i = 0; i < kClockProbeMaxSleeps && wall1 - wall0 < ticks; ++i) {
+    __builtin_amdgcn_s_sleep(127);
+    wall1 = __builtin_amdgcn_s_memrealtime();
+  }
+  const uint64_t clock1 = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x == 0) {
+    uint64_t* r = records + 4 * static_cast<long>(blockIdx.x);
+    r[0] = wall0;
+    r[1] = clock0;
+    r[2] = wall1;
+    r[3] = clock1;
+  }
+}
+
 }  // namespace
 }  // namespace piper
 
@@ -444,6 +468,31 @@ int piper_issue_probe(const piper_issue_probe_args* a, void* stream) {
                        dim3(256 * a->waves_per_simd), kIssueLdsBytes, static_cast<hipStream_t>(stream), p);
   err = hipGetLastError();
   if (err != hipSuccess) return fail(3, "issue probe launch failed: %s", hipGetErrorString(err));
+  g_last_error[0] = '\0';
+  return 0;
+}
+
+int piper_clock_probe(int32_t workgroups, int64_t duration_us, uint64_t* records, int32_t* wall_clock_khz,
+                      void* stream) {
+  using namespace piper;
+  if (workgroups < 1 || workgroups > PIPER_CLOCK_PROBE_MAX_WORKGROUPS)
+    return fail(1, "clock probe needs 1..%d workgroups, got %d", PIPER_CLOCK_PROBE_MAX_WORKGROUPS, workgroups);
+  if (duration_us < 1 || duration_us > 2000000)
+    return fail(1, "clock probe duration must be 1..2000000 us, got %lld", (long long)duration_us);
+  if (records == nullptr || (reinterpret_cast<uintptr_t>(records) & 7u) != 0 || wall_clock_khz == nullptr)
+    return fail(1, "records must be a non-NULL 8-byte aligned buffer of 4 * workgroups words, wall_clock_khz non-NULL");
+  int device = 0;
+  int khz = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device);
+  if (err != hipSuccess) return fail(3, "wall clock rate unavailable: %s", hipGetErrorString(err));
+  if (khz <= 0) return fail(2, "the device reports no wall clock rate");
+  const uint64_t ticks = static_cast<uint64_t>(duration_us) * static_cast<uint64_t>(khz) / 1000u;
+  hipLaunchKernelGGL(clock_probe_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), records, ticks);
+  err = hipGetLastError();
+  if (err != hipSuccess) return fail(3, "clock probe launch failed: %s", hipGetErrorString(err));
+  *wall_clock_khz = khz;
   g_last_error[0] = '\0';
   return 0;
 }

@@ -361,8 +361,9 @@ def library_available() -> bool:
 # ---------------------------------------------------------------------------------------
 # libpiper_probe.so (include/piper_probe.h)
 # ---------------------------------------------------------------------------------------
-PROBE_ABI_VERSION = 1
-PROBE_EXPORTED_SYMBOLS = ("piper_probe_abi_version", "piper_probe_last_error", "piper_mfma_probe", "piper_issue_probe")
+PROBE_ABI_VERSION = 2
+PROBE_EXPORTED_SYMBOLS = ("piper_probe_abi_version", "piper_probe_last_error", "piper_mfma_probe", "piper_issue_probe",
+                          "piper_clock_probe")
 
 # piper_mfma_probe kinds, workgroup size and operations per MFMA (PIPER_MFMA_PROBE_*)
 MFMA_PROBE_I8 = 0
@@ -377,6 +378,9 @@ MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 ISSUE_ROLES = ("idle", "mfma", "fma", "exp", "cvt", "mix", "valu_mix", "lds", "mfma_fma", "mix_vgpr", "cluster", "add_lit", "add_sgpr")
 ISSUE_MAX_WAVES_PER_SIMD = 4
 ISSUE_RECORDS_PER_WORKGROUP = 16
+
+# piper_clock_probe (PIPER_CLOCK_PROBE_*)
+CLOCK_PROBE_MAX_WORKGROUPS = 256
 
 
 class PiperIssueRecord(ctypes.Structure):
@@ -416,6 +420,8 @@ class ProbeLibrary:
         lib.piper_mfma_probe.restype = ctypes.c_int
         lib.piper_issue_probe.argtypes = [ctypes.POINTER(PiperIssueProbeArgs), _ptr]
         lib.piper_issue_probe.restype = ctypes.c_int
+        lib.piper_clock_probe.argtypes = [_i32, _i64, _ptr, ctypes.POINTER(_i32), _ptr]
+        lib.piper_clock_probe.restype = ctypes.c_int
         version = lib.piper_probe_abi_version()
         if version != PROBE_ABI_VERSION:
             raise LibraryUnavailableError(f"{self.path} has ABI version {version}, this package expects {PROBE_ABI_VERSION}")
@@ -435,6 +441,13 @@ class ProbeLibrary:
 
     def issue_probe(self, args: PiperIssueProbeArgs, stream: int) -> None:
         self._check(self._lib.piper_issue_probe(ctypes.byref(args), _ptr(stream)), "piper_issue_probe")
+
+    def clock_probe(self, workgroups: int, duration_us: int, records: int, stream: int) -> int:
+        """Launch the engine-clock probe; returns the wall clock counter's rate in kHz."""
+        khz = _i32(0)
+        self._check(self._lib.piper_clock_probe(workgroups, duration_us, _ptr(records), ctypes.byref(khz), _ptr(stream)),
+                    "piper_clock_probe")
+        return khz.value
 
 
 _probe_library: ProbeLibrary | None = None

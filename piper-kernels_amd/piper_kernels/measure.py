@@ -452,90 +452,53 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
     }
 
 
-class ClockSampler:
-    """The GPU's engine clock, read from the driver's metrics (amdsmi) by a background thread
-    while a workload runs: what the kernels actually ran at, beside the published peak the
-    roofline uses.  Reads only; the clock is never set.  ``available`` is False when amdsmi or
-    the device's handle cannot be opened (the samples are then empty)."""
+class ClockProbe:
+    """The engine clock a workload runs at, read on the GPU itself: the measurement library's
+    clock probe (``piper_clock_probe``) runs one sleeping wave per XCC on a stream of its own,
+    beside the workload on the caller's stream, and reads the variable-frequency shader clock
+    counter against the constant-rate wall clock counter over its life.  Reads only; the clock
+    is never set.  Usage: queue some of the workload, ``start()``, keep queueing until
+    ``done()``, then ``summary()``."""
 
-    def __init__(self, device: torch.device, period_s: float = 0.002) -> None:
-        import threading
+    def __init__(self, device: torch.device, duration_ms: float = 300.0, workgroups: int = 8) -> None:
+        from ._hip.library import load_probe_library
 
-        self.period_s = period_s
-        self.samples: list[dict] = []
-        self._stop = threading.Event()
-        self._thread = None
-        self._handle = None
-        self.available = False
-        try:
-            import amdsmi
-
-            amdsmi.amdsmi_init()
-            handles = amdsmi.amdsmi_get_processor_handles()
-            props = torch.cuda.get_device_properties(device)
-            bus = getattr(props, "pci_bus_id", None)
-            if len(handles) == 1:
-                self._handle = handles[0]
-            elif bus is not None:
-                for handle in handles:
-                    bdf = amdsmi.amdsmi_get_gpu_device_bdf(handle)  # "dddd:bb:dd.f"
-                    if int(bdf.split(":")[1], 16) == int(bus):
-                        self._handle = handle
-                        break
-            self._amdsmi = amdsmi
-            self.available = self._handle is not None
-        except Exception:  # noqa: BLE001  (no amdsmi, no permission: no samples)
-            self.available = False
-
-    def _read(self) -> dict:
-        metrics = self._amdsmi.amdsmi_get_gpu_metrics_info(self._handle)
-        per_xcc = metrics.get("current_gfxclks")
-        return {
-            "current_gfxclk": metrics.get("current_gfxclk"),
-            "average_gfxclk_frequency": metrics.get("average_gfxclk_frequency"),
-            "current_gfxclks": [c for c in per_xcc if isinstance(c, int) and c > 0] if isinstance(per_xcc, list) else None,
-        }
-
-    def _run(self) -> None:
-        import time
-
-        while not self._stop.is_set():
-            try:
-                self.samples.append(self._read())
-            except Exception:  # noqa: BLE001
-                return
-            time.sleep(self.period_s)
+        self.device = device
+        self.duration_us = int(duration_ms * 1000)
+        self.workgroups = workgroups
+        self._lib = load_probe_library()
+        self.records = torch.zeros(4 * workgroups, dtype=torch.int64, device=device)
+        self.stream = torch.cuda.Stream(device)  # default priority
+        self.wall_khz = 0
 
     def start(self) -> None:
-        import threading
+        self.wall_khz = self._lib.clock_probe(self.workgroups, self.duration_us, self.records.data_ptr(),
+                                              self.stream.cuda_stream)
 
-        if not self.available:
-            return
-        self.samples.clear()
-        self._stop.clear()
-        self._thread = threading.Thread(target=self._run, daemon=True)
-        self._thread.start()
+    def done(self) -> bool:
+        return self.stream.query()
 
-    def stop(self) -> None:
-        if self._thread is not None:
-            self._stop.set()
-            self._thread.join(timeout=2.0)
-            self._thread = None
-
-    def summary(self) -> dict | None:
-        """Median and range of the sampled clocks in MHz (None without samples)."""
+    def summary(self) -> dict:
+        """Per-wave engine clocks in MHz (one wave per XCC when workgroups = XCCs): median,
+        range, and the wall time the waves spanned."""
         import statistics
 
-        current = [s["current_gfxclk"] for s in self.samples if isinstance(s.get("current_gfxclk"), int)]
-        if not current:
-            return None
-        average = [s["average_gfxclk_frequency"] for s in self.samples
-                   if isinstance(s.get("average_gfxclk_frequency"), int)]
-        per_xcc = [c for s in self.samples if s.get("current_gfxclks") for c in s["current_gfxclks"]]
+        self.stream.synchronize()
+        r = self.records.cpu().tolist()
+        mhz, wall_ms = [], []
+        for g in range(self.workgroups):
+            wall0, clock0, wall1, clock1 = r[4 * g: 4 * g + 4]
+            if wall1 > wall0:
+                mhz.append((clock1 - clock0) / (wall1 - wall0) * self.wall_khz / 1000.0)
+                wall_ms.append((wall1 - wall0) / self.wall_khz)
+        if not mhz:
+            return {"engine_clock_mhz_median": None}
         return {
-            "samples": len(current),
-            "current_gfxclk_mhz_median": statistics.median(current),
-            "current_gfxclk_mhz_min_max": [min(current), max(current)],
-            "average_gfxclk_mhz_median": statistics.median(average) if average else None,
-            "per_xcc_gfxclk_mhz_median": statistics.median(per_xcc) if per_xcc else None,
+            "engine_clock_mhz_median": round(statistics.median(mhz), 1),
+            "engine_clock_mhz_min_max": [round(min(mhz), 1), round(max(mhz), 1)],
+            "probe_waves": len(mhz),
+            "probe_wall_ms": round(statistics.median(wall_ms), 1),
+            "wall_clock_khz": self.wall_khz,
         }
+
+

@@ -52,3 +52,35 @@ def test_issue_sharing_summary(gfx950_device) -> None:
     placement = result["mfma_placement"]
     assert all(0.0 < v < 2 * result["mfma_ticks"] for v in placement.values()), placement
     assert result["operand"]["add_literal_ticks"] > 0 and result["operand"]["add_sgpr_ticks"] > 0
+
+
+def test_clock_probe_reads_a_physical_engine_clock(gfx950_device) -> None:
+    """The clock probe's waves span at least the requested wall time, and the shader clock they read
+    lies between the idle floor and the 2.4 GHz maximum; beside a busy MFMA probe the clock is up."""
+    import time
+
+    import torch
+
+    from piper_kernels.measure import ClockProbe
+
+    log("[probe] clock probe, 30 ms, 8 waves, alone and beside the MFMA probe")
+    probe = ClockProbe(gfx950_device, duration_ms=30.0, workgroups=8)
+    probe.start()
+    alone = probe.summary()
+    log(f"   alone {alone}")
+    assert alone["probe_waves"] == 8 and alone["wall_clock_khz"] > 0
+    assert alone["probe_wall_ms"] >= 30.0
+    assert 20.0 < alone["engine_clock_mhz_min_max"][0] <= alone["engine_clock_mhz_min_max"][1] <= 2400.0 * 1.01
+    busy = ClockProbe(gfx950_device, duration_ms=30.0, workgroups=8)
+    lib = native.load_probe_library()
+    sink = torch.empty(1024 * native.MFMA_PROBE_THREADS, dtype=torch.int32, device=gfx950_device)
+    stream = torch.cuda.current_stream(gfx950_device)
+    lib.mfma_probe(native.MFMA_PROBE_I8, 1024, 4096, sink.data_ptr(), stream.cuda_stream)
+    busy.start()
+    guard = time.perf_counter()
+    while not busy.done() and time.perf_counter() - guard < 5.0:
+        lib.mfma_probe(native.MFMA_PROBE_I8, 1024, 4096, sink.data_ptr(), stream.cuda_stream)
+        stream.synchronize()
+    beside = busy.summary()
+    log(f"   beside MFMA work {beside}")
+    assert beside["probe_waves"] == 8 and 500.0 < beside["engine_clock_mhz_median"] <= 2400.0 * 1.01

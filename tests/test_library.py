@@ -411,7 +411,8 @@ def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
              '  printf("%d %d %d %d %d %d %d %d %d\\n", PIPER_PROBE_ABI_VERSION, PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8,'
              ' PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8, PIPER_MFMA_PROBE_P_CODES_U8_SCALED,'
              ' PIPER_MFMA_PROBE_THREADS,'
-             ' PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8));']
+             ' PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_I8), PIPER_MFMA_PROBE_OPS(PIPER_MFMA_PROBE_F8));',
+             '  printf("%d\\n", PIPER_CLOCK_PROBE_MAX_WORKGROUPS);']
     lines.append('  printf("' + " ".join(["%d"] * (len(roles) + 3)) + '\\n", '
                  + ", ".join(f"PIPER_ISSUE_{r}" for r in roles)
                  + ", PIPER_ISSUE_ROLES, PIPER_ISSUE_MAX_WAVES_PER_SIMD, PIPER_ISSUE_RECORDS_PER_WORKGROUP);")
@@ -428,6 +429,8 @@ def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
                           native.MFMA_PROBE_P_CODES_U8, native.MFMA_PROBE_P_CODES_FP8,
                           native.MFMA_PROBE_P_CODES_U8_SCALED, native.MFMA_PROBE_THREADS,
                           native.MFMA_PROBE_OPS[native.MFMA_PROBE_I8], native.MFMA_PROBE_OPS[native.MFMA_PROBE_F8]]
+    assert values[9] == native.CLOCK_PROBE_MAX_WORKGROUPS
+    values = values[:9] + values[10:]
     n = len(roles)
     assert values[9:9 + n] == list(range(len(native.ISSUE_ROLES)))
     assert [r.upper() for r in native.ISSUE_ROLES] == roles
