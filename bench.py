@@ -25,9 +25,9 @@ Beside the timing (all after the timed region):
   codes of the call sit at -127 or 127 (the reference harness's saturation fields,
   benchmarks/lib/quality.py:16-41);
 * ``cpu_baseline``: the CPU oracle (a numpy restatement of the reference's portable path) on
-  whole heads of the same workload, one head per host thread on all the host threads the run
-  may use, per thread-group Q/K scales (the reference's default) and, on one round of heads,
-  per block;
+  whole heads of the same workload (or row ranges of them, where there are fewer heads than
+  threads), one task per host thread on all the host threads the run may use, per thread-group
+  Q/K scales (the reference's default) and, on one round of tasks, per block;
 * ``mfma_peak_measured``: the sustained dense INT8 and FP8 MFMA rate of the same GPU (the
   measurement library's back-to-back MFMA probe, results checked), with the kernel's fraction
   of it in ``attention_kernel``;
@@ -154,23 +154,37 @@ def _cpu_worker_ready() -> int:
     return os.getpid()
 
 
-def _cpu_head(task: tuple[str, int, int, str]):
-    """The full reference computation of one (batch, head) slice on one thread: K/V means,
-    Q/K/V codes and the 64-key streaming loop over every query row.  Returns the slice, its
-    wall time (input generation excluded) and the FP32 output [S, D]."""
+def _cpu_head(task: tuple[str, int, int, str, int, int]):
+    """The full reference computation of query rows [r0, r1) of one (batch, head) slice on one
+    thread: K/V means, Q/K/V codes of the whole slice, and the 64-key streaming loop over those
+    rows.  Returns the task, its wall time (input generation excluded) and the FP32 output rows."""
     from threadpoolctl import threadpool_limits
 
     from oracle import piper_oracle as oracle
     from piper_kernels.workloads import WORKLOADS, make_inputs
 
-    name, b, h, granularity = task
+    name, b, h, granularity, r0, r1 = task
     w = WORKLOADS[name]
     q, k, v = make_inputs(w, heads=[h], batches=[b])
     with threadpool_limits(limits=1):
         start = time.perf_counter()
-        out = oracle.piper_attention_reference(q, k, v, w.head_dim**-0.5, w.is_causal, granularity)
+        prepared = oracle.prepare(q, k, v, w.is_causal, granularity)
+        if (r0, r1) != (0, w.query_length):
+            prepared = dict(prepared)
+            for key in ("query_code", "query_scale"):
+                prepared[key] = prepared[key][:, :, r0:r1]
+        out = oracle.attention_from_prepared(prepared, w.head_dim**-0.5, w.is_causal, query_offset=r0)
         seconds = time.perf_counter() - start
-    return b, h, granularity, seconds, out[0, 0]
+    return b, h, granularity, r0, r1, seconds, out[0, 0]
+
+
+def row_range_operations(workload, r0: int, r1: int) -> int:
+    """The reference's operation count (4 x pairs x D) for query rows [r0, r1) of one slice; causal
+    rows see keys 0..row."""
+    pairs = (r1 - r0) * workload.key_length
+    if workload.is_causal:
+        pairs = (r1 * (r1 + 1) - r0 * (r0 + 1)) // 2
+    return 4 * pairs * workload.head_dim
 
 
 def host_threads() -> int:
@@ -200,52 +214,60 @@ def start_cpu_pool(threads: int):
 
 
 def cpu_baseline(pool, threads: int, workload, seconds: float) -> tuple[dict, dict]:
-    """Time the CPU oracle on whole (batch, head) slices of the workload, ``threads`` slices at a
+    """Time the CPU oracle on whole (batch, head) slices of the workload, ``threads`` tasks at a
     time in the worker processes (one numpy thread each), until ~``seconds`` of wall time have
-    passed or every slice is done; then one round per block.  Returns the record and the
-    oracle's FP32 outputs by (batch, head)."""
+    passed or every slice is done; then one round per block.  A workload with fewer slices than
+    threads (r2: one head of 131072 rows) splits each slice's query rows into contiguous ranges,
+    one task each, so that every thread works and a round stays bounded.  Returns the record and
+    the oracle's FP32 outputs of the completed slices by (batch, head)."""
     import numpy as np
-
-    from piper_kernels.measure import attention_operations
 
     # heads interleaved from both halves (0, H/2, 1, H/2+1, ...) so that a bounded sample covers
     # both of c5's V families (constant along the sequence below H/2, random above)
     half = max(1, workload.heads // 2)
     head_order = sorted(range(workload.heads), key=lambda h: (h % half, h // half))
     slices = [(b, h) for b in range(workload.batch) for h in head_order]
+    parts = max(1, threads // len(slices)) if len(slices) < threads else 1
+    rows = workload.query_length
+    bounds = [(rows * i // parts, rows * (i + 1) // parts) for i in range(parts)]
+    tasks = [(b, h, r0, r1) for b, h in slices for r0, r1 in bounds if r1 > r0]
+    pieces: dict[tuple[int, int], dict[int, np.ndarray]] = {}
     outputs: dict[tuple[int, int], np.ndarray] = {}
     per_thread_wall = 0.0
+    per_thread_ops = 0
     done = 0
-    while done < len(slices) and (done == 0 or per_thread_wall < seconds):
-        batch = slices[done : done + threads]
+    while done < len(tasks) and (done == 0 or per_thread_wall < seconds):
+        batch = tasks[done : done + threads]
         start = time.perf_counter()
-        for b, h, _, _, out in pool.map(_cpu_head, [(workload.name, b, h, "per_thread") for b, h in batch]):
-            outputs[(b, h)] = out
+        for b, h, _, r0, r1, _, out in pool.map(_cpu_head, [(workload.name, b, h, "per_thread", r0, r1)
+                                                             for b, h, r0, r1 in batch]):
+            pieces.setdefault((b, h), {})[r0] = out
+            per_thread_ops += row_range_operations(workload, r0, r1)
+            if len(pieces[(b, h)]) == len(bounds):
+                outputs[(b, h)] = np.concatenate([pieces[(b, h)][r] for r, _ in bounds])
         per_thread_wall += time.perf_counter() - start
         done += len(batch)
-        log(f"[bench] cpu baseline: {done} slice(s) per_thread, {per_thread_wall:.1f} s")
-    batch = slices[: min(threads, len(slices))]
+        log(f"[bench] cpu baseline: {done} task(s) per_thread, {per_thread_wall:.1f} s")
+    batch = tasks[: min(threads, len(tasks))]
     start = time.perf_counter()
-    list(pool.map(_cpu_head, [(workload.name, b, h, "per_warp") for b, h in batch]))
+    list(pool.map(_cpu_head, [(workload.name, b, h, "per_warp", r0, r1) for b, h, r0, r1 in batch]))
     warp_wall = time.perf_counter() - start
-    log(f"[bench] cpu baseline: {len(batch)} slice(s) per_warp, {warp_wall:.1f} s")
-
-    def tops(count: int, wall: float) -> float:
-        ops = attention_operations(1, count, workload.query_length, workload.key_length, workload.head_dim,
-                                   workload.is_causal)
-        return ops / wall / 1e12
+    warp_ops = sum(row_range_operations(workload, r0, r1) for _, _, r0, r1 in batch)
+    log(f"[bench] cpu baseline: {len(batch)} task(s) per_warp, {warp_wall:.1f} s")
+    split = f"each slice's {rows} query rows in {parts} contiguous ranges, one task each, " if parts > 1 else ""
 
     record = {
-        "value": tops(done, per_thread_wall),
+        "value": per_thread_ops / per_thread_wall / 1e12,
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "per_warp_value": tops(len(batch), warp_wall),
+        "per_warp_value": warp_ops / warp_wall / 1e12,
         "sample": (
-            f"{workload.name}: {done} of {len(slices)} (batch, head) slices, each the full reference computation "
-            f"(K/V means, per_thread Q/K codes, V codes, 64-key streaming loop over all {workload.query_length} query "
-            f"rows), {threads} at a time in worker processes with one numpy thread each; {per_thread_wall:.1f} s wall; "
-            f"per_warp: {len(batch)} slices in {warp_wall:.1f} s; numpy {np.__version__}; "
+            f"{workload.name}: {done} of {len(tasks)} tasks over {len(slices)} (batch, head) slices ({split}"
+            f"each task the full reference computation: K/V means, per_thread Q/K codes and V codes of its slice, "
+            f"64-key streaming loop over its query rows), {threads} at a time in worker processes with one numpy "
+            f"thread each; {per_thread_wall:.1f} s wall; per_warp: {len(batch)} tasks in {warp_wall:.1f} s; "
+            f"numpy {np.__version__}; "
             f"host threads used {threads} of os.cpu_count={os.cpu_count()}"
         ),
     }
@@ -484,6 +506,9 @@ def main() -> int:
             events[2].record()
         return out
 
+    # the timed region's events exist before the warm-up ends, so that no host work (slower under
+    # a profiler) leaves the GPU idle, and its clock falling, between warm-up and timing
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     with torch.no_grad():
         # warm-up: at least --warmup steps and at least --warmup-ms of GPU time (the clock ramps)
         warm_steps = 0
@@ -499,7 +524,6 @@ def main() -> int:
             if warm_steps >= args.warmup and warm_begin.elapsed_time(warm_end) >= args.warmup_ms:
                 break
         log(f"[bench] warmup {warm_steps} steps, {warm_begin.elapsed_time(warm_end):.0f} ms")
-        events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
         log(f"[bench] timing {args.steps} steps")
         torch.cuda.synchronize()
         start = time.perf_counter()
