@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define PIPER_ABI_VERSION 4
+#define PIPER_ABI_VERSION 5
 
 /* Rows per quantisation group (sage/reference.py:6-7) and keys per P block (reference.py:16). */
 #define PIPER_QUERY_BLOCK 32
@@ -207,7 +207,14 @@ typedef struct piper_prepare_args {
  * pass, so split plans agree with the others to rounding, not bit for bit. */
 #define PIPER_PLAN_KEY_PARTS(parts) (((parts) - 1) << 5)
 #define PIPER_PLAN_KEY_PARTS_OF(plan) ((((plan) >> 5) & 7) + 1)
-#define PIPER_PLAN_MASK 255
+/* Work queues (Piper Attention, with PIPER_PLAN_THREE_WORKGROUPS, no key-range split): a
+ * persistent grid of at most three workgroups per CU takes the query tiles, in the order the
+ * other bits give, from one queue per XCC (relaxed atomic counters in the call's workspace,
+ * piper_attention_workspace_bytes) instead of one workgroup per tile dispatched by the hardware,
+ * whose in-order round-robin over the XCCs leaves slots idle when tiles differ in length (causal).
+ * Bit-identical to the other plans. */
+#define PIPER_PLAN_WORK_QUEUE 256
+#define PIPER_PLAN_MASK 511
 
 /* piper_attention_args.flags / piper_attention_fused_args.flags */
 #define PIPER_ATTENTION_QK_PER_THREAD 1 /* Q/K scales per thread group: read slot (row % 8) of the
@@ -360,8 +367,9 @@ int piper_prepare_static(const piper_prepare_args* args, void* stream);
 /* Fused INT8-QK / UINT8-P x INT8-V online-softmax attention on `stream`. */
 int piper_attention_forward(const piper_attention_args* args, void* stream);
 
-/* Workspace bytes the attention entry points need for `plan` (0 unless the plan splits the key
- * range: parts * B * H * Sq * (D + 2) * 4). */
+/* Workspace bytes the attention entry points need for `plan`: parts * B * H * Sq * (D + 2) * 4 for
+ * a key-range split, 256 for the work-queue plan (its counters; the library zeroes them on the
+ * stream before each call), 0 otherwise. */
 int piper_attention_workspace_bytes(const piper_shape* shape, int32_t plan, int64_t* bytes);
 
 /* The same with the query quantised inside the kernel (see piper_attention_fused_args). */

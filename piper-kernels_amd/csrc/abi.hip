@@ -2,6 +2,7 @@
 //
 // Validation, launch geometry and error reporting only: the library never allocates,
 // frees or synchronises; every buffer belongs to the caller.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -147,15 +148,21 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   if (plan < 0 || plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", plan);
   if ((flags & ~PIPER_ATTENTION_QK_PER_THREAD) != 0) return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", flags);
   const int key_parts = PIPER_PLAN_KEY_PARTS_OF(plan);
+  const bool work_queue = (plan & PIPER_PLAN_WORK_QUEUE) != 0;
   if (key_parts > 1) {
     if (is_causal) return fail(PIPER_ERROR_UNSUPPORTED, "the key-range split plans are non-causal");
     if (!(plan & PIPER_PLAN_THREE_WORKGROUPS))
       return fail(PIPER_ERROR_UNSUPPORTED, "the key-range split needs PIPER_PLAN_THREE_WORKGROUPS");
+    if (work_queue) return fail(PIPER_ERROR_UNSUPPORTED, "the work-queue plan has no key-range split");
+  }
+  if (work_queue && !(plan & PIPER_PLAN_THREE_WORKGROUPS))
+    return fail(PIPER_ERROR_UNSUPPORTED, "the work-queue plan needs PIPER_PLAN_THREE_WORKGROUPS");
+  if (key_parts > 1 || work_queue) {
     int64_t need = 0;
     if (int st = piper_attention_workspace_bytes(&s, plan, &need)) return st;
     if (workspace == nullptr || workspace_bytes < need)
-      return fail(PIPER_ERROR_INVALID_ARGUMENT, "the key-range split needs a workspace of %lld bytes, got %lld",
-                  (long long)need, (long long)workspace_bytes);
+      return fail(PIPER_ERROR_INVALID_ARGUMENT, "the %s needs a workspace of %lld bytes, got %lld",
+                  work_queue ? "work-queue plan" : "key-range split", (long long)need, (long long)workspace_bytes);
     if (!aligned16(workspace)) return fail(PIPER_ERROR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   }
   if (query != nullptr) {
@@ -191,6 +198,7 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   ap.nkb = ap.sk64 / PIPER_KEY_BLOCK;
   ap.query_tiles = static_cast<int>(ceil_div(s.query_length, block_m));
   ap.scale_log2e = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  ap.score_multiplier = ap.scale_log2e * 67108864.0f;  // x 2^26: exact
   ap.causal_forward = (plan & PIPER_PLAN_CAUSAL_FORWARD) ? 1 : 0;
   ap.xcd_remap = (plan & PIPER_PLAN_NO_XCD_REMAP) ? 0 : 1;
   ap.causal_interleave = (plan & PIPER_PLAN_CAUSAL_INTERLEAVE) ? 1 : 0;
@@ -210,6 +218,16 @@ int launch_attention_call(int32_t abi_version, int32_t output_dtype, int32_t is_
   }
   if (static_cast<int64_t>(ap.query_tiles) * ap.batch_heads * ap.key_parts > 0x7fffffff)
     return fail(PIPER_ERROR_UNSUPPORTED, "too many workgroups");
+  if (work_queue) {
+    // one queue per XCC of the device (one queue if the runtime reports no XCC count), a
+    // persistent grid of three workgroups per CU, or fewer when there are fewer tiles
+    int cus = 0, xccs = 0;
+    if (int st = device_topology(&cus, &xccs)) return st;
+    const long tiles = static_cast<long>(ap.query_tiles) * ap.batch_heads;
+    ap.queue_xccs = std::max(1, std::min(xccs, piper::kQueueCounters));
+    ap.queue_workers = static_cast<int>(std::max(1L, std::min(tiles, 3L * std::max(cus, 1))));
+    ap.queue = static_cast<uint32_t*>(workspace);
+  }
 
   const hipError_t err = piper::launch_attention(static_cast<int>(s.head_dim), is_causal != 0, output_dtype, waves,
                                                  ap, static_cast<hipStream_t>(stream));
@@ -387,8 +405,10 @@ int piper_attention_workspace_bytes(const piper_shape* shape, int32_t plan, int6
   if (int st = check_shape(shape)) return st;
   if (bytes == nullptr) return fail(PIPER_ERROR_INVALID_ARGUMENT, "bytes is NULL");
   if (plan < 0 || plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", plan);
-  *bytes = piper::attention_partial_bytes(shape->batch * shape->heads, shape->query_length,
-                                          static_cast<int>(shape->head_dim), PIPER_PLAN_KEY_PARTS_OF(plan));
+  *bytes = (plan & PIPER_PLAN_WORK_QUEUE)
+               ? piper::kQueueBytes
+               : piper::attention_partial_bytes(shape->batch * shape->heads, shape->query_length,
+                                                static_cast<int>(shape->head_dim), PIPER_PLAN_KEY_PARTS_OF(plan));
   g_last_error[0] = '\0';
   return PIPER_OK;
 }
@@ -498,6 +518,7 @@ int piper_sage_attention_forward(const piper_sage_attention_args* a, void* strea
   if (a->plan < 0 || a->plan > PIPER_PLAN_MASK) return fail(PIPER_ERROR_UNSUPPORTED, "unknown plan %d", a->plan);
   if (PIPER_PLAN_KEY_PARTS_OF(a->plan) > 1)
     return fail(PIPER_ERROR_UNSUPPORTED, "SageAttention2++ has no key-range split plans");
+  if (a->plan & PIPER_PLAN_WORK_QUEUE) return fail(PIPER_ERROR_UNSUPPORTED, "SageAttention2++ has no work-queue plan");
   if ((a->flags & ~(PIPER_ATTENTION_QK_PER_THREAD | PIPER_SAGE_FP16_PARTIALS)) != 0)
     return fail(PIPER_ERROR_UNSUPPORTED, "unknown flags %d", a->flags);
   if (int st = check_input("query", a->query)) return st;

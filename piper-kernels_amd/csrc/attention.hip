@@ -391,34 +391,19 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) attention_kernel(const AttnPa
 // tile and writes its numerator, denominator and reference maximum for attention_merge_kernel.
 constexpr int kPartials = 3;
 
-template <int D, bool kCausal, int kOut, bool kPerThread>
-__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3, 3)))
-attention_w3_kernel(const AttnParams p) {
+// One query tile (and, for the key-range split, one key part) of attention_w3_kernel or of the
+// work-queue kernel below: the whole prologue, key loop and epilogue of one workgroup.  The caller
+// provides the LDS stages and the lane id; every wave of the workgroup calls it with the same tile.
+template <int D, bool kCausal, int kOut, bool kPerThread, bool kFreshLane = false>
+__device__ __forceinline__ void w3_tile(const AttnParams& p, char* smem, TileCoord tc, int part, int lane) {
   constexpr int NW = 4;
   using L = TileLayout<D, NW>;
   constexpr int kChunksD = D / 32;
-  constexpr int kStages = 2;
   static_assert(kOut != kPartials || !kCausal, "the key-range split is non-causal");
-  __shared__ __attribute__((aligned(16))) char smem[kStages * L::kStageBytes];
 
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5;
   const int n = lane & 31;
-  int part = 0;
-  TileCoord tc;
-  if constexpr (kOut == kPartials) {
-    // logical id -> (batch-head, key part, query tile): the workgroups of one key range of a
-    // head are neighbours, so an XCD's workgroups stream the same tiles through its L2
-    const int logical = p.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
-    const int per_head = p.key_parts * p.query_tiles;
-    tc.bh = logical / per_head;
-    const int rem = logical - tc.bh * per_head;
-    part = rem / p.query_tiles;
-    tc.qtile = rem - part * p.query_tiles;
-  } else {
-    tc = workgroup_tile<kCausal>(p);
-  }
   const int bh = __builtin_amdgcn_readfirstlane(tc.bh);
   const int qtile = __builtin_amdgcn_readfirstlane(tc.qtile);
   part = __builtin_amdgcn_readfirstlane(part);
@@ -449,7 +434,7 @@ attention_w3_kernel(const AttnParams p) {
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) qf[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
     cq = p.query_scale[(static_cast<long>(bh) * p.nqb + (q0 >> 5)) * kQueryScaleSlots + (kPerThread ? (n & 7) : 0)] *
-         (p.scale_log2e * kScoreUnit);
+         p.score_multiplier;
 #pragma unroll
     for (int c = 0; c < kChunksD; ++c) asm volatile("" ::"v"(qf[c]));
     asm volatile("" ::"v"(cq));
@@ -469,7 +454,7 @@ attention_w3_kernel(const AttnParams p) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kRounds - 1) : "memory");
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(raw[i]));
-    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * (p.scale_log2e * kScoreUnit);
+    cq = quantize_query_block<D, kPerThread>(p, q0, n, raw, qf) * p.score_multiplier;
   }
 
   float num[kChunksD][16];
@@ -512,7 +497,13 @@ attention_w3_kernel(const AttnParams p) {
 
   // the row's denominator: the four partial sums of both lane halves
   const float den_total = cross_half_sum((den[0] + den[1]) + (den[2] + den[3]));
-  const int query = q0 + n;
+  // kFreshLane (the work-queue kernel): the lane's row and half read again rather than kept
+  // through the key loop
+  int epilogue_lane = lane;
+  if constexpr (kFreshLane) asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(epilogue_lane));
+  const int eh = epilogue_lane >> 5;
+  const int en = epilogue_lane & 31;
+  const int query = q0 + en;
   if (!wave_live || query >= p.query_length) return;
   if constexpr (kOut == kPartials) {
     const long rows = static_cast<long>(p.batch_heads) * p.query_length;
@@ -522,10 +513,10 @@ attention_w3_kernel(const AttnParams p) {
     for (int j = 0; j < kChunksD; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<float4*>(dst + 32 * j + 8 * g + 4 * h) =
+        *reinterpret_cast<float4*>(dst + 32 * j + 8 * g + 4 * eh) =
             make_float4(num[j][4 * g + 0], num[j][4 * g + 1], num[j][4 * g + 2], num[j][4 * g + 3]);
     // both lane halves hold the row's den_total and mref
-    if (h == 0) reinterpret_cast<float2*>(p.partials + p.key_parts * rows * D)[row] = make_float2(den_total, mref);
+    if (eh == 0) reinterpret_cast<float2*>(p.partials + p.key_parts * rows * D)[row] = make_float2(den_total, mref);
     return;
   } else {
     const float rden = (1.0f / 255.0f) / fmaxf(den_total, 1e-30f);  // the numerator holds 255 x the reference's
@@ -535,7 +526,7 @@ attention_w3_kernel(const AttnParams p) {
     for (int j = 0; j < kChunksD; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * j + 8 * g + 4 * h;
+        const int d0 = 32 * j + 8 * g + 4 * eh;
         float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (!kCausal) m = *reinterpret_cast<const float4*>(vmean + d0);
         store4<kOut>(p.output, out_row + d0, fmaf(num[j][4 * g + 0], rden, m.x), fmaf(num[j][4 * g + 1], rden, m.y),
@@ -543,6 +534,117 @@ attention_w3_kernel(const AttnParams p) {
       }
     }
   }
+}
+
+template <int D, bool kCausal, int kOut, bool kPerThread>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3, 3)))
+attention_w3_kernel(const AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * TileLayout<D, 4>::kStageBytes];
+  int part = 0;
+  TileCoord tc;
+  if constexpr (kOut == kPartials) {
+    // logical id -> (batch-head, key part, query tile): the workgroups of one key range of a
+    // head are neighbours, so an XCD's workgroups stream the same tiles through its L2
+    const int logical = p.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
+    const int per_head = p.key_parts * p.query_tiles;
+    tc.bh = logical / per_head;
+    const int rem = logical - tc.bh * per_head;
+    part = rem / p.query_tiles;
+    tc.qtile = rem - part * p.query_tiles;
+  } else {
+    tc = workgroup_tile<kCausal>(p);
+  }
+  w3_tile<D, kCausal, kOut, kPerThread>(p, smem, tc, part, threadIdx.x & 63);
+}
+
+// The work-queue plan: a persistent grid (at most three workgroups per CU) whose workgroups take
+// query tiles from one queue per XCC instead of waiting for the hardware to dispatch them.  The
+// hardware deals workgroups round-robin over the XCCs in id order, so a workgroup that cannot be
+// placed on a full XCC holds back the next ones for every XCC: with causal tiles of unequal
+// length, slots stayed empty 7-28 us after a short tile ended.  Here queue q holds the logical ids
+// that XCC q runs under the XCD-aware order (the same tiles in the same longest-first order);
+// workgroup b takes its tiles from queue b % queue_xccs with one relaxed atomic each, and once that
+// queue is empty from the others in turn.  The tiles are computed exactly as by
+// attention_w3_kernel, so the output is bit-identical.  Every claim increments a counter, so each
+// workgroup ends after at most (tiles + queues) claims; no workgroup waits for another.
+template <int D, bool kCausal, int kOut, bool kPerThread>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(3, 3)))
+attention_w3_queue_kernel(const AttnParams p) {
+  static_assert(kOut != kPartials, "the work-queue plan has no key-range split");
+  __shared__ __attribute__((aligned(16))) char smem[2 * TileLayout<D, 4>::kStageBytes];
+  // The claim state lives in LDS (state[0]: the tile claimed, state[1]: the queue being taken
+  // from).  Nothing of the claim may stay in registers across the tiles: at 168 VGPRs the key loop
+  // has none to spare, so the lane id and a zero are read afresh in each iteration with inline
+  // assembly the compiler cannot hoist, the LDS addresses are formed from them, and the divisors
+  // are laundered the same way (hoisted, their reciprocals would hold registers too).
+  __shared__ int state[4];
+  for (bool first = true;; first = false) {
+    int lane, zero;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    int queues = p.queue_xccs, qt = p.query_tiles, heads = p.batch_heads;
+    asm volatile("" : "+s"(queues), "+s"(qt), "+s"(heads));
+    const int total = qt * heads;
+    const int base = total / queues, rem = total - base * queues;
+    volatile int* st = state + zero;
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == 0) {
+      // wave 0 claims: lane 0 takes the next tile of queue q; when q is empty, every lane reads
+      // one queue's counter and the wave moves to the first queue with tiles left, or stops when
+      // it has seen every queue empty.  Each attempt increments a counter, and a counter stops
+      // being tried once it has passed its queue's length, so the loop ends.
+      int q = __builtin_amdgcn_readfirstlane(first ? static_cast<int>(blockIdx.x) % queues : st[1]);
+      int logical = -1;
+      // the first tile needs no atomic: the workers of queue q start with its first tiles in
+      // order (queue_init_kernel starts each counter past them), so the grid does not open with
+      // every workgroup's atomic on the same few counters
+      const int rank = static_cast<int>(blockIdx.x) / queues;
+      if (first && rank < base + (q < rem ? 1 : 0)) logical = q * base + min(q, rem) + rank;
+      while (logical < 0) {
+        int i = 0;
+        if (lane == 0)
+          i = static_cast<int>(__hip_atomic_fetch_add(p.queue + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        i = __builtin_amdgcn_readfirstlane(i);
+        if (i < base + (q < rem ? 1 : 0)) {
+          logical = q * base + min(q, rem) + i;
+          break;
+        }
+        const int other = q + lane < queues ? q + lane : q + lane - queues;
+        bool left = false;
+        if (lane < queues)
+          left = static_cast<int>(__hip_atomic_load(p.queue + other, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) <
+                 base + (other < rem ? 1 : 0);
+        const uint64_t with_tiles = __builtin_amdgcn_ballot_w64(left);
+        if (with_tiles == 0) break;
+        const int step = __builtin_ctzll(with_tiles);
+        q = q + step < queues ? q + step : q + step - queues;
+      }
+      if (lane == 0) {
+        st[0] = logical;
+        st[1] = q;
+      }
+    }
+    // the claim is visible to every wave, and every wave is done with the previous tile's stages
+    __syncthreads();
+    const int logical = __builtin_amdgcn_readfirstlane(st[0]);
+    __syncthreads();  // every wave has read the claim before thread 0 overwrites it
+    if (logical < 0) return;
+    // the key-tile and query counts laundered too: conditions derived from them were hoisted as
+    // per-lane flags
+    AttnParams pl = p;
+    asm volatile("" : "+s"(pl.nkb), "+s"(pl.query_length));
+    w3_tile<D, kCausal, kOut, kPerThread, true>(pl, smem, queue_tile<kCausal>(pl, logical, queues, qt, heads), 0, lane);
+  }
+}
+
+// Sets the work-queue counters before the persistent grid (a fill kernel rather than
+// hipMemsetAsync, so that a captured graph replays it correctly): queue q starts past the tiles
+// its workers take first without an atomic, min(its tiles, its workers).
+__global__ void __launch_bounds__(64) queue_init_kernel(uint32_t* counters, int queues, int total, int workers) {
+  const int q = static_cast<int>(threadIdx.x);
+  if (q >= queues) return;
+  const int tiles = total / queues + (q < total % queues ? 1 : 0);
+  const int starters = workers / queues + (q < workers % queues ? 1 : 0);
+  counters[q] = static_cast<uint32_t>(min(tiles, starters));
 }
 
 // The key-range split's merge, one thread per four features of a query row: the parts' reference
@@ -582,6 +684,19 @@ __global__ void __launch_bounds__(256) attention_merge_kernel(const AttnParams p
 template <int D, bool kCausal, bool kPerThread>
 static hipError_t launch_w3(int out_dtype, const AttnParams& ap, hipStream_t stream) {
   const dim3 block(256);
+  if (ap.queue_xccs > 0) {
+    hipLaunchKernelGGL(queue_init_kernel, dim3(1), dim3(64), 0, stream, ap.queue, ap.queue_xccs,
+                       ap.query_tiles * ap.batch_heads, ap.queue_workers);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const dim3 grid(static_cast<unsigned>(ap.queue_workers));
+    switch (out_dtype) {
+      case 0: hipLaunchKernelGGL((attention_w3_queue_kernel<D, kCausal, 0, kPerThread>), grid, block, 0, stream, ap); break;
+      case 1: hipLaunchKernelGGL((attention_w3_queue_kernel<D, kCausal, 1, kPerThread>), grid, block, 0, stream, ap); break;
+      default: hipLaunchKernelGGL((attention_w3_queue_kernel<D, kCausal, 2, kPerThread>), grid, block, 0, stream, ap); break;
+    }
+    return hipGetLastError();
+  }
   if constexpr (!kCausal) {
     if (ap.key_parts > 1) {
       const dim3 grid(static_cast<unsigned>(ap.query_tiles * ap.batch_heads * ap.key_parts));

@@ -39,15 +39,19 @@ __device__ __forceinline__ void widen8(const uint4 raw, float (&out)[8]) {
   }
 }
 
-// Round-to-nearest-even narrowing of float to the 16-bit output formats.
-__device__ __forceinline__ uint32_t float_to_half_bits(float x) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(x)));
+// Round-to-nearest-even narrowing of two floats to a packed pair of the 16-bit output formats
+// (a in the low half): one gfx950 v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 per pair.  Finite values
+// round exactly as torch's casts do; a NaN becomes a NaN of the format.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){a, b}, half2_t));
 }
 
-__device__ __forceinline__ uint32_t float_to_bf16_bits(float x) {
-  const uint32_t bits = __float_as_uint(x);
-  if ((bits & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN
-  return (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){a, b}, bf16x2_t));
 }
 
 // Max / sum of a value over the two 32-lane halves of a wave (lane l and l ^ 32).

@@ -155,12 +155,23 @@ struct AttnParams {
   int key_parts;
   int part_tiles;
   float* partials;
+  // Work-queue plan (three workgroups per CU, no key-range split): a persistent grid takes query
+  // tiles from queue_xccs queues of consecutive logical ids, counters in `queue` (zero before the
+  // launch).  queue_xccs = 0: the hardware dispatches one workgroup per query tile.
+  int queue_xccs;
+  int queue_workers;  // the persistent grid (at most three workgroups per CU)
+  float score_multiplier;  // scale_log2e * 2^26 (kScoreUnit), exact: the logits' multiplier per query scale
+  uint32_t* queue;
 };
 
 // The workspace bytes of a key-range split (0 without one).
 inline long attention_partial_bytes(long batch_heads, long query_length, int head_dim, int key_parts) {
   return key_parts > 1 ? static_cast<long>(key_parts) * batch_heads * query_length * (head_dim + 2) * 4 : 0;
 }
+
+// The work-queue plan's counters: one per XCC, at most kQueueCounters.
+constexpr int kQueueCounters = 64;
+constexpr long kQueueBytes = kQueueCounters * 4;
 
 // SageAttention2++: the prep quantises K (per 64-row block, after K smoothing) and V (FP8
 // per channel) into tile records; the attention kernel quantises each query block itself.

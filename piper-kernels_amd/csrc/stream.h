@@ -84,6 +84,25 @@ __device__ __forceinline__ TileCoord workgroup_tile(const Params& p) {
   return {bh, kCausal && !p.causal_forward ? qt - 1 - qtile : qtile};
 }
 
+// Logical id -> (batch-head, query tile) of the work-queue plan, whose `queues` queues hold
+// consecutive logical ranges (queue q: what XCC q runs under the XCD-aware order); qt and
+// batch_heads are p.query_tiles and p.batch_heads, passed in by the caller.  The same order
+// as workgroup_tile with the XCD remap: with causal_interleave and batch-heads divisible by the
+// queues, each queue walks its own batch-heads' query tiles longest first across them.
+template <bool kCausal, class Params>
+__device__ __forceinline__ TileCoord queue_tile(const Params& p, int logical, int queues, int qt, int batch_heads) {
+  if (kCausal && !p.causal_forward && p.causal_interleave && batch_heads % queues == 0) {
+    const int heads = batch_heads / queues;
+    const int group = logical / (heads * qt);
+    const int r = logical - group * heads * qt;
+    const int rank = r / heads;
+    return {group * heads + (r - rank * heads), qt - 1 - rank};
+  }
+  const int bh = logical / qt;
+  const int qtile = logical - bh * qt;
+  return {bh, kCausal && !p.causal_forward ? qt - 1 - qtile : qtile};
+}
+
 // One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from src + off (src
 // wave-uniform, held in SGPRs; off the lane's 32-bit offset) to LDS byte lds + 16 * i.  The
 // scalar-base form keeps the per-piece address arithmetic on the scalar unit.  Issued as inline
@@ -174,12 +193,10 @@ __device__ __forceinline__ void store4(void* out, long index, float a, float b, 
   if constexpr (kOut == 2) {
     *reinterpret_cast<float4*>(static_cast<float*>(out) + index) = make_float4(a, b, c, d);
   } else if constexpr (kOut == 1) {
-    const uint2 v = make_uint2(float_to_bf16_bits(a) | (float_to_bf16_bits(b) << 16),
-                               float_to_bf16_bits(c) | (float_to_bf16_bits(d) << 16));
+    const uint2 v = make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + index) = v;
   } else {
-    const uint2 v = make_uint2(float_to_half_bits(a) | (float_to_half_bits(b) << 16),
-                               float_to_half_bits(c) | (float_to_half_bits(d) << 16));
+    const uint2 v = make_uint2(pack_half2(a, b), pack_half2(c, d));
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + index) = v;
   }
 }
@@ -257,9 +274,16 @@ __device__ __forceinline__ float quantize_query_block(const Params& p, int q0, i
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[i][e]));
   if constexpr (kPerThread) {
-    amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    // max over lanes l ^ 8, l ^ 16, l ^ 32 (the lanes whose low three bits agree) without lane
+    // addresses: a row rotation by 8 (within 16 lanes, that is l ^ 8), then the gfx950 row-pair
+    // and half swaps
+    amax = fmaxf(amax, dpp<0x128>(amax));  // row_ror:8
+    const uint32_t u16 = __float_as_uint(amax);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(u16, u16, false, false);
+    amax = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const uint32_t u32 = __float_as_uint(amax);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(u32, u32, false, false);
+    amax = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
   } else {
     amax = wave_max(amax);
   }

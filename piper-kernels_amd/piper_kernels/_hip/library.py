@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first; see module docstrin
 
 from .build import LIBRARY_PATH, PROBE_LIBRARY_PATH
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 QUERY_BLOCK = 32
 KEY_BLOCK = 64
 QUERY_SCALE_SLOTS = 8  # per 32-row Q block: one per thread group (per-block prep repeats its scale)

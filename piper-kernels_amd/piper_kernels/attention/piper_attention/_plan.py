@@ -33,7 +33,8 @@ PLAN_NO_XCD_REMAP = 4
 PLAN_CAUSAL_INTERLEAVE = 8
 PLAN_THREE_WORKGROUPS = 16
 PLAN_KEY_PARTS_SHIFT = 5  # bits 5-7: key parts - 1 (PIPER_PLAN_KEY_PARTS)
-PLAN_MASK = 255
+PLAN_WORK_QUEUE = 256
+PLAN_MASK = 511
 MAX_KEY_PARTS = 8
 WAVE_SLOTS = 3 * 4 * COMPUTE_UNITS  # three waves on each of the 1024 SIMDs
 
@@ -54,6 +55,8 @@ class MI355XPlan:
     two.  ``key_parts`` (three per CU, non-causal): the key tiles of each query tile are cut into
     that many ranges, one workgroup each, whose FP32 partial sums a merge kernel combines; for
     grids with too few query waves to give every SIMD three (results equal to rounding).
+    ``work_queue`` (three per CU, no split): a persistent grid takes the query tiles from one
+    queue per XCC instead of the hardware dispatching one workgroup per tile (bit-identical).
     """
 
     waves: int = 8
@@ -62,6 +65,7 @@ class MI355XPlan:
     causal_interleave: bool = False
     three_per_cu: bool = False
     key_parts: int = 1
+    work_queue: bool = False
 
     def __post_init__(self) -> None:
         if self.waves not in (4, 8):
@@ -72,6 +76,9 @@ class MI355XPlan:
             raise ValueError(f"key_parts must be 1..{MAX_KEY_PARTS}, got {self.key_parts}")
         if self.key_parts > 1 and not self.three_per_cu:
             raise ValueError("the key-range split runs three workgroups per CU")
+        if self.work_queue and (not self.three_per_cu or self.key_parts > 1 or not self.xcd_remap):
+            raise ValueError("the work-queue plan runs three workgroups per CU, one queue per XCC, without a "
+                             "key-range split")
 
     @property
     def block_m(self) -> int:
@@ -87,6 +94,7 @@ class MI355XPlan:
             | (PLAN_CAUSAL_INTERLEAVE if self.causal_interleave else 0)
             | (PLAN_THREE_WORKGROUPS if self.three_per_cu else 0)
             | ((self.key_parts - 1) << PLAN_KEY_PARTS_SHIFT)
+            | (PLAN_WORK_QUEUE if self.work_queue else 0)
         )
 
     @classmethod
@@ -100,22 +108,30 @@ class MI355XPlan:
             xcd_remap=not plan_id & PLAN_NO_XCD_REMAP,
             causal_interleave=bool(plan_id & PLAN_CAUSAL_INTERLEAVE),
             three_per_cu=three,
-            key_parts=(plan_id >> PLAN_KEY_PARTS_SHIFT) + 1,
+            key_parts=((plan_id >> PLAN_KEY_PARTS_SHIFT) & 7) + 1,
+            work_queue=bool(plan_id & PLAN_WORK_QUEUE),
         )
 
     @classmethod
     def all_plans(cls) -> list["MI355XPlan"]:
         """Every distinct plan without a key-range split, by plan id: the plans that compute
         bit-identical results (PIPER_PLAN_THREE_WORKGROUPS implies 4-wave workgroups, so ids that
-        also carry PIPER_PLAN_FOUR_WAVES name the same plans and are left out)."""
+        also carry PIPER_PLAN_FOUR_WAVES name the same plans and are left out), then the
+        work-queue plans."""
         return [cls.from_id(i) for i in range(PLAN_THREE_WORKGROUPS * 2)
-                if not (i & PLAN_THREE_WORKGROUPS and i & PLAN_FOUR_WAVES)]
+                if not (i & PLAN_THREE_WORKGROUPS and i & PLAN_FOUR_WAVES)] + cls.queue_plans()
 
     @classmethod
     def split_plans(cls) -> list["MI355XPlan"]:
         """The key-range split plans: three workgroups per CU, 2..8 key parts, either workgroup order."""
         return [cls(waves=4, three_per_cu=True, key_parts=k, xcd_remap=x)
                 for k in range(2, MAX_KEY_PARTS + 1) for x in (True, False)]
+
+    @classmethod
+    def queue_plans(cls) -> list["MI355XPlan"]:
+        """The work-queue plans: three workgroups per CU in each causal tile order."""
+        return [cls(waves=4, three_per_cu=True, work_queue=True, causal_longest_first=f, causal_interleave=i)
+                for f in (True, False) for i in ((False, True) if f else (False,))]
 
     def workgroups(self, batch: int, heads: int, query_length: int) -> int:
         return batch * heads * (-(-query_length // self.block_m)) * self.key_parts

@@ -224,9 +224,10 @@ def _launch_piper_attention(
         raise ValueError("output must be a contiguous [B, H, Sq, D] float16/bfloat16/float32 tensor")
     device = out.device
     flags = native.ATTENTION_QK_PER_THREAD if prepared.qk_granularity == "per_thread" else 0
-    # key-range split plans: FP32 partial sums of each key part, merged by the library's kernel
+    # key-range split plans: FP32 partial sums of each key part, merged by the library's kernel;
+    # the work-queue plan: its counters
     workspace = None
-    if prepared.plan.key_parts > 1:
+    if prepared.plan.key_parts > 1 or prepared.plan.work_queue:
         size = lib.attention_workspace_bytes(_native_shape(batch, heads, sq, sk, d), prepared.plan.plan_id)
         workspace = torch.empty(size, dtype=torch.uint8, device=device)
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel())

@@ -56,6 +56,10 @@ def candidate_plans(is_causal: bool, operator: str = "piper_attention"):
         MI355XPlan(waves=w, causal_longest_first=o, xcd_remap=x, causal_interleave=i, three_per_cu=t)
         for (w, t), (o, i), x in product(occupancy, orders, (True, False))
     ]
+    if operator == "piper_attention":
+        # work queues per XCC (bit-identical), in each causal order
+        plans += [MI355XPlan(waves=4, three_per_cu=True, work_queue=True, causal_longest_first=o, causal_interleave=i)
+                  for o, i in orders]
     if operator == "piper_attention" and not is_causal:
         plans += [MI355XPlan(waves=4, three_per_cu=True, key_parts=k, xcd_remap=x)
                   for k, x in product(SPLIT_PARTS, (True, False))]

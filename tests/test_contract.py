@@ -255,7 +255,7 @@ def test_plan_selection() -> None:
     assert MI355XPlan(8).plan_id == 0 and MI355XPlan(4).plan_id == 1
     assert MI355XPlan(8).as_dict() == {"waves": 8, "causal_longest_first": True, "xcd_remap": True,
                                         "causal_interleave": False, "three_per_cu": False, "key_parts": 1,
-                                        "block_m": 256, "block_n": 64}
+                                        "work_queue": False, "block_m": 256, "block_n": 64}
     assert MI355XPlan(4, three_per_cu=True).plan_id == 16 and MI355XPlan(4, three_per_cu=True).block_m == 128
     with pytest.raises(ValueError):
         MI355XPlan(waves=2)
@@ -270,7 +270,14 @@ def test_plan_selection() -> None:
             MI355XPlan(4, three_per_cu=True, key_parts=bad_parts)
     with pytest.raises(ValueError):
         MI355XPlan(8, key_parts=2)
-    for bad in (17, 32, -1, 256, 1 << 5):
+    # the work-queue plan: three per CU, XCD-aware, no split; bit 8
+    queue = MI355XPlan(4, three_per_cu=True, work_queue=True)
+    assert queue.plan_id == 16 | 256 and MI355XPlan.from_id(272) == queue
+    for bad_queue in (dict(waves=8), dict(waves=4), dict(waves=4, three_per_cu=True, key_parts=2),
+                      dict(waves=4, three_per_cu=True, xcd_remap=False)):
+        with pytest.raises(ValueError):
+            MI355XPlan(work_queue=True, **bad_queue)
+    for bad in (17, 32, -1, 256, 1 << 5, 16 | 32 | 256, 16 | 4 | 256, 512):
         with pytest.raises(ValueError):
             MI355XPlan.from_id(bad)
 
@@ -280,15 +287,17 @@ def test_plan_ids_round_trip_and_match_the_header() -> None:
 
     header = (REPO / "include" / "piper_mi355x.h").read_text()
     for name, value in (("FOUR_WAVES", 1), ("CAUSAL_FORWARD", 2), ("NO_XCD_REMAP", 4), ("CAUSAL_INTERLEAVE", 8),
-                        ("THREE_WORKGROUPS", 16), ("MASK", 255)):
+                        ("THREE_WORKGROUPS", 16), ("WORK_QUEUE", 256), ("MASK", 511)):
         assert f"#define PIPER_PLAN_{name} {value}" in header
     assert "#define PIPER_PLAN_KEY_PARTS(parts) (((parts) - 1) << 5)" in header
     assert "#define PIPER_PLAN_KEY_PARTS_OF(plan) ((((plan) >> 5) & 7) + 1)" in header
     assert (_plan.PLAN_FOUR_WAVES, _plan.PLAN_CAUSAL_FORWARD, _plan.PLAN_NO_XCD_REMAP) == (1, 2, 4)
-    assert (_plan.PLAN_CAUSAL_INTERLEAVE, _plan.PLAN_THREE_WORKGROUPS, _plan.PLAN_MASK) == (8, 16, 255)
+    assert (_plan.PLAN_CAUSAL_INTERLEAVE, _plan.PLAN_THREE_WORKGROUPS, _plan.PLAN_MASK) == (8, 16, 511)
+    assert _plan.PLAN_WORK_QUEUE == 256
     assert _plan.PLAN_KEY_PARTS_SHIFT == 5
     plans = MI355XPlan.all_plans()  # the bit-identical plans
-    assert len(set(plans)) == len(plans) == 24 and all(p.key_parts == 1 for p in plans)
+    assert len(set(plans)) == len(plans) == 27 and all(p.key_parts == 1 for p in plans)
+    assert sum(p.work_queue for p in plans) == 3
     split = MI355XPlan.split_plans()
     assert len(set(split)) == len(split) == 14 and all(p.three_per_cu and p.key_parts > 1 for p in split)
     for plan in plans + split:

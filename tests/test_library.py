@@ -160,8 +160,18 @@ def test_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 256
+    args.plan = 512
     with pytest.raises(RuntimeError, match="unknown plan"):
+        lib.attention_forward(args, 0)
+    # the work-queue plan: three workgroups per CU, no split, with a workspace for its counters
+    args.plan = 256
+    with pytest.raises(RuntimeError, match="work-queue plan needs PIPER_PLAN_THREE_WORKGROUPS"):
+        lib.attention_forward(args, 0)
+    args.plan = 16 | 32 | 256
+    with pytest.raises(RuntimeError, match="work-queue plan has no key-range split"):
+        lib.attention_forward(args, 0)
+    args.plan = 16 | 256
+    with pytest.raises(RuntimeError, match="work-queue plan needs a workspace of 256 bytes, got 0"):
         lib.attention_forward(args, 0)
     # the key-range split: three workgroups per CU, non-causal, with a workspace
     args.plan = 32
@@ -293,7 +303,7 @@ def test_fused_attention_validates_before_launching(lib) -> None:
     args.query = native.PiperTensor(fake, 512, 512, 64)
     with pytest.raises(RuntimeError, match="output pointer is NULL"):
         lib.attention_forward_fused(args, 0)
-    args.plan = 256
+    args.plan = 512
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.attention_forward_fused(args, 0)
     args.plan, args.flags = 0, 4
@@ -355,11 +365,14 @@ def test_sage_attention_validates_before_launching(lib) -> None:
     with pytest.raises(RuntimeError, match="scale must be finite and positive"):
         lib.sage_attention_forward(args, 0)
     args.scale = 0.125
-    args.plan = 256
+    args.plan = 512
     with pytest.raises(RuntimeError, match="unknown plan"):
         lib.sage_attention_forward(args, 0)
     args.plan = 16 | 32
     with pytest.raises(RuntimeError, match="no key-range split"):
+        lib.sage_attention_forward(args, 0)
+    args.plan = 16 | 256
+    with pytest.raises(RuntimeError, match="no work-queue plan"):
         lib.sage_attention_forward(args, 0)
     args.plan, args.flags = 0, 4
     with pytest.raises(RuntimeError, match="unknown flags"):
@@ -516,5 +529,7 @@ def test_attention_workspace_bytes(lib, shape) -> None:
     for parts in range(2, 9):
         plan = 16 | ((parts - 1) << 5)
         assert lib.attention_workspace_bytes(native.PiperShape(*shape), plan) == parts * b * h * sq * (d + 2) * 4
+    # the work-queue plan: its counters
+    assert lib.attention_workspace_bytes(native.PiperShape(*shape), 16 | 256) == 256
     with pytest.raises(RuntimeError, match="unknown plan"):
-        lib.attention_workspace_bytes(native.PiperShape(*shape), 256)
+        lib.attention_workspace_bytes(native.PiperShape(*shape), 512)
