@@ -146,7 +146,8 @@ def tune_shape(q, k, v, is_causal: bool, *, warmup_ms: float, rounds: int, launc
         "key": {"batch_heads": batch_heads, "query_length": ql, "key_length": kl, "head_dim": hd, "is_causal": causal},
         "plan": {"waves": best.waves, "causal_longest_first": best.causal_longest_first, "xcd_remap": best.xcd_remap,
                  "causal_interleave": best.causal_interleave, "three_per_cu": best.three_per_cu,
-                 **({"key_parts": best.key_parts} if best.key_parts > 1 else {})},
+                 **({"key_parts": best.key_parts} if best.key_parts > 1 else {}),
+                 **({"work_queue": True} if best.work_queue else {})},
         "candidates": [
             {"plan_id": p.plan_id, **p.as_dict(), "median_ms": round(medians[p], 5),
              ("within_split_tolerance" if p.key_parts > 1 else "bitwise_equal_to_default"): passed[p]}
