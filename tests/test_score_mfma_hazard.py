@@ -9,6 +9,11 @@ This test compiles both attention sources to gfx950 assembly, exactly as the bui
 checks every such MFMA in every instantiation: the first instruction after it that touches its
 destination registers must be an MFMA that reads them as its full accumulator operand, with no
 branch in between.
+
+The same assembly (and the prep's) also shows each kernel's register spills: the attention loops
+run at 168 VGPRs (three 4-wave workgroups per CU), where one value too many goes to scratch memory
+and costs a store and a reload with its wait; every product kernel must keep a private segment of
+zero bytes.
 """
 
 from __future__ import annotations
@@ -87,24 +92,55 @@ def test_checker_flags_a_copy_of_the_result() -> None:
     assert found == 1 and len(bad) == 1 and "v_accvgpr_write_b32" in bad[0]
 
 
-def test_every_inline_assembly_score_mfma_feeds_only_its_chain(tmp_path) -> None:
+@pytest.fixture(scope="module")
+def assembly(tmp_path_factory) -> dict[str, str]:
+    """gfx950 assembly of the attention and prep sources, compiled in parallel as the build does."""
     try:
         compiler = build.hipcc()
     except FileNotFoundError:
         pytest.skip("hipcc not found")
+    tmp = tmp_path_factory.mktemp("asm")
     flags = [f for f in build.COMPILE_FLAGS if f != "-fPIC"]
     procs = []
-    for source in SOURCES:
-        out = tmp_path / (Path(source).stem + ".s")
+    for source in (*SOURCES, "prep.hip"):
+        out = tmp / (Path(source).stem + ".s")
         cmd = [compiler, *flags, f"-I{build.INCLUDE}", f"-I{build.CSRC}", "--cuda-device-only", "-S",
                str(build.CSRC / source), "-o", str(out)]
         procs.append((source, out, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
-    total = 0
+    texts = {}
     for source, out, proc in procs:
         _, err = proc.communicate(timeout=900)
         assert proc.returncode == 0, f"{source}: {err[-2000:]}"
-        found, bad = unsafe_first_mfmas(out.read_text())
+        texts[source] = out.read_text()
+    return texts
+
+
+def test_every_inline_assembly_score_mfma_feeds_only_its_chain(assembly) -> None:
+    total = 0
+    for source in SOURCES:
+        found, bad = unsafe_first_mfmas(assembly[source])
         assert found > 0, f"{source}: no inline-assembly score MFMA found"
         assert not bad, f"{source}: {len(bad)} unsafe of {found}:\n" + "\n".join(bad[:10])
         total += found
     assert total > 0
+
+
+def kernel_spills(text: str) -> dict[str, tuple[int, int]]:
+    """kernel name -> (private segment bytes, spilled VGPRs), from the code-object metadata."""
+    meta = text[text.index("amdhsa.kernels:"):]
+    spills = {}
+    for m in re.finditer(r"\.name:\s+(\S+)\n(.*?)(?=\n  - |\Z)", meta, re.S):
+        body = m.group(2)
+        private = re.search(r"\.private_segment_fixed_size:\s+(\d+)", body)
+        vgprs = re.search(r"\.vgpr_spill_count:\s+(\d+)", body)
+        if private and vgprs:
+            spills[m.group(1)] = (int(private.group(1)), int(vgprs.group(1)))
+    return spills
+
+
+def test_no_product_kernel_spills_to_scratch(assembly) -> None:
+    for source, text in assembly.items():
+        spills = kernel_spills(text)
+        assert len(spills) > 10, f"{source}: kernel metadata not found"
+        bad = {name: v for name, v in spills.items() if v != (0, 0)}
+        assert not bad, f"{source}: {len(bad)} kernels use scratch (bytes, VGPRs): {sorted(bad.items())[:5]}"
