@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PIPER_PROBE_ABI_VERSION 2
+#define PIPER_PROBE_ABI_VERSION 3
 
 int piper_probe_abi_version(void);
 const char* piper_probe_last_error(void);
@@ -76,6 +76,13 @@ int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint3
  *               the attention loop's ratio with its MFMAs bunched as the score MFMAs are
  *   ADD_LIT     32 v_add_f32 per round with a 32-bit literal operand, 16 chains
  *   ADD_SGPR    32 v_add_f32 per round with an SGPR operand, 16 chains
+ *   FMA_SPLIT   32 v_fma_f32 per round into 8 registers, the three sources in VGPR banks 0, 1, 2
+ *               (bank = register number mod 4); fixed registers v64-v79, no dependences
+ *   FMA_SAME    FMA_SPLIT with its first two sources in the same bank
+ *   FMAC_SAME   32 v_fmac_f32 per round on 8 accumulators, each accumulator's bank that of the
+ *               first source
+ *   MAX3        32 v_max3_f32 per round, the sources in banks 0, 1, 2 (the attention loop's row max)
+ *   PERM        32 v_perm_b32 per round, the sources in banks 0, 1, 2 (its code packing)
  *
  * A wave's record: its hardware ids, role, slot, the ticks its loop took and the rounds it
  * completed (rounds / ticks is its rate while the other waves of its SIMD ran theirs).
@@ -93,7 +100,12 @@ int piper_mfma_probe(int32_t kind, int32_t workgroups, int32_t iterations, uint3
 #define PIPER_ISSUE_CLUSTER 10
 #define PIPER_ISSUE_ADD_LIT 11
 #define PIPER_ISSUE_ADD_SGPR 12
-#define PIPER_ISSUE_ROLES 13
+#define PIPER_ISSUE_FMA_SPLIT 13
+#define PIPER_ISSUE_FMA_SAME 14
+#define PIPER_ISSUE_FMAC_SAME 15
+#define PIPER_ISSUE_MAX3 16
+#define PIPER_ISSUE_PERM 17
+#define PIPER_ISSUE_ROLES 18
 #define PIPER_ISSUE_MAX_WAVES_PER_SIMD 4
 #define PIPER_ISSUE_RECORDS_PER_WORKGROUP 16
 

@@ -204,6 +204,22 @@ __device__ __forceinline__ void add16_literal(float (&f)[16]) { asm volatile(PIP
 
 __device__ __forceinline__ void add16_sgpr(float (&f)[16], float b) { asm volatile(PIPER_ADD16("%16") : PIPER_F16_OUTS : "s"(b)); }
 
+// 32 instructions of one form into v72-v79 (four passes), sources in v64-v68 (banks 0, 1, 2, 3, 0):
+// fixed registers, so that the banks of the operands are the form's and not the allocator's.  They
+// stay below v80: with the 32 AGPRs of the MFMA roles the kernel needs at most 128 registers per
+// lane, the most a 1024-thread workgroup (four waves per SIMD) can be given.
+#define PIPER_BANK8(FORM)                                                                                     \
+  FORM("v72", "v64") FORM("v73", "v65") FORM("v74", "v66") FORM("v75", "v67") FORM("v76", "v64")            \
+  FORM("v77", "v65") FORM("v78", "v66") FORM("v79", "v67")
+#define PIPER_BANK32(FORM) PIPER_BANK8(FORM) PIPER_BANK8(FORM) PIPER_BANK8(FORM) PIPER_BANK8(FORM)
+#define PIPER_FMA_SPLIT(D, S) "v_fma_f32 " D ", v64, v65, v66\n\t"
+#define PIPER_FMA_SAME(D, S) "v_fma_f32 " D ", v64, v68, v66\n\t"
+#define PIPER_FMAC_SAME(D, S) "v_fmac_f32 " D ", " S ", v69\n\t"  // S: the bank of D
+#define PIPER_MAX3(D, S) "v_max3_f32 " D ", v64, v65, v66\n\t"
+#define PIPER_PERM(D, S) "v_perm_b32 " D ", v64, v65, v66\n\t"
+#define PIPER_BANK_CLOBBERS                                                                                   \
+  "v64", "v65", "v66", "v67", "v68", "v69", "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79"
+
 template <int R>
 __device__ __forceinline__ uint32_t issue_loop(uint64_t t0, uint64_t budget, const char* lds, uint32_t& rounds,
                                                uint64_t& t1) {
@@ -286,6 +302,16 @@ __device__ __forceinline__ uint32_t issue_loop(uint64_t t0, uint64_t budget, con
       } else if constexpr (R == PIPER_ISSUE_ADD_SGPR) {
         add16_sgpr(f, negb);
         add16_sgpr(f, negb);
+      } else if constexpr (R == PIPER_ISSUE_FMA_SPLIT) {
+        asm volatile(PIPER_BANK32(PIPER_FMA_SPLIT)::: PIPER_BANK_CLOBBERS);
+      } else if constexpr (R == PIPER_ISSUE_FMA_SAME) {
+        asm volatile(PIPER_BANK32(PIPER_FMA_SAME)::: PIPER_BANK_CLOBBERS);
+      } else if constexpr (R == PIPER_ISSUE_FMAC_SAME) {
+        asm volatile(PIPER_BANK32(PIPER_FMAC_SAME)::: PIPER_BANK_CLOBBERS);
+      } else if constexpr (R == PIPER_ISSUE_MAX3) {
+        asm volatile(PIPER_BANK32(PIPER_MAX3)::: PIPER_BANK_CLOBBERS);
+      } else if constexpr (R == PIPER_ISSUE_PERM) {
+        asm volatile(PIPER_BANK32(PIPER_PERM)::: PIPER_BANK_CLOBBERS);
       }
     }
     rounds += kInner;
@@ -345,6 +371,11 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(256, 1024))) issue_pr
     case PIPER_ISSUE_CLUSTER: check = issue_loop<PIPER_ISSUE_CLUSTER>(t0, p.budget, lds, rounds, t1); break;
     case PIPER_ISSUE_ADD_LIT: check = issue_loop<PIPER_ISSUE_ADD_LIT>(t0, p.budget, lds, rounds, t1); break;
     case PIPER_ISSUE_ADD_SGPR: check = issue_loop<PIPER_ISSUE_ADD_SGPR>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_FMA_SPLIT: check = issue_loop<PIPER_ISSUE_FMA_SPLIT>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_FMA_SAME: check = issue_loop<PIPER_ISSUE_FMA_SAME>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_FMAC_SAME: check = issue_loop<PIPER_ISSUE_FMAC_SAME>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_MAX3: check = issue_loop<PIPER_ISSUE_MAX3>(t0, p.budget, lds, rounds, t1); break;
+    case PIPER_ISSUE_PERM: check = issue_loop<PIPER_ISSUE_PERM>(t0, p.budget, lds, rounds, t1); break;
     default: break;
   }
   if ((threadIdx.x & 63) == 0) {

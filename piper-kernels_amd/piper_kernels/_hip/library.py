@@ -361,7 +361,7 @@ def library_available() -> bool:
 # ---------------------------------------------------------------------------------------
 # libpiper_probe.so (include/piper_probe.h)
 # ---------------------------------------------------------------------------------------
-PROBE_ABI_VERSION = 2
+PROBE_ABI_VERSION = 3
 PROBE_EXPORTED_SYMBOLS = ("piper_probe_abi_version", "piper_probe_last_error", "piper_mfma_probe", "piper_issue_probe",
                           "piper_clock_probe")
 
@@ -375,7 +375,8 @@ MFMA_PROBE_THREADS = 512
 MFMA_PROBE_OPS = {MFMA_PROBE_I8: 65536, MFMA_PROBE_F8: 131072}
 
 # piper_issue_probe roles (PIPER_ISSUE_*)
-ISSUE_ROLES = ("idle", "mfma", "fma", "exp", "cvt", "mix", "valu_mix", "lds", "mfma_fma", "mix_vgpr", "cluster", "add_lit", "add_sgpr")
+ISSUE_ROLES = ("idle", "mfma", "fma", "exp", "cvt", "mix", "valu_mix", "lds", "mfma_fma", "mix_vgpr", "cluster", "add_lit", "add_sgpr",
+               "fma_split", "fma_same", "fmac_same", "max3", "perm")
 ISSUE_MAX_WAVES_PER_SIMD = 4
 ISSUE_RECORDS_PER_WORKGROUP = 16
 

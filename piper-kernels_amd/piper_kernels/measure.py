@@ -297,6 +297,11 @@ ISSUE_ROUND = {
     "cluster": {"mfma": 8, "valu": 176},
     "add_lit": {"valu": 32},
     "add_sgpr": {"valu": 32},
+    "fma_split": {"valu": 32},
+    "fma_same": {"valu": 32},
+    "fmac_same": {"valu": 32},
+    "max3": {"valu": 32},
+    "perm": {"valu": 32},
 }
 
 
@@ -381,7 +386,14 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
       instead of spread one per 22 VALU instructions;
     * ``operand``: v_add_f32 ticks per instruction with a 32-bit literal and with an SGPR
       operand, three waves per SIMD (an FP32 VALU instruction reading an SGPR issues at half
-      the rate).
+      the rate);
+    * ``vgpr_banks``: v_fma_f32 with its sources in three different VGPR banks (register number
+      mod 4) and with its first two sources in one bank, and v_fmac_f32 with its accumulator in
+      the bank of its first source, three waves per SIMD (a bank conflict costs the FP32 pipe
+      extra cycles);
+    * ``valu_class``: v_max3_f32 and v_perm_b32 (the attention loop's row maximum and code
+      packing), sources in different banks, three waves per SIMD, beside ``vgpr_banks``'
+      conflict-free FMA.
     """
 
     def run(*roles: str) -> dict:
@@ -410,6 +422,7 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
     cluster3 = run("cluster", "cluster", "cluster")
     lit3 = run("add_lit", "add_lit", "add_lit")
     sgpr3 = run("add_sgpr", "add_sgpr", "add_sgpr")
+    banked = {role: per_instr(run(role, role, role), role, "valu") for role in ("fma_split", "fma_same", "fmac_same", "max3", "perm")}
     vmix_round = vmix3["valu_mix"]["ticks_per_round"]
     return {
         "ticks": "s_memtime",
@@ -448,6 +461,16 @@ def measure_issue_sharing(device: torch.device, *, cycle_budget: int = 400_000) 
         "operand": {
             "add_literal_ticks": per_instr(lit3, "add_lit", "valu"),
             "add_sgpr_ticks": per_instr(sgpr3, "add_sgpr", "valu"),
+        },
+        "vgpr_banks": {
+            "fma_distinct_banks_ticks": banked["fma_split"],
+            "fma_src0_src1_same_bank_ticks": banked["fma_same"],
+            "fmac_accumulator_src0_same_bank_ticks": banked["fmac_same"],
+        },
+        "valu_class": {
+            "fma_ticks": banked["fma_split"],
+            "max3_ticks": banked["max3"],
+            "perm_ticks": banked["perm"],
         },
     }
 

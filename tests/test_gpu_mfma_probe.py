@@ -52,6 +52,10 @@ def test_issue_sharing_summary(gfx950_device) -> None:
     placement = result["mfma_placement"]
     assert all(0.0 < v < 2 * result["mfma_ticks"] for v in placement.values()), placement
     assert result["operand"]["add_literal_ticks"] > 0 and result["operand"]["add_sgpr_ticks"] > 0
+    banks, classes = result["vgpr_banks"], result["valu_class"]
+    assert all(v > 0 for v in (*banks.values(), *classes.values())), (banks, classes)
+    # a bank conflict never makes an FMA faster
+    assert banks["fma_src0_src1_same_bank_ticks"] >= 0.95 * banks["fma_distinct_banks_ticks"], banks
 
 
 def test_clock_probe_reads_a_physical_engine_clock(gfx950_device) -> None:

@@ -419,7 +419,7 @@ def test_probe_library_exports_exactly_its_header(probe) -> None:
 def test_probe_constants_and_structs_match_the_header(tmp_path) -> None:
     source = tmp_path / "probe.c"
     roles = ["IDLE", "MFMA", "FMA", "EXP", "CVT", "MIX", "VALU_MIX", "LDS", "MFMA_FMA", "MIX_VGPR", "CLUSTER", "ADD_LIT",
-             "ADD_SGPR"]
+             "ADD_SGPR", "FMA_SPLIT", "FMA_SAME", "FMAC_SAME", "MAX3", "PERM"]
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "piper_probe.h"', "int main(void) {",
              '  printf("%d %d %d %d %d %d %d %d %d\\n", PIPER_PROBE_ABI_VERSION, PIPER_MFMA_PROBE_I8, PIPER_MFMA_PROBE_F8,'
              ' PIPER_MFMA_PROBE_P_CODES_U8, PIPER_MFMA_PROBE_P_CODES_FP8, PIPER_MFMA_PROBE_P_CODES_U8_SCALED,'

@@ -102,7 +102,7 @@ def assembly(tmp_path_factory) -> dict[str, str]:
     tmp = tmp_path_factory.mktemp("asm")
     flags = [f for f in build.COMPILE_FLAGS if f != "-fPIC"]
     procs = []
-    for source in (*SOURCES, "prep.hip"):
+    for source in (*SOURCES, "prep.hip", "probe.hip"):
         out = tmp / (Path(source).stem + ".s")
         cmd = [compiler, *flags, f"-I{build.INCLUDE}", f"-I{build.CSRC}", "--cuda-device-only", "-S",
                str(build.CSRC / source), "-o", str(out)]
@@ -138,8 +138,36 @@ def kernel_spills(text: str) -> dict[str, tuple[int, int]]:
     return spills
 
 
+def kernel_registers(text: str) -> dict[str, tuple[int, int]]:
+    """kernel name -> (VGPRs + AGPRs per lane, largest workgroup), from the code-object metadata."""
+    meta = text[text.index("amdhsa.kernels:"):]
+    found = {}
+    for entry in meta.split("\n  - ")[1:]:
+        name = re.search(r"\.name:\s+(\S+)", entry)
+        vgprs = re.search(r"\.vgpr_count:\s+(\d+)", entry)
+        group = re.search(r"\.max_flat_workgroup_size:\s+(\d+)", entry)
+        if name and vgprs and group:
+            found[name.group(1)] = (int(vgprs.group(1)), int(group.group(1)))
+    return found
+
+
+def test_every_kernel_fits_its_largest_workgroup(assembly) -> None:
+    """A SIMD holds 512 registers per lane; a workgroup of g threads puts ceil(g / 256) of its waves
+    on each SIMD, so its kernel may use at most 512 / that many (in granules of 8).  Registers an
+    inline-assembly block names explicitly are outside the compiler's budget, and a kernel over it
+    builds but cannot be dispatched."""
+    for source, text in assembly.items():
+        registers = kernel_registers(text)
+        assert registers, f"{source}: kernel metadata not found"
+        for name, (vgprs, group) in registers.items():
+            waves_per_simd = -(-group // 256)
+            assert -(-vgprs // 8) * 8 * waves_per_simd <= 512, f"{source}: {name} needs {vgprs} registers at {group} threads"
+
+
 def test_no_product_kernel_spills_to_scratch(assembly) -> None:
     for source, text in assembly.items():
+        if source == "probe.hip":  # the measurement library, not a product kernel
+            continue
         spills = kernel_spills(text)
         assert len(spills) > 10, f"{source}: kernel metadata not found"
         bad = {name: v for name, v in spills.items() if v != (0, 0)}
