@@ -451,7 +451,7 @@ def test_student_t_workload_has_constant_value_heads() -> None:
 
 
 def test_integration_ops_coexist_with_the_reference_registration() -> None:
-    """INTEGRATION.md's HIP module registers its own qualified op, so it coexists with the
+    """The integration guide's HIP module registers its own qualified op, so it coexists with the
     reference's Triton registration of piper_kernels::piper_attention (triton.py:984), which the
     reference imports on ROCm too (dispatch.py:10-15); a second registration of one name raises."""
     import re

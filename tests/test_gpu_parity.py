@@ -143,7 +143,7 @@ def test_per_thread_output_matches_golden_fixture(fixture, gfx950_device) -> Non
 
 
 MEAN_CASES = [
-    # (workload, batches, heads): head subsets of the BASELINE configurations at their full S
+    # (workload, batches, heads): head subsets of the c1-c5 benchmark workloads at their full S
     ("c2", None, [0, 7, 23]),
     ("c3", None, [0, 23]),
     ("c4", [0, 3], [0, 31]),

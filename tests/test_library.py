@@ -275,7 +275,7 @@ def test_prepare_static_validates_before_touching_the_gpu(lib) -> None:
     assert lib.prepared_layout(args.shape).workspace_bytes > native.STATIC_SCRATCH_BYTES
     with pytest.raises(RuntimeError, match="more than the static 16777216 bytes"):
         lib.prepare_static(args, 0)
-    # the largest BASELINE workload fits (c5: 80 batch-heads at Sk = 32768)
+    # the largest benchmark workload fits (c5: 80 batch-heads at Sk = 32768)
     assert lib.prepared_layout(native.PiperShape(2, 40, 32768, 32768, 128)).workspace_bytes <= native.STATIC_SCRATCH_BYTES
 
 
